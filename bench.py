@@ -1,0 +1,224 @@
+"""Recognition-head benchmark on one MI355X.
+
+A step is one pass of the head over one batch already resident in HBM: the dense batch
+of 256 text lines x T=120 (m = 30720 rows, k = 120, 18710 classes), INT8 weights, through
+the fused projection + online softmax + argmax (never writing logits) and the CTC
+collapse.  The metric is rows/s (rows = B*T).  The same JSON line carries the roofline of
+the dominant kernel, the unfused variant (logits written to HBM, softmax, argmax, CTC)
+and the CPU oracle (the C restatement of the reference's AVX2 INT8 path) timed on a
+bounded sample on this host.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "rust-ppocrv6_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="dense_256")
+    p.add_argument("--mode", type=int, default=2, help="0 fp32 FMA, 1/2/3 bf16 terms")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", default="", help="fused|unfused|probs (profiling runs)")
+    return p.parse_args()
+
+
+def timed(fn, stream, steps, warmup):
+    """Run fn() warmup times, then time `steps` calls with HIP events on `stream`."""
+    from ppocr_rechead.hip import Event, synchronize
+    for _ in range(warmup):
+        fn()
+    synchronize()
+    e0, e1 = Event(), Event()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    wall = time.perf_counter() - t0
+    synchronize()
+    return e0.elapsed_ms(e1) / steps, wall / steps * 1e3
+
+
+def traffic_from_profiles(kernel_key):
+    """HBM bytes per launch measured with rocprofv3 --pmc (committed under profiles/)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(wk, q, s, seconds):
+    """The oracle's line-parallel head (one line per worker, inner serial, as
+    src/pipeline.rs:417-433) on as many lines as fit in about `seconds` of CPU work."""
+    from oracle import oracle as orc
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    off = wk["line_off"]
+    a = wk["a"]
+    # calibrate on a few lines, then size the sample
+    probe_lines = min(threads, len(off) - 1)
+    t0 = time.perf_counter()
+    orc.rechead_lines(a[: off[probe_lines]], off[: probe_lines + 1], q, s, wk["bias"], exec_threads=threads)
+    per_line = (time.perf_counter() - t0) / probe_lines * threads
+    lines = int(max(probe_lines, min(len(off) - 1, seconds * threads / max(per_line, 1e-9))))
+    lines = max(threads, (lines // threads) * threads) if lines >= threads else lines
+    rows = int(off[lines])
+    t0 = time.perf_counter()
+    orc.rechead_lines(a[:rows], off[: lines + 1], q, s, wk["bias"], exec_threads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": rows / dt, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{lines} lines x T=120 ({rows} rows) of the same batch, INT8 AVX2 path restated in C, "
+                      f"one line per OpenMP thread, {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU: the head shards along rows with the "
+                                   "weights replicated, so more GPUs are not measured here"}))
+        sys.exit(2)
+
+    import ppocr_rechead as rh
+    from ppocr_rechead import workloads as wl
+    from ppocr_rechead.hip import DeviceArray, Stream, synchronize
+
+    L = rh._lib.lib()
+    wk = wl.make(args.workload) if args.workload != "stress_1024" else None
+    a = wk["a"]
+    m, k = a.shape
+    n = wl.N_CLASSES
+    lines = len(wk["line_off"]) - 1
+    qw = rh.QuantizedWeight.from_f32_transposed(wk["w_t"])  # GPU packer
+    head = rh.RecHead(qw=qw, bias=wk["bias"])
+    mode = args.mode
+
+    stream = Stream()
+    st = stream.h
+    da = DeviceArray.from_numpy(a)
+    doff = DeviceArray.from_numpy(wk["line_off"])
+    didx = DeviceArray((m,), np.int32)
+    dmp = DeviceArray((m,), np.float32)
+    dseq = DeviceArray((m,), np.int32)
+    dlen = DeviceArray((lines,), np.int64)
+    dscore = DeviceArray((lines,), np.float32)
+    ws_bytes = head.workspace_bytes(m, mode)
+    dws = DeviceArray((max(ws_bytes, 1),), np.uint8)
+    synchronize()
+
+    def fused_argmax():
+        rh._check(L.ppocr_rh_argmax_dev(head.handle, da.p, m, mode, didx.p, dmp.p, dws.p, ws_bytes, st))
+
+    def ctc():
+        rh._check(L.ppocr_ctc_greedy_dev(didx.p, dmp.p, doff.p, lines, 0, dseq.p, dlen.p, dscore.p, st))
+
+    def fused_step():
+        fused_argmax()
+        ctc()
+
+    out = {}
+    flops = 2.0 * m * n * k
+    if args.only in ("", "fused"):
+        ms_step, wall_ms = timed(fused_step, stream, args.steps, args.warmup)
+        ms_head, _ = timed(fused_argmax, stream, args.steps, args.warmup)
+        out["fused"] = (ms_step, wall_ms, ms_head)
+
+    unf = None
+    if args.only in ("", "unfused"):
+        dlog = DeviceArray((m, n), np.float32)
+
+        def unfused_step():
+            rh._check(L.ppocr_rh_logits_dev(head.handle, da.p, m, mode, dlog.p, dws.p, ws_bytes, st))
+            rh._check(L.ppocr_softmax_rows_dev(dlog.p, m, n, didx.p, dmp.p, st))
+            ctc()
+
+        def logits_only():
+            rh._check(L.ppocr_rh_logits_dev(head.handle, da.p, m, mode, dlog.p, dws.p, ws_bytes, st))
+
+        ms_u, _ = timed(unfused_step, stream, max(3, args.steps // 2), 2)
+        ms_l, _ = timed(logits_only, stream, max(3, args.steps // 2), 2)
+        logits_bytes = 4.0 * m * n + 4.0 * m * k + 1.0 * n * k + 8.0 * n
+        total_bytes = logits_bytes + 8.0 * m * n + 8.0 * m
+        unf = {"ms_per_step": round(ms_u, 4), "rows_per_s": round(m / (ms_u / 1e3), 1),
+               "algorithmic_GBps": round(total_bytes / (ms_u / 1e3) / 1e9, 1),
+               "logits_kernel_ms": round(ms_l, 4),
+               "logits_kernel_GBps": round(logits_bytes / (ms_l / 1e3) / 1e9, 1),
+               "logits_hbm_frac": round(logits_bytes / (ms_l / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+        dlog.free()
+
+    probs = None
+    if args.only in ("", "probs"):
+        dprobs = DeviceArray((m, n), np.float32)
+        pws = head.workspace_bytes(m, mode)
+
+        def probs_step():
+            rh._check(L.ppocr_rh_probs_dev(head.handle, da.p, m, mode, dprobs.p, dws.p, pws, st))
+
+        ms_p, _ = timed(probs_step, stream, max(3, args.steps // 2), 2)
+        pbytes = 4.0 * m * n
+        probs = {"ms_per_step": round(ms_p, 4), "rows_per_s": round(m / (ms_p / 1e3), 1),
+                 "probs_write_GBps": round(pbytes / (ms_p / 1e3) / 1e9, 1),
+                 "hbm_frac": round(pbytes / (ms_p / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+        dprobs.free()
+
+    cpu = None
+    if not args.no_cpu and args.only == "":
+        cpu = cpu_baseline(wk, qw.data, qw.scales, args.cpu_seconds)
+
+    if "fused" in out:
+        ms_step, wall_ms, ms_head = out["fused"]
+        achieved = flops / (ms_head / 1e3) / 1e12
+        peak = FP32_PEAK_TFLOPS if mode == 0 else BF16_PEAK_TFLOPS
+        line = {
+            "metric": "rec-head rows/s (B*T x 18710 INT8 proj+softmax+CTC)",
+            "value": round(m / (ms_step / 1e3), 1),
+            "unit": "rows/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_step, 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": {0: "f32", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3"}[mode] + " MFMA, f32 accumulate, int8 weights"
+            if mode else "f32 FMA, int8 weights",
+            "data": "synthetic (seeded N(0,1) activations, N(0,0.05^2) weights packed to INT8 on the GPU)",
+            "config": {"workload": f"{args.workload}: {lines} lines x T=120, m={m}, k={k}, n={n}, fused "
+                                   "projection+softmax-max+argmax+CTC", "mode": mode},
+            "roofline": {"bound": "mfma" if mode else "valu", "kernel": "stats_mfma_kernel + merge_stats_kernel",
+                         "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                         "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles("stats_mfma_dense_256"),
+                         "algorithmic_flops_per_launch": flops, "kernel_ms": round(ms_head, 5)},
+            "wall_ms_per_step": round(wall_ms, 5),
+            "unfused": unf,
+            "probs_fused": probs,
+            "cpu_baseline": cpu,
+        }
+    else:
+        line = {"metric": "profiling run", "unfused": unf, "probs_fused": probs}
+    print(json.dumps(line), flush=True)
+    head.close()
+
+
+if __name__ == "__main__":
+    main()

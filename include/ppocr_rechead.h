@@ -1,0 +1,161 @@
+/*
+ * ppocr_rechead.h — C ABI of the MI355X (gfx950) recognition-head library.
+ *
+ * This is the drop-in boundary for the recognition head of rust_ppocrv6: the INT8
+ * packer, the vocabulary projection MatMul.12 (x[.., T, 120] @ W^T[18710, 120] + b),
+ * the 18710-way Softmax.2 and the CTC greedy decode.  Each entry point names the
+ * reference function it replaces (file:line in the rust_ppocrv6 crate).
+ *
+ * Conventions
+ *  - Every function returning int returns PPOCR_OK (0) on success.  On failure it
+ *    returns a PPOCR_ERR_* code and ppocr_last_error() (thread-local) holds a message
+ *    "<op>: <msg>" in the form of OcrError::OperatorError { op, msg } (src/error.rs:4-27).
+ *    Nothing aborts or panics across this boundary.
+ *  - Host-pointer entry points copy inputs to the device, run, copy results back and
+ *    synchronise.  `_dev` entry points take device pointers and a HIP stream
+ *    (hipStream_t passed as void*, NULL = the null stream), enqueue only, and never
+ *    synchronise.
+ *  - Matrices are row-major and contiguous.  m is the number of activation rows (B*T),
+ *    k the inner dimension (120 for PP-OCRv6_small_rec), n the number of classes (18710).
+ *  - A head handle is immutable after creation and may be shared by threads; calls that
+ *    overlap on one handle are safe as long as each passes its own workspace (or uses the
+ *    host-pointer entry points).
+ */
+#ifndef PPOCR_RECHEAD_H
+#define PPOCR_RECHEAD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PPOCR_OK 0
+#define PPOCR_ERR_INVALID_ARG 1 /* shape / argument error (OperatorError) */
+#define PPOCR_ERR_DEVICE 2      /* HIP runtime error */
+#define PPOCR_ERR_NO_MEMORY 3   /* device allocation failed */
+
+/* How the projection's inner products are computed.  All modes accumulate in fp32 and
+ * apply the per-class scale and bias in fp32 in the epilogue. */
+typedef enum {
+    PPOCR_MODE_FP32_FMA = 0, /* fp32 vector FMA over dequantised weights */
+    PPOCR_MODE_BF16X1 = 1,   /* bf16 MFMA, activation rounded to 1 bf16 term */
+    PPOCR_MODE_BF16X2 = 2,   /* bf16 MFMA, activation split into 2 bf16 terms (default) */
+    PPOCR_MODE_BF16X3 = 3    /* bf16 MFMA, activation split into 3 bf16 terms; for an
+                                FP32 head, a_hi*w_hi + a_hi*w_lo + a_lo*w_hi */
+} ppocr_mode_t;
+
+typedef struct ppocr_rh ppocr_rh_t;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ppocr_last_error(void);
+
+/* ---------------------------------------------------------------- packer
+ * Replaces QuantizedWeight::from_f32_transposed (src/ops/matmul.rs:1173-1202): per row j
+ * of W^T[n][k], scale = max|w|/127 if max|w| > 1e-8 else 1.0, q = round_half_away(w *
+ * (1/scale)) clamped to [-127, 127] (NaN -> 0).  Bit-exact with the reference. */
+int ppocr_rh_pack_int8(const float* w_t, int64_t n, int64_t k, int8_t* q_out, float* scales_out);
+int ppocr_rh_pack_int8_dev(const float* d_w_t, int64_t n, int64_t k, int8_t* d_q_out,
+                           float* d_scales_out, void* stream);
+
+/* ---------------------------------------------------------------- head handle
+ * Replaces the resident head weight of Model: the INT8 entry built by
+ * Model::quantize_matmul_weights (src/engine/model.rs:628-638, QuantizedWeight
+ * src/ops/matmul.rs:1165-1171) or the FP32 transposed copy of the prepack
+ * (src/engine/model.rs:565-605), plus the bias folded into MatMul.12
+ * (src/engine/model.rs:141-166).  Weights are uploaded once and stay resident in HBM.
+ * bias may be NULL (no bias).  device is a HIP device ordinal. */
+int ppocr_rh_create(const int8_t* q, const float* scales, const float* bias, int64_t n,
+                    int64_t k, int device, ppocr_rh_t** out);
+int ppocr_rh_create_f32(const float* w_t, const float* bias, int64_t n, int64_t k, int device,
+                        ppocr_rh_t** out);
+void ppocr_rh_destroy(ppocr_rh_t* h);
+
+/* Bytes this weight contributes to Model::weight_footprint_bytes
+ * (src/engine/model.rs:651-667): n*k + 4*n for an INT8 head (2,320,040 for the
+ * 18710x120 head), 4*n*k for an FP32 transposed head.  The bias is not counted, as in
+ * the reference. */
+size_t ppocr_rh_footprint_bytes(const ppocr_rh_t* h);
+/* Bytes of device memory the handle holds (packed weights, scales, bias, MFMA tiles). */
+size_t ppocr_rh_device_bytes(const ppocr_rh_t* h);
+/* n, k and whether the head is INT8 (1) or FP32 (0). */
+int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized);
+
+/* Device workspace needed by the `_dev` entry points below for m rows (0 if none).  A
+ * NULL workspace makes the call allocate one on its stream (stream-ordered) and free it
+ * after use.  Calls that share one workspace must not overlap. */
+size_t ppocr_rh_workspace_bytes(const ppocr_rh_t* h, int64_t m, int mode);
+
+/* ---------------------------------------------------------------- MatMul.12
+ * Replaces matmul_quantized_b (src/ops/matmul.rs:1204-1336) for an INT8 head and
+ * matmul_transposed_b (src/ops/matmul.rs:514-897) for an FP32 head:
+ * out[r][j] = (sum_k a[r][k] * w[j][k]) * scale[j] + bias[j], a [m][k] -> out [m][n].
+ * In PPOCR_MODE_BF16X2 rows whose largest |a| times the head's largest |w| exceeds 16 are
+ * recomputed with three activation terms (a precision guard; the same applies to the
+ * probs/argmax entry points). */
+int ppocr_rh_logits(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* out);
+int ppocr_rh_logits_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, float* d_out,
+                        void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- Softmax.2
+ * Replaces softmax_inplace(x, -1) (src/ops/softmax.rs:199-285) on rows [rows][cols]:
+ * max, exp(x - max), sum, multiply by 1/sum (1 if the sum is 0).  The `_dev` variant can
+ * also emit the first-index argmax of each probability row and its value (the per-step
+ * find_argmax of CtcDecoder::decode_batch, src/postprocess/ctc.rs:151-154); d_idx and
+ * d_maxprob may be NULL. */
+int ppocr_softmax_rows(float* x, int64_t rows, int64_t cols);
+int ppocr_softmax_rows_dev(float* d_x, int64_t rows, int64_t cols, int32_t* d_idx,
+                           float* d_maxprob, void* stream);
+
+/* find_argmax (src/postprocess/ctc.rs:178-258) of every row of x [rows][cols]: the first
+ * index of the maximum (strict >, NaN never wins; (0, -inf) for an all-NaN row). */
+int ppocr_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx, float* val);
+int ppocr_argmax_rows_dev(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx,
+                          float* d_val, void* stream);
+
+/* ---------------------------------------------------------------- MatMul.12 + Softmax.2
+ * The graph segment MatMul.12 -> Softmax.2 -> output (src/engine/model.rs:1245-1302)
+ * as one call.  _probs writes the softmax probabilities [m][n] (the graph output
+ * fetch_name_0); the logits never round-trip through HBM.  _argmax writes only, per
+ * row, the first-index argmax of the probabilities and the maximum probability
+ * (= 1 / sum exp(l - max)), which is all CtcDecoder::decode_batch reads
+ * (src/postprocess/ctc.rs:151-163). */
+int ppocr_rh_probs(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* probs);
+int ppocr_rh_probs_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, float* d_probs,
+                       void* d_workspace, size_t workspace_bytes, void* stream);
+int ppocr_rh_argmax(const ppocr_rh_t* h, const float* a, int64_t m, int mode, int32_t* idx,
+                    float* maxprob);
+int ppocr_rh_argmax_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, int32_t* d_idx,
+                        float* d_maxprob, void* d_workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* ---------------------------------------------------------------- CTC greedy
+ * Replaces the collapse and score of CtcDecoder::decode_batch
+ * (src/postprocess/ctc.rs:144-172) for `lines` text lines whose per-step argmax and max
+ * probability are idx/maxprob [line_off[lines]] (line i = steps line_off[i] ..
+ * line_off[i+1]).  A step is emitted when idx != blank and idx != the previous step's
+ * idx (the previous index starts as blank, and is updated on blanks too).  Emitted
+ * indices of line i are written to seq[line_off[i] ...], their count to seq_len[i] and
+ * score[i] = (f32 sum of the emitted maxprob, in order) / count, 0 when none.  The
+ * reference's blank is 0. */
+int ppocr_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* line_off,
+                     int64_t lines, int32_t blank, int32_t* seq, int64_t* seq_len, float* score);
+int ppocr_ctc_greedy_dev(const int32_t* d_idx, const float* d_maxprob, const int64_t* d_line_off,
+                         int64_t lines, int32_t blank, int32_t* d_seq, int64_t* d_seq_len,
+                         float* d_score, void* stream);
+
+/* ---------------------------------------------------------------- whole head
+ * recognize() for a ragged batch of text lines (src/pipeline.rs:395-436, one
+ * Model::forward + CtcDecoder::decode per line): a [line_off[lines]][k] holds the lines'
+ * activations back to back.  Runs the fused projection/softmax/argmax and the CTC
+ * collapse; outputs as ppocr_rh_argmax and ppocr_ctc_greedy.  idx and maxprob may be
+ * NULL. */
+int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off, int64_t lines,
+                    int mode, int32_t* idx, float* maxprob, int32_t* seq, int64_t* seq_len,
+                    float* score);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PPOCR_RECHEAD_H */

@@ -1,0 +1,662 @@
+// The extern "C" boundary (include/ppocr_rechead.h): head handles, argument checks with
+// the reference's error messages, and the host/device entry points.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+
+namespace ppocr {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+int fail(int code, const std::string& msg) {
+    set_error(msg);
+    return code;
+}
+
+}  // namespace ppocr
+
+using namespace ppocr;
+
+struct ppocr_rh {
+    int device = 0;
+    int64_t n = 0, k = 0;
+    bool quantized = true;
+    TileGeom geom{};
+    bool mfma_ok = false;
+    // device memory
+    int8_t* d_q = nullptr;     // [n][k] packed INT8 weight (INT8 head)
+    float* d_w = nullptr;      // [n][k] fp32 W^T (FP32 head)
+    float* d_scale = nullptr;  // [n] per-class scale (1.0 for an FP32 head)
+    float* d_bias = nullptr;   // [n] bias (0 when absent)
+    uint8_t* d_rec = nullptr;  // tiles x rec_bytes MFMA tile records
+    size_t device_bytes = 0;
+    // Precision guard of the 2-term split: rows with max|a| above this are recomputed with
+    // three terms.  16 / (largest |dequantised weight|): a single product then carries at
+    // most 16 * 2^-17 of split residual.
+    float amax_limit = INFINITY;
+};
+
+namespace {
+
+struct DeviceGuard {
+    int prev = -1;
+    int err = 0;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev && hipSetDevice(dev) != hipSuccess) err = 1;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Device buffer owned for the duration of a host-pointer call.
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t bytes) {
+        if (bytes == 0) bytes = 1;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation of " + std::to_string(bytes) + " bytes failed");
+        }
+        return PPOCR_OK;
+    }
+    template <typename T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+uint16_t bf16_bits_rne(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float bf16_to_float(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Build the MFMA tile records on the host (see TileGeom in kernels.hpp).
+std::vector<uint8_t> build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
+                                   const float* scale, const float* bias) {
+    std::vector<uint8_t> rec((size_t)g.tiles * g.rec_bytes(), 0);
+    for (int t = 0; t < g.tiles; ++t) {
+        uint8_t* r = rec.data() + (size_t)t * g.rec_bytes();
+        uint16_t* frag = reinterpret_cast<uint16_t*>(r);
+        for (int i = 0; i < 32; ++i) {
+            const int64_t row = (int64_t)t * 32 + i;
+            if (row >= n) continue;
+            for (int64_t kk = 0; kk < k; ++kk) {
+                const int gg = (int)(kk / 8), e = (int)(kk % 8);
+                uint16_t hi, lo = 0;
+                if (q) {
+                    hi = bf16_bits_rne((float)q[row * k + kk]);  // exact
+                } else {
+                    const float v = w[row * k + kk];
+                    hi = bf16_bits_rne(v);
+                    lo = bf16_bits_rne(v - bf16_to_float(hi));
+                }
+                frag[((size_t)(0 * g.G + gg) * 32 + i) * 8 + e] = hi;
+                if (g.wplanes == 2) frag[((size_t)(1 * g.G + gg) * 32 + i) * 8 + e] = lo;
+            }
+        }
+        float* ep = reinterpret_cast<float*>(r + g.frag_bytes());
+        for (int i = 0; i < 32; ++i) {
+            const int64_t row = (int64_t)t * 32 + i;
+            if (row < n) {
+                const float sc = scale[row], bi = bias ? bias[row] : 0.0f;
+                ep[i] = sc * kLog2e;
+                ep[32 + i] = bi * kLog2e;
+                ep[64 + i] = sc;
+                ep[96 + i] = bi;
+            } else {
+                ep[i] = 0.0f;
+                ep[32 + i] = -INFINITY;
+                ep[64 + i] = 0.0f;
+                ep[96 + i] = 0.0f;
+            }
+        }
+    }
+    return rec;
+}
+
+void free_handle(ppocr_rh* h) {
+    if (!h) return;
+    DeviceGuard dg(h->device);
+    if (h->d_q) (void)hipFree(h->d_q);
+    if (h->d_w) (void)hipFree(h->d_w);
+    if (h->d_scale) (void)hipFree(h->d_scale);
+    if (h->d_bias) (void)hipFree(h->d_bias);
+    if (h->d_rec) (void)hipFree(h->d_rec);
+    delete h;
+}
+
+template <typename T>
+int upload(T** dst, const T* src, size_t count, size_t* total) {
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 1);
+    if (hipMalloc((void**)dst, bytes) != hipSuccess) {
+        *dst = nullptr;
+        (void)hipGetLastError();
+        return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation failed");
+    }
+    *total += bytes;
+    if (count) PPOCR_HIP(hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice));
+    return PPOCR_OK;
+}
+
+int create_common(const int8_t* q, const float* w_t, const float* scales, const float* bias, int64_t n, int64_t k,
+                  int device, ppocr_rh_t** out) {
+    const char* op = q ? "MatMulQuantizedB" : "MatMulTransposedB";
+    if (!out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": out handle pointer is null");
+    *out = nullptr;
+    if (n <= 0 || k <= 0) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": weight must have positive shape");
+    if (n > (1LL << 30) || k > (1LL << 20)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": weight too large");
+    if ((q && !scales) || (!q && !w_t)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null weight pointer");
+    int ndev = 0;
+    PPOCR_HIP(hipGetDeviceCount(&ndev));
+    if (device < 0 || device >= ndev)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: device " + std::to_string(device) + " out of range");
+    DeviceGuard dg(device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: hipSetDevice failed");
+
+    std::unique_ptr<ppocr_rh, void (*)(ppocr_rh*)> h(new (std::nothrow) ppocr_rh, free_handle);
+    if (!h) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
+    h->device = device;
+    h->n = n;
+    h->k = k;
+    h->quantized = q != nullptr;
+    h->geom.G = (int)((k + 7) / 8);
+    h->geom.wplanes = q ? 1 : 2;
+    h->geom.tiles = (int)((n + 31) / 32);
+    h->mfma_ok = mfma_supports_groups(h->geom.G);
+    if (q) {
+        float wmax = 0.0f;
+        for (int64_t j = 0; j < n; ++j) {
+            int qm = 0;
+            for (int64_t kk = 0; kk < k; ++kk) qm = std::max(qm, std::abs((int)q[j * k + kk]));
+            wmax = std::max(wmax, (float)qm * scales[j]);
+        }
+        h->amax_limit = wmax > 0.0f ? 16.0f / wmax : INFINITY;
+    }
+
+    std::vector<float> sc_host;
+    const float* sc = scales;
+    if (!q) {
+        sc_host.assign((size_t)n, 1.0f);
+        sc = sc_host.data();
+    }
+    std::vector<float> bias_host;
+    const float* bi = bias;
+    if (!bias) {
+        bias_host.assign((size_t)n, 0.0f);
+        bi = bias_host.data();
+    }
+    size_t total = 0;
+    if (q) {
+        if (int e = upload(&h->d_q, q, (size_t)(n * k), &total)) return e;
+    } else {
+        if (int e = upload(&h->d_w, w_t, (size_t)(n * k), &total)) return e;
+    }
+    if (int e = upload(&h->d_scale, sc, (size_t)n, &total)) return e;
+    if (int e = upload(&h->d_bias, bi, (size_t)n, &total)) return e;
+    if (h->mfma_ok) {
+        std::vector<uint8_t> rec = build_records(h->geom, n, k, q, w_t, sc, bias);
+        if (int e = upload(&h->d_rec, rec.data(), rec.size(), &total)) return e;
+    }
+    h->device_bytes = total;
+    *out = h.release();
+    return PPOCR_OK;
+}
+
+int check_head(const ppocr_rh* h, const char* op) {
+    if (!h) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null head handle");
+    return PPOCR_OK;
+}
+
+// Which MFMA configuration a mode maps to for this head (-1: fp32 FMA path).
+int mode_cfg(const ppocr_rh* h, int mode, int* cfg) {
+    switch (mode) {
+        case PPOCR_MODE_FP32_FMA: *cfg = -1; return PPOCR_OK;
+        case PPOCR_MODE_BF16X1: *cfg = h->quantized ? CFG_Q1 : CFG_F1; break;
+        case PPOCR_MODE_BF16X2:
+            if (!h->quantized)
+                return fail(PPOCR_ERR_INVALID_ARG,
+                            "MatMulTransposedB: an FP32 head supports modes FP32_FMA, BF16X1 and BF16X3");
+            *cfg = CFG_Q2;
+            break;
+        case PPOCR_MODE_BF16X3: *cfg = h->quantized ? CFG_Q3 : CFG_F3; break;
+        default: return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: unknown mode " + std::to_string(mode));
+    }
+    if (!h->mfma_ok)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: no MFMA kernel for k = " + std::to_string(h->k) +
+                                               " (supported: 73..80, 113..120); use PPOCR_MODE_FP32_FMA");
+    return PPOCR_OK;
+}
+
+int fma_nsplit(int64_t m, int64_t n) {
+    const int64_t mblocks = (m + kFmaRowsPerBlock - 1) / kFmaRowsPerBlock;
+    const int64_t ntiles = (n + 63) / 64;
+    int64_t ns = (1024 + mblocks - 1) / std::max<int64_t>(mblocks, 1);
+    ns = std::min<int64_t>(std::max<int64_t>(ns, 1), std::min<int64_t>(ntiles, 1024));
+    return (int)ns;
+}
+
+int nsplit_for(const ppocr_rh* h, int64_t m, int cfg) {
+    if (cfg < 0) return fma_nsplit(m, h->n);
+    return stats_nsplit(m, stats_rows_per_block_mfma(cfg));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct WsLayout {
+    size_t p_best, p_sum, p_idx, row_max, row_inv, guard_count, guard_rows, total;
+};
+WsLayout ws_layout(int64_t m, int nsplit) {
+    WsLayout L;
+    const size_t pm = align_up((size_t)nsplit * (size_t)m * 4);
+    const size_t rm = align_up((size_t)m * 4);
+    L.p_best = 0;
+    L.p_sum = pm;
+    L.p_idx = 2 * pm;
+    L.row_max = 3 * pm;
+    L.row_inv = L.row_max + rm;
+    L.guard_count = L.row_inv + rm;
+    L.guard_rows = L.guard_count + kAlign;
+    L.total = L.guard_rows + rm;
+    return L;
+}
+
+Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws) {
+    return Guard{h->amax_limit, reinterpret_cast<int*>(ws + L.guard_count), reinterpret_cast<int*>(ws + L.guard_rows)};
+}
+
+// Projection + softmax statistics + merge, on device pointers.
+int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* d_idx, float* d_maxprob,
+              float* d_row_max, float* d_row_inv, uint8_t* ws, hipStream_t st) {
+    const int nsplit = nsplit_for(h, m, cfg);
+    const WsLayout L = ws_layout(m, nsplit);
+    float* p_best = reinterpret_cast<float*>(ws + L.p_best);
+    float* p_sum = reinterpret_cast<float*>(ws + L.p_sum);
+    int* p_idx = reinterpret_cast<int*>(ws + L.p_idx);
+    int e;
+    if (cfg < 0) {
+        e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx,
+                             st);
+    } else {
+        const Guard g = make_guard(h, L, ws);
+        e = launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, st);
+    }
+    if (e) return e;
+    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, st);
+}
+
+// Workspace: caller's, or stream-ordered scratch freed on the same stream.
+struct Workspace {
+    uint8_t* p = nullptr;
+    bool owned = false;
+    hipStream_t st = nullptr;
+    ~Workspace() {
+        if (owned && p) (void)hipFreeAsync(p, st);
+    }
+    int get(void* user, size_t user_bytes, size_t need, hipStream_t s, const char* op) {
+        st = s;
+        if (user) {
+            if (user_bytes < need)
+                return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": workspace of " + std::to_string(user_bytes) +
+                                                       " bytes, need " + std::to_string(need));
+            p = static_cast<uint8_t*>(user);
+            return PPOCR_OK;
+        }
+        void* q = nullptr;
+        if (hipMallocAsync(&q, std::max<size_t>(need, 1), s) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(PPOCR_ERR_NO_MEMORY, std::string(op) + ": workspace allocation failed");
+        }
+        p = static_cast<uint8_t*>(q);
+        owned = true;
+        return PPOCR_OK;
+    }
+};
+
+int check_m(int64_t m, const char* op) {
+    if (m < 0) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": negative row count");
+    if (m > (1LL << 31)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": too many rows");
+    return PPOCR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ppocr_last_error(void) { return g_last_error.c_str(); }
+
+int ppocr_rh_pack_int8_dev(const float* d_w_t, int64_t n, int64_t k, int8_t* d_q_out, float* d_scales_out,
+                           void* stream) {
+    if (n < 0 || k < 0) return fail(PPOCR_ERR_INVALID_ARG, "QuantizedWeight: negative shape");
+    if (n > 0 && (!d_w_t || !d_q_out || !d_scales_out)) return fail(PPOCR_ERR_INVALID_ARG, "QuantizedWeight: null pointer");
+    return launch_pack_int8(d_w_t, n, k, d_q_out, d_scales_out, (hipStream_t)stream);
+}
+
+int ppocr_rh_pack_int8(const float* w_t, int64_t n, int64_t k, int8_t* q_out, float* scales_out) {
+    if (n < 0 || k < 0) return fail(PPOCR_ERR_INVALID_ARG, "QuantizedWeight: negative shape");
+    if (n == 0) return PPOCR_OK;
+    if (!w_t || !q_out || !scales_out) return fail(PPOCR_ERR_INVALID_ARG, "QuantizedWeight: null pointer");
+    DevBuf dw, dq, ds;
+    if (int e = dw.alloc((size_t)(n * k) * 4)) return e;
+    if (int e = dq.alloc((size_t)(n * k))) return e;
+    if (int e = ds.alloc((size_t)n * 4)) return e;
+    if (n * k) PPOCR_HIP(hipMemcpy(dw.p, w_t, (size_t)(n * k) * 4, hipMemcpyHostToDevice));
+    if (int e = launch_pack_int8(dw.as<float>(), n, k, dq.as<int8_t>(), ds.as<float>(), nullptr)) return e;
+    if (n * k) PPOCR_HIP(hipMemcpy(q_out, dq.p, (size_t)(n * k), hipMemcpyDeviceToHost));
+    PPOCR_HIP(hipMemcpy(scales_out, ds.p, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_rh_create(const int8_t* q, const float* scales, const float* bias, int64_t n, int64_t k, int device,
+                    ppocr_rh_t** out) {
+    if (!q) {
+        if (out) *out = nullptr;
+        return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: null weight pointer");
+    }
+    return create_common(q, nullptr, scales, bias, n, k, device, out);
+}
+
+int ppocr_rh_create_f32(const float* w_t, const float* bias, int64_t n, int64_t k, int device, ppocr_rh_t** out) {
+    if (!w_t) {
+        if (out) *out = nullptr;
+        return fail(PPOCR_ERR_INVALID_ARG, "MatMulTransposedB: null weight pointer");
+    }
+    return create_common(nullptr, w_t, nullptr, bias, n, k, device, out);
+}
+
+void ppocr_rh_destroy(ppocr_rh_t* h) { free_handle(h); }
+
+size_t ppocr_rh_footprint_bytes(const ppocr_rh_t* h) {
+    if (!h) return 0;
+    // src/engine/model.rs:657-666: INT8 data.len() + 4*scales.len(); FP32 numel*4.
+    return h->quantized ? (size_t)(h->n * h->k) + 4 * (size_t)h->n : 4 * (size_t)(h->n * h->k);
+}
+
+size_t ppocr_rh_device_bytes(const ppocr_rh_t* h) { return h ? h->device_bytes : 0; }
+
+int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (n) *n = h->n;
+    if (k) *k = h->k;
+    if (quantized) *quantized = h->quantized ? 1 : 0;
+    return PPOCR_OK;
+}
+
+size_t ppocr_rh_workspace_bytes(const ppocr_rh_t* h, int64_t m, int mode) {
+    if (!h || m <= 0) return 0;
+    int cfg;
+    if (mode_cfg(h, mode, &cfg)) return 0;
+    return ws_layout(m, nsplit_for(h, m, cfg)).total;
+}
+
+int ppocr_rh_logits_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, float* d_out, void* d_workspace,
+                        size_t workspace_bytes, void* stream) {
+    const char* op = (h && !h->quantized) ? "MatMulTransposedB" : "MatMulQuantizedB";
+    if (int e = check_head(h, op)) return e;
+    if (int e = check_m(m, op)) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m == 0) return PPOCR_OK;
+    if (!d_a || !d_out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null pointer");
+    DeviceGuard dg(h->device);
+    hipStream_t st = (hipStream_t)stream;
+    if (cfg < 0) return launch_logits_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, d_out, st);
+    const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, op)) return e;
+    const Guard g = make_guard(h, L, ws.p);
+    return launch_logits_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, d_out, &g, st);
+}
+
+int ppocr_rh_logits(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* out) {
+    const char* op = (h && !h->quantized) ? "MatMulTransposedB" : "MatMulQuantizedB";
+    if (int e = check_head(h, op)) return e;
+    if (int e = check_m(m, op)) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m == 0) return PPOCR_OK;
+    if (!a || !out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null pointer");
+    DeviceGuard dg(h->device);
+    DevBuf da, dout;
+    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
+    if (int e = dout.alloc((size_t)(m * h->n) * 4)) return e;
+    PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
+    if (int e = ppocr_rh_logits_dev(h, da.as<float>(), m, mode, dout.as<float>(), nullptr, 0, nullptr)) return e;
+    PPOCR_HIP(hipMemcpy(out, dout.p, (size_t)(m * h->n) * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_softmax_rows_dev(float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, float* d_maxprob, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: negative shape");
+    if (rows == 0 || cols == 0) return PPOCR_OK;
+    if (!d_x) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: null pointer");
+    return launch_softmax_rows(d_x, rows, cols, d_idx, d_maxprob, (hipStream_t)stream);
+}
+
+int ppocr_softmax_rows(float* x, int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: negative shape");
+    if (rows == 0 || cols == 0) return PPOCR_OK;  // empty input: nothing to do (src/ops/softmax.rs:226-229)
+    if (!x) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: null pointer");
+    DevBuf dx;
+    if (int e = dx.alloc((size_t)(rows * cols) * 4)) return e;
+    PPOCR_HIP(hipMemcpy(dx.p, x, (size_t)(rows * cols) * 4, hipMemcpyHostToDevice));
+    if (int e = launch_softmax_rows(dx.as<float>(), rows, cols, nullptr, nullptr, nullptr)) return e;
+    PPOCR_HIP(hipMemcpy(x, dx.p, (size_t)(rows * cols) * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_argmax_rows_dev(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, float* d_val, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative shape");
+    if (rows == 0) return PPOCR_OK;
+    if ((!d_x && cols) || !d_idx || !d_val) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    return launch_argmax_rows(d_x, rows, cols, d_idx, d_val, (hipStream_t)stream);
+}
+
+int ppocr_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx, float* val) {
+    if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative shape");
+    if (rows == 0) return PPOCR_OK;
+    if ((!x && cols) || !idx || !val) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    DevBuf dx, di, dv;
+    if (int e = dx.alloc((size_t)(rows * cols) * 4)) return e;
+    if (int e = di.alloc((size_t)rows * 4)) return e;
+    if (int e = dv.alloc((size_t)rows * 4)) return e;
+    if (rows * cols) PPOCR_HIP(hipMemcpy(dx.p, x, (size_t)(rows * cols) * 4, hipMemcpyHostToDevice));
+    if (int e = launch_argmax_rows(dx.as<float>(), rows, cols, di.as<int32_t>(), dv.as<float>(), nullptr)) return e;
+    PPOCR_HIP(hipMemcpy(idx, di.p, (size_t)rows * 4, hipMemcpyDeviceToHost));
+    PPOCR_HIP(hipMemcpy(val, dv.p, (size_t)rows * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_rh_argmax_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, int32_t* d_idx, float* d_maxprob,
+                        void* d_workspace, size_t workspace_bytes, void* stream) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m == 0) return PPOCR_OK;
+    if (!d_a || !d_idx || !d_maxprob) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    hipStream_t st = (hipStream_t)stream;
+    const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;
+    return run_stats(h, cfg, d_a, m, d_idx, d_maxprob, nullptr, nullptr, ws.p, st);
+}
+
+int ppocr_rh_argmax(const ppocr_rh_t* h, const float* a, int64_t m, int mode, int32_t* idx, float* maxprob) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m == 0) return PPOCR_OK;
+    if (!a || !idx || !maxprob) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    DevBuf da, di, dp, dws;
+    const size_t wsb = ws_layout(m, nsplit_for(h, m, cfg)).total;
+    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
+    if (int e = di.alloc((size_t)m * 4)) return e;
+    if (int e = dp.alloc((size_t)m * 4)) return e;
+    if (int e = dws.alloc(wsb)) return e;
+    PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
+    if (int e = ppocr_rh_argmax_dev(h, da.as<float>(), m, mode, di.as<int32_t>(), dp.as<float>(), dws.p, wsb, nullptr))
+        return e;
+    PPOCR_HIP(hipMemcpy(idx, di.p, (size_t)m * 4, hipMemcpyDeviceToHost));
+    PPOCR_HIP(hipMemcpy(maxprob, dp.p, (size_t)m * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_rh_probs_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, float* d_probs, void* d_workspace,
+                       size_t workspace_bytes, void* stream) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m == 0) return PPOCR_OK;
+    if (!d_a || !d_probs) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    hipStream_t st = (hipStream_t)stream;
+    const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;
+    float* rmax = reinterpret_cast<float*>(ws.p + L.row_max);
+    float* rinv = reinterpret_cast<float*>(ws.p + L.row_inv);
+    if (int e = run_stats(h, cfg, d_a, m, nullptr, nullptr, rmax, rinv, ws.p, st)) return e;
+    if (cfg < 0)
+        return launch_probs_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, rmax, rinv, d_probs, st);
+    const Guard g = make_guard(h, L, ws.p);
+    return launch_probs_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, rmax, rinv, d_probs, &g, st);
+}
+
+int ppocr_rh_probs(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* probs) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m == 0) return PPOCR_OK;
+    if (!a || !probs) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    DevBuf da, dp, dws;
+    const size_t wsb = ws_layout(m, nsplit_for(h, m, cfg)).total;
+    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
+    if (int e = dp.alloc((size_t)(m * h->n) * 4)) return e;
+    if (int e = dws.alloc(wsb)) return e;
+    PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
+    if (int e = ppocr_rh_probs_dev(h, da.as<float>(), m, mode, dp.as<float>(), dws.p, wsb, nullptr)) return e;
+    PPOCR_HIP(hipMemcpy(probs, dp.p, (size_t)(m * h->n) * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_ctc_greedy_dev(const int32_t* d_idx, const float* d_maxprob, const int64_t* d_line_off, int64_t lines,
+                         int32_t blank, int32_t* d_seq, int64_t* d_seq_len, float* d_score, void* stream) {
+    if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
+    if (lines == 0) return PPOCR_OK;
+    if (!d_line_off || !d_seq_len || !d_score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    return launch_ctc_greedy(d_idx, d_maxprob, d_line_off, lines, blank, d_seq, d_seq_len, d_score,
+                             (hipStream_t)stream);
+}
+
+static int check_offsets(const int64_t* line_off, int64_t lines) {
+    if (line_off[0] != 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: line offsets must start at 0");
+    for (int64_t i = 0; i < lines; ++i)
+        if (line_off[i + 1] < line_off[i])
+            return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: line offsets must be non-decreasing");
+    return PPOCR_OK;
+}
+
+int ppocr_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* line_off, int64_t lines, int32_t blank,
+                     int32_t* seq, int64_t* seq_len, float* score) {
+    if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
+    if (lines == 0) return PPOCR_OK;
+    if (!line_off || !seq_len || !score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    if (int e = check_offsets(line_off, lines)) return e;
+    const int64_t steps = line_off[lines];
+    if (steps > 0 && (!idx || !maxprob || !seq)) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    DevBuf di, dv, doff, dseq, dlen, dsc;
+    if (int e = di.alloc((size_t)steps * 4)) return e;
+    if (int e = dv.alloc((size_t)steps * 4)) return e;
+    if (int e = doff.alloc((size_t)(lines + 1) * 8)) return e;
+    if (int e = dseq.alloc((size_t)steps * 4)) return e;
+    if (int e = dlen.alloc((size_t)lines * 8)) return e;
+    if (int e = dsc.alloc((size_t)lines * 4)) return e;
+    if (steps) {
+        PPOCR_HIP(hipMemcpy(di.p, idx, (size_t)steps * 4, hipMemcpyHostToDevice));
+        PPOCR_HIP(hipMemcpy(dv.p, maxprob, (size_t)steps * 4, hipMemcpyHostToDevice));
+    }
+    PPOCR_HIP(hipMemcpy(doff.p, line_off, (size_t)(lines + 1) * 8, hipMemcpyHostToDevice));
+    if (int e = launch_ctc_greedy(di.as<int32_t>(), dv.as<float>(), doff.as<int64_t>(), lines, blank,
+                                  dseq.as<int32_t>(), dlen.as<int64_t>(), dsc.as<float>(), nullptr))
+        return e;
+    PPOCR_HIP(hipMemcpy(seq_len, dlen.p, (size_t)lines * 8, hipMemcpyDeviceToHost));
+    PPOCR_HIP(hipMemcpy(score, dsc.p, (size_t)lines * 4, hipMemcpyDeviceToHost));
+    if (steps) PPOCR_HIP(hipMemcpy(seq, dseq.p, (size_t)steps * 4, hipMemcpyDeviceToHost));
+    return PPOCR_OK;
+}
+
+int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off, int64_t lines, int mode,
+                    int32_t* idx, float* maxprob, int32_t* seq, int64_t* seq_len, float* score) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
+    if (lines == 0) return PPOCR_OK;
+    if (!line_off || !seq_len || !score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    if (int e = check_offsets(line_off, lines)) return e;
+    const int64_t m = line_off[lines];
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (m > 0 && (!a || !seq)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    const size_t wsb = m > 0 ? ws_layout(m, nsplit_for(h, m, cfg)).total : 0;
+    DevBuf da, di, dp, dws, doff, dseq, dlen, dsc;
+    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
+    if (int e = di.alloc((size_t)m * 4)) return e;
+    if (int e = dp.alloc((size_t)m * 4)) return e;
+    if (int e = dws.alloc(wsb)) return e;
+    if (int e = doff.alloc((size_t)(lines + 1) * 8)) return e;
+    if (int e = dseq.alloc((size_t)m * 4)) return e;
+    if (int e = dlen.alloc((size_t)lines * 8)) return e;
+    if (int e = dsc.alloc((size_t)lines * 4)) return e;
+    if (m > 0) {
+        PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
+        if (int e = ppocr_rh_argmax_dev(h, da.as<float>(), m, mode, di.as<int32_t>(), dp.as<float>(), dws.p, wsb,
+                                        nullptr))
+            return e;
+    }
+    PPOCR_HIP(hipMemcpy(doff.p, line_off, (size_t)(lines + 1) * 8, hipMemcpyHostToDevice));
+    if (int e = launch_ctc_greedy(di.as<int32_t>(), dp.as<float>(), doff.as<int64_t>(), lines, 0, dseq.as<int32_t>(),
+                                  dlen.as<int64_t>(), dsc.as<float>(), nullptr))
+        return e;
+    PPOCR_HIP(hipMemcpy(seq_len, dlen.p, (size_t)lines * 8, hipMemcpyDeviceToHost));
+    PPOCR_HIP(hipMemcpy(score, dsc.p, (size_t)lines * 4, hipMemcpyDeviceToHost));
+    if (m > 0) {
+        PPOCR_HIP(hipMemcpy(seq, dseq.p, (size_t)m * 4, hipMemcpyDeviceToHost));
+        if (idx) PPOCR_HIP(hipMemcpy(idx, di.p, (size_t)m * 4, hipMemcpyDeviceToHost));
+        if (maxprob) PPOCR_HIP(hipMemcpy(maxprob, dp.p, (size_t)m * 4, hipMemcpyDeviceToHost));
+    }
+    return PPOCR_OK;
+}
+
+}  // extern "C"

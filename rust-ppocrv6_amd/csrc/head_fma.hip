@@ -1,0 +1,216 @@
+// fp32 vector-FMA kernels of MatMul.12: the accuracy anchor for the MFMA kernels.
+// Same contraction as compute_quantized_b_cols_avx2 (src/ops/matmul.rs:1338-1443) and
+// transposed_b_tile_fma (src/ops/matmul.rs:1025-1087): fp32 products of the activation
+// and the (exactly dequantised) weight, fp32 accumulation, then (sum * scale) + bias.
+// Register tile: every thread owns 8 rows x 4 classes of a 128 x 64 block; k is staged
+// through LDS in chunks of 40.
+#include "kernels.hpp"
+
+namespace ppocr {
+
+namespace {
+constexpr int BM = 128, BN = 64, KC = 40;
+constexpr int AST = BM + 4;  // LDS row strides (floats); +4 keeps 16-byte alignment
+constexpr int WST = BN + 1;
+
+enum { EPI_LOGITS = 0, EPI_PROBS = 1, EPI_STATS = 2 };
+
+template <int EPI>
+__global__ __launch_bounds__(256) void head_fma_kernel(
+    const int8_t* __restrict__ q, const float* __restrict__ w, const float* __restrict__ scale,
+    const float* __restrict__ bias, const float* __restrict__ a, int64_t m, int n, int k,
+    int tiles_per_chunk, float* __restrict__ out, const float* __restrict__ row_max,
+    const float* __restrict__ row_inv, float* __restrict__ p_best, float* __restrict__ p_sum,
+    int* __restrict__ p_idx) {
+    __shared__ __align__(16) float As[KC * AST];
+    __shared__ float Ws[KC * WST];
+
+    const int tid = threadIdx.x, tm = tid >> 4, tn = tid & 15;
+    const int64_t m0 = (int64_t)blockIdx.y * BM;
+    const int chunk = blockIdx.x;
+    const int ntiles = (n + BN - 1) / BN;
+    const int t0 = chunk * tiles_per_chunk;
+    const int t1 = min(t0 + tiles_per_chunk, ntiles);
+
+    RowStat st[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) st[r] = RowStat{-INFINITY, 0.0f, 0.0f, 0};
+    bool refzero = true;
+    float rmax[8], rinv[8];
+    if (EPI == EPI_PROBS) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int64_t row = m0 + 8 * tm + r;
+            rmax[r] = row < m ? row_max[row] : 0.0f;
+            rinv[r] = row < m ? row_inv[row] : 0.0f;
+        }
+    }
+
+    for (int t = t0; t < t1; ++t) {
+        const int n0 = t * BN;
+        float acc[8][4];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[r][j] = 0.0f;
+
+        for (int k0 = 0; k0 < k; k0 += KC) {
+            __syncthreads();
+            for (int idx = tid; idx < BM * KC; idx += 256) {
+                const int mm = idx / KC, kk = idx % KC;
+                const int64_t row = m0 + mm;
+                As[kk * AST + mm] = (row < m && k0 + kk < k) ? a[row * k + k0 + kk] : 0.0f;
+            }
+            for (int idx = tid; idx < BN * KC; idx += 256) {
+                const int nn = idx / KC, kk = idx % KC;
+                const int col = n0 + nn;
+                float v = 0.0f;
+                if (col < n && k0 + kk < k)
+                    v = q ? (float)q[(int64_t)col * k + k0 + kk] : w[(int64_t)col * k + k0 + kk];
+                Ws[kk * WST + nn] = v;
+            }
+            __syncthreads();
+            const int kend = min(KC, k - k0);
+            for (int kk = 0; kk < kend; ++kk) {
+                const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm]);
+                const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm + 4]);
+                float wv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wv[j] = Ws[kk * WST + tn + 16 * j];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc[r][j] = fmaf(a0[r], wv[j], acc[r][j]);
+                        acc[r + 4][j] = fmaf(a1[r], wv[j], acc[r + 4][j]);
+                    }
+                }
+            }
+        }
+
+        if (EPI == EPI_STATS) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                float tv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = n0 + tn + 16 * j;
+                    tv[j] = col < n ? fmaf(acc[r][j], scale[col] * kLog2e, bias[col] * kLog2e) : -INFINITY;
+                }
+                float tmax = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
+                const bool better = tmax > st[r].best;
+                if (better) {
+                    int jj = 3;
+#pragma unroll
+                    for (int j = 2; j >= 0; --j) jj = (tv[j] == tmax) ? j : jj;
+                    st[r].best = tmax;
+                    st[r].idx = n0 + tn + 16 * jj;
+                }
+                const bool shift =
+                    st[r].best != -INFINITY && (st[r].best > st[r].ref + 64.0f || st[r].best < st[r].ref - 64.0f);
+                if (__any(shift)) {
+                    if (shift) {
+                        const float nr = st[r].best;
+                        st[r].sum *= __builtin_amdgcn_exp2f(st[r].ref - nr);
+                        st[r].ref = nr;
+                    }
+                    refzero = false;
+                }
+                float e = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) e += __builtin_amdgcn_exp2f(refzero ? tv[j] : tv[j] - st[r].ref);
+                st[r].sum += e;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = n0 + tn + 16 * j;
+                if (col >= n) continue;
+                const float sc = scale[col], bi = bias[col];
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const int64_t row = m0 + 8 * tm + r;
+                    if (row >= m) continue;
+                    float v;
+                    if (EPI == EPI_LOGITS)
+                        v = __fadd_rn(__fmul_rn(acc[r][j], sc), bi);
+                    else
+                        v = __builtin_amdgcn_exp2f(fmaf(acc[r][j], sc * kLog2e, bi * kLog2e) - rmax[r]) * rinv[r];
+                    out[row * n + col] = v;
+                }
+            }
+        }
+    }
+
+    if (EPI == EPI_STATS) {
+        // the 16 threads of one tm are 16 consecutive lanes: butterfly over them.
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            RowStat s = st[r];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                RowStat other;
+                other.best = __shfl_xor(s.best, o, 64);
+                other.sum = __shfl_xor(s.sum, o, 64);
+                other.ref = __shfl_xor(s.ref, o, 64);
+                other.idx = __shfl_xor(s.idx, o, 64);
+                s = stat_merge(s, other);
+            }
+            const int64_t row = m0 + 8 * tm + r;
+            if (tn == 0 && row < m) {
+                p_best[(int64_t)chunk * m + row] = s.best;
+                p_sum[(int64_t)chunk * m + row] = s.sum;
+                p_idx[(int64_t)chunk * m + row] = s.idx;
+            }
+        }
+    }
+}
+
+int check_fma_args(int64_t m, int64_t n, int64_t k) {
+    if (n > 0x7fffffff - BN || k > 0x7fffffff) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: shape too large");
+    if ((m + BM - 1) / BM > 65535) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large for the fp32 path");
+    return PPOCR_OK;
+}
+}  // namespace
+
+int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
+                      const float* a, int64_t m, int64_t n, int64_t k, float* out, hipStream_t st) {
+    if (int e = check_fma_args(m, n, k)) return e;
+    if (m <= 0 || n <= 0) return PPOCR_OK;
+    const int ntiles = (int)((n + BN - 1) / BN);
+    dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
+    head_fma_kernel<EPI_LOGITS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, 1, out, nullptr,
+                                                      nullptr, nullptr, nullptr, nullptr);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
+                     const float* a, int64_t m, int64_t n, int64_t k, const float* row_max,
+                     const float* row_inv, float* probs, hipStream_t st) {
+    if (int e = check_fma_args(m, n, k)) return e;
+    if (m <= 0 || n <= 0) return PPOCR_OK;
+    const int ntiles = (int)((n + BN - 1) / BN);
+    dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
+    head_fma_kernel<EPI_PROBS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, 1, probs, row_max,
+                                                     row_inv, nullptr, nullptr, nullptr);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
+                     const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
+                     float* p_sum, int* p_idx, hipStream_t st) {
+    if (int e = check_fma_args(m, n, k)) return e;
+    if (nsplit < 1 || nsplit > 1024) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad nsplit");
+    if (m <= 0) return PPOCR_OK;
+    const int ntiles = (int)((n + BN - 1) / BN);
+    const int tpc = (ntiles + nsplit - 1) / nsplit;
+    dim3 grid(nsplit, (unsigned)((m + BM - 1) / BM));
+    head_fma_kernel<EPI_STATS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, tpc, nullptr, nullptr,
+                                                     nullptr, p_best, p_sum, p_idx);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+}  // namespace ppocr

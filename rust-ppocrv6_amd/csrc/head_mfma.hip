@@ -1,0 +1,638 @@
+// bf16 MFMA kernels of the vocabulary projection MatMul.12 (matmul_quantized_b,
+// src/ops/matmul.rs:1204-1336; matmul_transposed_b, src/ops/matmul.rs:514-897) and of its
+// fusion with Softmax.2 (src/ops/softmax.rs:199-285) and the CTC argmax
+// (src/postprocess/ctc.rs:151-163).
+//
+// Exactness: int8 weights are exact in bf16 (|q| <= 127 < 2^8).  The fp32 activation is
+// split into bf16 terms a = a0 + a1 + a2 + ... (each term the bf16 rounding of what the
+// previous ones left), and the products of all terms are summed by the MFMA in fp32:
+// the terms are concatenated along k, so one accumulation chain covers every term.
+//
+// Operand layout of v_mfma_f32_32x32x16_bf16 (checked on gfx950): lane l holds row
+// (l % 32) of A and column (l % 32) of B for k in [8*(l/32), 8*(l/32) + 8); the result
+// D[i][j] sits in lane j + 32*((i/4) % 2), register (i % 4) + 4*(i/8).
+//
+// K-concatenation: the product list ("pairs") of a configuration, times the G groups of
+// 8 along k, gives P = pairs*G pair-groups; MFMA step s feeds pair-group 2s to lanes
+// 0-31 and 2s+1 to lanes 32-63 (a half-step past P reads a zero block).
+#include <utility>
+
+#include "kernels.hpp"
+
+namespace ppocr {
+
+template <int C>
+struct CfgT;
+template <>
+struct CfgT<CFG_Q1> {  // a0 * q
+    static constexpr int pairs = 1, wplanes = 1, terms = 1;
+    __host__ __device__ static constexpr int act(int) { return 0; }
+    __host__ __device__ static constexpr int wpl(int) { return 0; }
+};
+template <>
+struct CfgT<CFG_Q2> {  // a0 * q + a1 * q
+    static constexpr int pairs = 2, wplanes = 1, terms = 2;
+    __host__ __device__ static constexpr int act(int p) { return p; }
+    __host__ __device__ static constexpr int wpl(int) { return 0; }
+};
+template <>
+struct CfgT<CFG_Q3> {  // a0 * q + a1 * q + a2 * q
+    static constexpr int pairs = 3, wplanes = 1, terms = 3;
+    __host__ __device__ static constexpr int act(int p) { return p; }
+    __host__ __device__ static constexpr int wpl(int) { return 0; }
+};
+template <>
+struct CfgT<CFG_F1> {  // a0 * w0
+    static constexpr int pairs = 1, wplanes = 2, terms = 1;
+    __host__ __device__ static constexpr int act(int) { return 0; }
+    __host__ __device__ static constexpr int wpl(int) { return 0; }
+};
+template <>
+struct CfgT<CFG_F3> {  // a0 * w0 + a0 * w1 + a1 * w0
+    static constexpr int pairs = 3, wplanes = 2, terms = 2;
+    __host__ __device__ static constexpr int act(int p) { return p == 2 ? 1 : 0; }
+    __host__ __device__ static constexpr int wpl(int p) { return p == 1 ? 1 : 0; }
+};
+
+bool mfma_supports_groups(int G) { return G == 15 || G == 10; }
+
+// Tile geometry of a configuration: P pair-groups, S MFMA steps, FRAG bytes of weight
+// fragments per staged tile, REC bytes per tile record (fragments + epilogue constants),
+// BUF bytes per LDS buffer (record + a 512-byte zero block for the half-step past P).
+template <int C, int G>
+struct Geo {
+    static constexpr int P = CfgT<C>::pairs * G;
+    static constexpr int S = (P + 1) / 2;
+    static constexpr int FRAG = CfgT<C>::wplanes * G * 512;
+    static constexpr int REC = FRAG + 512;
+    static constexpr int BUF = REC + 512;
+    // LDS byte offset of the fragment of pair-group pg within a staged tile.
+    __host__ __device__ static constexpr int off(int pg) {
+        return pg >= P ? REC : (CfgT<C>::wpl(pg / G) * G + pg % G) * 512;
+    }
+};
+
+// Weight fragment of MFMA step s for lane (i, h).  In the common case the two lane halves
+// read consecutive fragments, so the address is one per-lane register plus an immediate.
+template <int C, int G>
+__device__ __forceinline__ bf16x8 weight_frag(const uint8_t* buf, int s, int lane_base, int i16, int h) {
+    const int o0 = Geo<C, G>::off(2 * s);
+    const int o1 = Geo<C, G>::off(2 * s + 1);
+    const int addr = (o1 - o0 == 512) ? lane_base + o0 : i16 + (h ? o1 : o0);
+    return *reinterpret_cast<const bf16x8*>(buf + addr);
+}
+
+// Grid position -> (block of rows, vocabulary chunk).  Workgroups go to the 8 XCDs of
+// the MI355X round-robin by id, so ids are arranged so that every XCD works on its own
+// 1/8 of the vocabulary (or of a multiple of it) and keeps that slice of the weight
+// tiles resident in its L2.
+__device__ __forceinline__ void map_block(int bid, int nsplit, int* mbi, int* chunk) {
+    const int x = bid & 7, slot = bid >> 3;
+    if (nsplit >= 8) {
+        const int per = nsplit >> 3;
+        *chunk = x * per + slot % per;
+        *mbi = slot / per;
+    } else {
+        const int r8 = 8 / nsplit;
+        *chunk = x % nsplit;
+        *mbi = slot * r8 + x / nsplit;
+    }
+}
+static int grid_blocks(int mblocks, int nsplit) {
+    if (nsplit >= 8) return mblocks * nsplit;
+    const int r8 = 8 / nsplit;
+    return ((mblocks + r8 - 1) / r8) * 8;
+}
+
+// Split x into bf16 terms and return term t (0 = nearest bf16, 1 = nearest bf16 of the
+// remainder, 2 = of the remainder after that).  Every subtraction is exact.
+__device__ __forceinline__ __bf16 split_term(float x, int t) {
+    const __bf16 b0 = (__bf16)x;
+    if (t == 0) return b0;
+    const float r1 = x - (float)b0;
+    const __bf16 b1 = (__bf16)r1;
+    if (t == 1) return b1;
+    const float r2 = r1 - (float)b1;
+    return (__bf16)r2;
+}
+
+// Activation fragment of one lane for MFMA step s: row `row` of a (zero when the row
+// is not valid), the 8 k values of the lane's pair-group, as the bf16 term that pair
+// uses; `amax` is raised to the largest |value| loaded.  `vec`: rows and groups are
+// 16-byte aligned, so each fragment is two float4 loads.
+template <int C, int G>
+__device__ __forceinline__ bf16x8 act_frag(const float* __restrict__ a, int64_t row, bool valid, int k, bool vec,
+                                          int s, int h, float& amax) {
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (__bf16)0.0f;
+    const int pg = 2 * s + h;
+    if (pg >= Geo<C, G>::P || !valid) return f;
+    const int p = pg / G, g = pg % G;
+    const int term = CfgT<C>::act(p);
+    const float* src = a + row * (int64_t)k + 8 * g;
+    float x[8];
+    if (vec && 8 * g + 8 <= k) {
+        const f32x4 v0 = reinterpret_cast<const f32x4*>(src)[0];
+        const f32x4 v1 = reinterpret_cast<const f32x4*>(src)[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[e] = v0[e];
+            x[4 + e] = v1[e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (8 * g + e < k) ? src[e] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        amax = fmaxf(amax, __builtin_fabsf(x[e]));
+        f[e] = split_term(x[e], term);
+    }
+    return f;
+}
+
+// Rows of the batch a workgroup works on: a contiguous block of rows, or (rescue pass)
+// entries of a device-side row list.
+struct RowSource {
+    const int* list;  // null: contiguous rows
+    int count;        // list length
+    __device__ __forceinline__ int64_t row(int64_t j, int64_t m, bool& valid) const {
+        if (list) {
+            valid = j < count;
+            return valid ? (int64_t)list[j] : 0;
+        }
+        valid = j < m;
+        return j;
+    }
+};
+
+// Precision guard of the split-activation modes: a row whose largest |a| times the
+// head's largest |w| exceeds the limit is appended to a device list, to be recomputed
+// with one more activation term.  lanes i and i+32 see complementary k groups.
+__device__ __forceinline__ void guard_append(float amax, float amax_limit, bool valid, int64_t row, int h,
+                                             int* guard_count, int* guard_rows) {
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    if (h == 0 && valid && amax > amax_limit) {
+        const int pos = atomicAdd(guard_count, 1);
+        guard_rows[pos] = (int)row;
+    }
+}
+
+// Global -> registers -> LDS staging of one tile record by 256 threads (16-byte chunks).
+// Every register is loaded unconditionally (indices clamped in bounds) so the staging
+// stays in registers and the load latency hides behind the MFMAs of the current tile.
+template <int REC>
+struct Stage {
+    static constexpr int CH = REC / 16;
+    static constexpr int PER = (CH + 255) / 256;
+    static_assert(PER >= 1 && PER <= 4, "tile record too large");
+    u32x4 v0, v1, v2, v3;
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ src, int tid) {
+        const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+        v0 = s4[min(tid, CH - 1)];
+        if constexpr (PER > 1) v1 = s4[min(tid + 256, CH - 1)];
+        if constexpr (PER > 2) v2 = s4[min(tid + 512, CH - 1)];
+        if constexpr (PER > 3) v3 = s4[min(tid + 768, CH - 1)];
+    }
+    __device__ __forceinline__ void store(uint8_t* dst, int tid) const {
+        u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+        if (CH >= 256 || tid < CH) d4[tid] = v0;
+        if constexpr (PER > 1)
+            if (CH >= 512 || tid + 256 < CH) d4[tid + 256] = v1;
+        if constexpr (PER > 2)
+            if (CH >= 768 || tid + 512 < CH) d4[tid + 512] = v2;
+        if constexpr (PER > 3)
+            if (CH >= 1024 || tid + 768 < CH) d4[tid + 768] = v3;
+    }
+};
+
+__device__ __forceinline__ void zero_blocks(uint8_t* lds, int buf_bytes, int rec_bytes, int tid) {
+    if (tid < 64) reinterpret_cast<u32x4*>(lds + (tid >> 5) * buf_bytes + rec_bytes)[tid & 31] = u32x4{0, 0, 0, 0};
+}
+
+// ============================================================ logits: out = (a w^T)*scale + bias
+// Rows of the MFMA = activation rows, columns = classes: a lane owns one class of each
+// tile, so a store instruction writes 32 consecutive classes (128 bytes) in each of two
+// rows.  Each workgroup (4 waves x 32 rows) walks one vocabulary chunk.
+template <int C, int G, int EPI>  // EPI 0: logits, 1: probabilities
+__global__ __launch_bounds__(256, 2) void rows_mfma_kernel(
+    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles, int n,
+    int nsplit, int tiles_per_chunk, int mblocks, const float* __restrict__ row_max,
+    const float* __restrict__ row_inv, float* __restrict__ out, float amax_limit, int* __restrict__ guard_count,
+    int* __restrict__ guard_rows, const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
+    using GE = Geo<C, G>;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    int mbi, chunk;
+    map_block(blockIdx.x, nsplit, &mbi, &chunk);
+    if (mbi >= mblocks) return;
+    const int t0 = chunk * tiles_per_chunk;
+    const int t1 = min(t0 + tiles_per_chunk, tiles);
+    if (t0 >= t1) return;
+    const RowSource src{gather_rows, gather_rows ? *gather_count : 0};
+    const int64_t nblocks = gather_rows ? ((int64_t)src.count + 127) / 128 : mblocks;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
+    zero_blocks(lds, GE::BUF, GE::REC, tid);
+    const int lb = i * 16 + h * 512;
+
+    for (int64_t blk = mbi; blk < nblocks; blk += mblocks) {
+        const int64_t j0 = blk * 128 + wave * 32;
+        bool valid;
+        const int64_t arow = src.row(j0 + i, m, valid);
+        float amax = 0.0f;
+        bf16x8 bf[GE::S];
+#pragma unroll
+        for (int s = 0; s < GE::S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec != 0, s, h, amax);
+        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid, arow, h, guard_count, guard_rows);
+
+        // rows of this lane's 16 accumulators (r -> activation-row slot 8*(r/4) + 4*h + (r%4))
+        int64_t orow[16];
+        bool ovalid[16];
+        bool all_valid = true;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            bool v;
+            orow[r] = src.row(j0 + 8 * (r >> 2) + 4 * h + (r & 3), m, v);
+            ovalid[r] = v;
+            all_valid = all_valid && v;
+        }
+        all_valid = __all(all_valid);
+        float rmax[16], rinv[16];
+        if (EPI == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                rmax[r] = ovalid[r] ? row_max[orow[r]] : 0.0f;
+                rinv[r] = ovalid[r] ? row_inv[orow[r]] : 0.0f;
+            }
+        }
+
+        Stage<GE::REC> stg;
+        stg.load(rec + (size_t)t0 * GE::REC, tid);
+        __syncthreads();  // previous block's last tile is no longer being read
+        stg.store(lds, tid);
+        __syncthreads();
+
+        for (int t = t0; t < t1; ++t) {
+            const int cur = (t - t0) & 1;
+            const bool more = t + 1 < t1;
+            if (more) stg.load(rec + (size_t)(t + 1) * GE::REC, tid);
+            const uint8_t* buf = lds + cur * GE::BUF;
+            f32x16 acc = {};
+#pragma unroll
+            for (int s = 0; s < GE::S; ++s)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[s], weight_frag<C, G>(buf, s, lb, i * 16, h), acc, 0,
+                                                              0, 0);
+            const float* ep = reinterpret_cast<const float*>(buf + GE::FRAG);
+            float c0, c1;
+            if (EPI == 0) {
+                c0 = ep[64 + i];  // scale
+                c1 = ep[96 + i];  // bias
+            } else {
+                c0 = ep[i];       // scale * log2(e)
+                c1 = ep[32 + i];  // bias * log2(e)
+            }
+            const int col = t * 32 + i;
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (EPI == 0) {
+#pragma clang fp contract(off)
+                    v[r] = acc[r] * c0 + c1;  // (sum * scale) + bias, two roundings (src/ops/matmul.rs:1396-1409)
+                } else {
+                    v[r] = __builtin_amdgcn_exp2f(fmaf(acc[r], c0, c1) - rmax[r]) * rinv[r];
+                }
+            }
+            if (all_valid && t * 32 + 32 <= n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) out[orow[r] * n + col] = v[r];
+            } else if (col < n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (ovalid[r]) out[orow[r] * n + col] = v[r];
+            }
+            if (more) stg.store(lds + (cur ^ 1) * GE::BUF, tid);
+            __syncthreads();
+        }
+    }
+}
+
+// ============================================================ online statistics epilogue
+// Rows of the MFMA = classes, columns = activation rows: lane (i, h) owns activation row
+// i and 16 classes n0 + 8*(r/4) + 4*h + (r%4), so a row's max/argmax/sum over its classes
+// needs no cross-lane traffic until the end of the chunk.  t = logit * log2(e) comes from
+// one fma with the record's scale*log2(e) and bias*log2(e).  The sum is kept relative to
+// `ref`, which stays 0 unless the row's maximum leaves [-64, 64]; then it follows the
+// maximum so the sum can neither overflow nor lose the maximum's term.
+__device__ __forceinline__ void stats_update(const f32x16& acc, const float* sl, const float* bl, int nrow0,
+                                             float& best, float& sum, float& ref, int& bidx, bool& refzero) {
+    float t[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t[r] = fmaf(acc[r], sl[r], bl[r]);
+    const float m01 = fmaxf(fmaxf(t[0], t[1]), t[2]);
+    const float m02 = fmaxf(fmaxf(t[3], t[4]), t[5]);
+    const float m03 = fmaxf(fmaxf(t[6], t[7]), t[8]);
+    const float m04 = fmaxf(fmaxf(t[9], t[10]), t[11]);
+    const float m05 = fmaxf(fmaxf(t[12], t[13]), t[14]);
+    const float tmax = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[15]));
+    const bool better = tmax > best;
+    if (__any(better)) {
+        if (better) {
+            int ri = 15;
+#pragma unroll
+            for (int r = 14; r >= 0; --r) ri = (t[r] == tmax) ? r : ri;
+            best = tmax;
+            bidx = nrow0 + 8 * (ri >> 2) + (ri & 3);
+            if (best > ref + 64.0f || best < ref - 64.0f) {
+                sum = (sum == 0.0f) ? 0.0f : sum * __builtin_amdgcn_exp2f(ref - best);
+                ref = best;
+            }
+        }
+        refzero = refzero && !__any(ref != 0.0f);
+    }
+    float e[16];
+    if (refzero) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t[r]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t[r] - ref);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) e[r] += e[r + 8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[r] += e[r + 4];
+    sum += (e[0] + e[2]) + (e[1] + e[3]);
+}
+
+// Fused projection + softmax statistics.  Each workgroup: 4 waves x MB blocks of 32
+// activation rows, one vocabulary chunk; writes per-row partial (max, sum, argmax).
+template <int C, int G, int MB>
+__global__ __launch_bounds__(256, 2) void stats_mfma_kernel(
+    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
+    int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
+    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows,
+    const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
+    using GE = Geo<C, G>;
+    constexpr int RPB = 128 * MB;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    int mbi, chunk;
+    map_block(blockIdx.x, nsplit, &mbi, &chunk);
+    if (mbi >= mblocks) return;
+    const int t0 = chunk * tiles_per_chunk;
+    const int t1 = min(t0 + tiles_per_chunk, tiles);
+    const RowSource src{gather_rows, gather_rows ? *gather_count : 0};
+    const int64_t nblocks = gather_rows ? ((int64_t)src.count + RPB - 1) / RPB : mblocks;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
+    zero_blocks(lds, GE::BUF, GE::REC, tid);
+    const int lb = i * 16 + h * 512;
+
+    for (int64_t blk = mbi; blk < nblocks; blk += mblocks) {
+        const int64_t j0 = blk * RPB + wave * (32 * MB);
+        int64_t arow[MB];
+        bool valid[MB];
+        bf16x8 bf[MB][GE::S];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            arow[b] = src.row(j0 + 32 * b + i, m, valid[b]);
+            float amax = 0.0f;
+#pragma unroll
+            for (int s = 0; s < GE::S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
+            if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
+        }
+
+        float best[MB], sum[MB], ref[MB];
+        int bidx[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            best[b] = -INFINITY;
+            sum[b] = 0.0f;
+            ref[b] = 0.0f;
+            bidx[b] = 0;
+        }
+        bool refzero = true;
+
+        if (t0 < t1) {
+            Stage<GE::REC> stg;
+            stg.load(rec + (size_t)t0 * GE::REC, tid);
+            __syncthreads();  // previous block's last tile is no longer being read
+            stg.store(lds, tid);
+            __syncthreads();
+
+            for (int t = t0; t < t1; ++t) {
+                const int cur = (t - t0) & 1;
+                const bool more = t + 1 < t1;
+                if (more) stg.load(rec + (size_t)(t + 1) * GE::REC, tid);
+                const uint8_t* buf = lds + cur * GE::BUF;
+                f32x16 acc[MB];
+#pragma unroll
+                for (int b = 0; b < MB; ++b) acc[b] = f32x16{};
+#pragma unroll
+                for (int s = 0; s < GE::S; ++s) {
+                    const bf16x8 wf = weight_frag<C, G>(buf, s, lb, i * 16, h);
+#pragma unroll
+                    for (int b = 0; b < MB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc[b], 0, 0, 0);
+                }
+                const float* ep = reinterpret_cast<const float*>(buf + GE::FRAG);
+                float sl[16], bl[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
+                    const f32x4 b4 = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sl[4 * q + e] = s4[e];
+                        bl[4 * q + e] = b4[e];
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                    stats_update(acc[b], sl, bl, t * 32 + 4 * h, best[b], sum[b], ref[b], bidx[b], refzero);
+                if (more) stg.store(lds + (cur ^ 1) * GE::BUF, tid);
+                __syncthreads();
+            }
+        }
+
+        // lanes i and i+32 hold the same activation row: merge, then lanes 0-31 write.
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            RowStat mine{best[b], sum[b], ref[b], bidx[b]};
+            RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
+                          __shfl_xor(bidx[b], 32, 64)};
+            const RowStat r = stat_merge(mine, other);
+            if (h == 0 && valid[b]) {
+                p_best[(int64_t)chunk * m + arow[b]] = r.best;
+                p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
+                p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
+            }
+        }
+    }
+}
+
+__global__ void guard_reset_kernel(int* guard_count) { *guard_count = 0; }
+
+// ============================================================ launchers
+template <int C>
+static constexpr int mb_of() {
+    return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1) ? 2 : 1;
+}
+
+int stats_rows_per_block_mfma(int cfg) {
+    switch (cfg) {
+        case CFG_Q1: return 128 * mb_of<CFG_Q1>();
+        case CFG_Q2: return 128 * mb_of<CFG_Q2>();
+        case CFG_Q3: return 128 * mb_of<CFG_Q3>();
+        case CFG_F1: return 128 * mb_of<CFG_F1>();
+        default: return 128 * mb_of<CFG_F3>();
+    }
+}
+
+// Vocabulary chunks per row block: at least 8 (one slice of the weights per XCD L2), more
+// when there are too few row blocks to give every CU two workgroups.
+int stats_nsplit(int64_t m, int rows_per_block) {
+    const int64_t mblocks = (m + rows_per_block - 1) / rows_per_block;
+    int ns = 8;
+    while (mblocks * ns < 512 && ns < 64) ns *= 2;
+    return ns;
+}
+
+template <typename F>
+static int dispatch_cfg_g(int cfg, int G, F&& f) {
+#define PPOCR_CASE(CC, GG) \
+    if (cfg == CC && G == GG) return f(std::integral_constant<int, CC>{}, std::integral_constant<int, GG>{});
+    PPOCR_CASE(CFG_Q1, 15) PPOCR_CASE(CFG_Q2, 15) PPOCR_CASE(CFG_Q3, 15) PPOCR_CASE(CFG_F1, 15)
+    PPOCR_CASE(CFG_F3, 15) PPOCR_CASE(CFG_Q1, 10) PPOCR_CASE(CFG_Q2, 10) PPOCR_CASE(CFG_Q3, 10)
+    PPOCR_CASE(CFG_F1, 10) PPOCR_CASE(CFG_F3, 10)
+#undef PPOCR_CASE
+    return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: no MFMA kernel for this k / mode");
+}
+
+static bool check_geom(int cfg, const TileGeom& tg, int64_t n, int64_t k) {
+    const int wpl = (cfg == CFG_F1 || cfg == CFG_F3) ? 2 : 1;
+    return tg.wplanes == wpl && k >= 1 && k <= 8LL * tg.G && tg.tiles == (int)((n + 31) / 32) &&
+           mfma_supports_groups(tg.G);
+}
+
+// Rows of a are 16-byte aligned and hold whole float4s: fragments load as float4 pairs.
+static int vec_ok(const float* a, int64_t k) {
+    return ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (k & 3) == 0) ? 1 : 0;
+}
+
+// Vocabulary chunks of the write-bound kernels: a multiple of 8 (one weight slice per
+// XCD), more only when there are too few row blocks to fill the GPU.
+static int rows_nsplit(int64_t mblocks) {
+    int ns = 8;
+    while (mblocks * ns < 1024 && ns < 64) ns *= 2;
+    return ns;
+}
+
+// Configuration that recomputes the rows flagged by the precision guard of `cfg`
+// (-1: the configuration has no guard).
+static int rescue_cfg(int cfg) { return cfg == CFG_Q2 ? CFG_Q3 : -1; }
+
+static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
+                       int64_t n, int64_t k, const float* row_max, const float* row_inv, float* out,
+                       const Guard* guard, hipStream_t st) {
+    if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: tile geometry mismatch");
+    if (m <= 0 || n <= 0) return PPOCR_OK;
+    const int64_t mblocks = (m + 127) / 128;
+    if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
+    const int nsplit = rows_nsplit(mblocks);
+    const int tpc = (tg.tiles + nsplit - 1) / nsplit;
+    const int64_t grid = grid_blocks((int)mblocks, nsplit);
+    if (grid > 0x7fffffff) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
+    const int vec = vec_ok(a, k);
+    const int rcfg = rescue_cfg(cfg);
+    const bool guarded = guard && guard->count && rcfg >= 0;
+    if (guarded) {
+        guard_reset_kernel<<<1, 1, 0, st>>>(guard->count);
+        PPOCR_HIP(hipGetLastError());
+    }
+    int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
+        constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
+        constexpr int LDS = 2 * Geo<C, G>::BUF;
+        auto kern = epi == 0 ? rows_mfma_kernel<C, G, 0> : rows_mfma_kernel<C, G, 1>;
+        kern<<<(unsigned)grid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, (int)mblocks,
+                                              row_max, row_inv, out, guarded ? guard->amax_limit : 0.0f,
+                                              guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
+                                              nullptr, nullptr);
+        PPOCR_HIP(hipGetLastError());
+        return PPOCR_OK;
+    });
+    if (e || !guarded) return e;
+    // rescue: the flagged rows again, one more activation term, every column
+    const int slots = (int)std::min<int64_t>(mblocks, 64);
+    const int rgrid = grid_blocks(slots, nsplit);
+    return dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
+        constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
+        constexpr int LDS = 2 * Geo<C, G>::BUF;
+        auto kern = epi == 0 ? rows_mfma_kernel<C, G, 0> : rows_mfma_kernel<C, G, 1>;
+        kern<<<(unsigned)rgrid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, slots,
+                                               row_max, row_inv, out, 0.0f, nullptr, nullptr, guard->rows,
+                                               guard->count);
+        PPOCR_HIP(hipGetLastError());
+        return PPOCR_OK;
+    });
+}
+
+int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
+                       int64_t k, float* out, const Guard* guard, hipStream_t st) {
+    return launch_rows(cfg, 0, tg, rec, a, m, n, k, nullptr, nullptr, out, guard, st);
+}
+
+int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
+                      int64_t k, const float* row_max, const float* row_inv, float* probs, const Guard* guard,
+                      hipStream_t st) {
+    return launch_rows(cfg, 1, tg, rec, a, m, n, k, row_max, row_inv, probs, guard, st);
+}
+
+int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
+                      int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx, const Guard* guard,
+                      hipStream_t st) {
+    if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
+    if (nsplit != 1 && nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16 && nsplit != 32 && nsplit != 64)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be a power of two <= 64");
+    if (m <= 0) return PPOCR_OK;
+    const int rpb = stats_rows_per_block_mfma(cfg);
+    const int64_t mblocks = (m + rpb - 1) / rpb;
+    if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
+    const int tpc = (tg.tiles + nsplit - 1) / nsplit;
+    const int grid = grid_blocks((int)mblocks, nsplit);
+    const int vec = vec_ok(a, k);
+    const int rcfg = rescue_cfg(cfg);
+    const bool guarded = guard && guard->count && rcfg >= 0;
+    if (guarded) {
+        guard_reset_kernel<<<1, 1, 0, st>>>(guard->count);
+        PPOCR_HIP(hipGetLastError());
+    }
+    int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
+        constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
+        constexpr int LDS = 2 * Geo<C, G>::BUF;
+        stats_mfma_kernel<C, G, mb_of<C>()><<<grid, 256, LDS, st>>>(
+            a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
+            guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
+            nullptr, nullptr);
+        PPOCR_HIP(hipGetLastError());
+        return PPOCR_OK;
+    });
+    if (e || !guarded) return e;
+    // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
+    const int rrpb = stats_rows_per_block_mfma(rcfg);
+    const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, 64);
+    const int rgrid = grid_blocks(slots, nsplit);
+    return dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
+        constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
+        constexpr int LDS = 2 * Geo<C, G>::BUF;
+        stats_mfma_kernel<C, G, mb_of<C>()><<<rgrid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc,
+                                                                     slots, p_best, p_sum, p_idx, 0.0f, nullptr,
+                                                                     nullptr, guard->rows, guard->count);
+        PPOCR_HIP(hipGetLastError());
+        return PPOCR_OK;
+    });
+}
+
+}  // namespace ppocr

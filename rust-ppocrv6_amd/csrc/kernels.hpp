@@ -1,0 +1,77 @@
+// Launch wrappers of the recognition-head kernels (host side).  Every wrapper checks
+// the shapes its grid assumes before it launches and returns a PPOCR_* status.
+#pragma once
+#include "common.hpp"
+
+namespace ppocr {
+
+// ---------------------------------------------------------------- tile records
+// The projection weights live in HBM as one record per 32-class tile:
+//   [plane][group g][row i][8 x bf16]   bf16 weight fragments, g = k / 8
+//   [4][32] f32                          scale*log2e, bias*log2e, scale, bias
+// Rows past n hold zero weights, scale 0, bias 0 and bias*log2e = -inf, so they never
+// win a maximum and add exp2(-inf) = 0 to a softmax sum.
+struct TileGeom {
+    int G;        // groups of 8 along k (k <= 8*G)
+    int wplanes;  // 1 for an INT8 head (q as bf16), 2 for an FP32 head (hi, lo)
+    int tiles;    // ceil(n / 32)
+    size_t frag_bytes() const { return (size_t)wplanes * G * 512; }
+    size_t rec_bytes() const { return frag_bytes() + 512; }
+};
+
+// Arithmetic configurations of the MFMA kernels: which activation term multiplies which
+// weight plane in each of the K-concatenated products.
+enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4 };
+
+// Precision guard of the split-activation modes: rows whose max |a| exceeds amax_limit
+// are collected in rows[0 .. *count) and recomputed with one more activation term.
+struct Guard {
+    float amax_limit;
+    int* count;
+    int* rows;
+};
+
+// Supported group counts (k = 113..120 and k = 73..80, the PP-OCRv6 small and tiny heads).
+bool mfma_supports_groups(int G);
+
+int launch_pack_int8(const float* w_t, int64_t n, int64_t k, int8_t* q, float* scales,
+                     hipStream_t st);
+
+int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
+                       int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
+// Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.
+int stats_nsplit(int64_t m, int rows_per_block);
+int stats_rows_per_block_mfma(int cfg);
+int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
+                      int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
+                      const Guard* guard, hipStream_t st);
+int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
+                      int64_t n, int64_t k, const float* row_max, const float* row_inv, float* probs,
+                      const Guard* guard, hipStream_t st);
+
+// fp32 vector FMA path over the packed int8 weights (q != null) or fp32 weights (w != null).
+int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
+                      const float* a, int64_t m, int64_t n, int64_t k, float* out, hipStream_t st);
+constexpr int kFmaRowsPerBlock = 128;
+int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
+                     const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
+                     float* p_sum, int* p_idx, hipStream_t st);
+int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
+                     const float* a, int64_t m, int64_t n, int64_t k, const float* row_max,
+                     const float* row_inv, float* probs, hipStream_t st);
+
+// Merge the per-chunk partials of each row: argmax index, max probability, and (when
+// row_max/row_inv are non-null) the row's log2-domain maximum and 1/sum for a probs pass.
+int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m,
+                       int nsplit, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
+                       hipStream_t st);
+
+int launch_softmax_rows(float* x, int64_t rows, int64_t cols, int32_t* idx, float* maxprob,
+                        hipStream_t st);
+int launch_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx, float* val,
+                       hipStream_t st);
+int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* line_off,
+                      int64_t lines, int32_t blank, int32_t* seq, int64_t* seq_len, float* score,
+                      hipStream_t st);
+
+}  // namespace ppocr

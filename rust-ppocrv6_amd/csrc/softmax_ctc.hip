@@ -1,0 +1,282 @@
+// Softmax.2 (softmax_inplace, src/ops/softmax.rs:199-285), the per-step argmax of the CTC
+// decoder (find_argmax, src/postprocess/ctc.rs:178-258), the merge of the fused head's
+// per-chunk statistics, and the CTC collapse (CtcDecoder::decode_batch,
+// src/postprocess/ctc.rs:144-172).
+#include "kernels.hpp"
+
+namespace ppocr {
+
+namespace {
+
+// (value, index) pair reduction: larger value wins, equal values keep the lower index
+// (first occurrence).  NaN never wins because every comparison with it is false.
+__device__ __forceinline__ void argmax_pair(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(i, o, 64);
+        argmax_pair(v, i, ov, oi);
+    }
+}
+
+// Block (256 threads) reductions through LDS; every thread gets the result.
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ void block_argmax(float& v, int& i, float* redv, int* redi) {
+    wave_argmax(v, i);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        redv[w] = v;
+        redi[w] = i;
+    }
+    __syncthreads();
+    v = redv[0];
+    i = redi[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) argmax_pair(v, i, redv[j], redi[j]);
+}
+
+// One 256-thread workgroup per row.  Rows up to 256*VPT classes stay in registers, so
+// the row is read once and written once.  exp(x - max) is computed as
+// exp2((x - max) * log2(e)) on the hardware exp2.
+template <int VPT>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(float* __restrict__ x, int64_t rows, int cols,
+                                                           int32_t* __restrict__ idx,
+                                                           float* __restrict__ maxprob) {
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    const int64_t row = blockIdx.x;
+    float* p = x + row * (int64_t)cols;
+    const int tid = threadIdx.x;
+    float v[VPT];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c = tid + 256 * j;
+        v[j] = c < cols ? p[c] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    mx = block_max(mx, redf);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c = tid + 256 * j;
+        v[j] = c < cols ? __builtin_amdgcn_exp2f((v[j] - mx) * kLog2e) : 0.0f;
+        s += v[j];
+    }
+    s = block_sum(s, redf);
+    const float inv = s > 0.0f ? __fdiv_rn(1.0f, s) : 1.0f;
+    float bv = -INFINITY;
+    int bi = 0;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c = tid + 256 * j;
+        if (c < cols) {
+            const float pv = v[j] * inv;
+            p[c] = pv;
+            if (pv > bv) {
+                bv = pv;
+                bi = c;
+            }
+        }
+    }
+    if (idx || maxprob) {
+        block_argmax(bv, bi, redf, redi);
+        if (tid == 0) {
+            if (idx) idx[row] = bi;
+            if (maxprob) maxprob[row] = bv;
+        }
+    }
+}
+
+// Rows too long for registers: three passes over global memory.
+__global__ __launch_bounds__(256) void softmax_rows_stream_kernel(float* __restrict__ x, int64_t rows,
+                                                                  int64_t cols, int32_t* __restrict__ idx,
+                                                                  float* __restrict__ maxprob) {
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    float* p = x + (int64_t)blockIdx.x * cols;
+    float mx = -INFINITY;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, p[c]);
+    mx = block_max(mx, redf);
+    float s = 0.0f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+        const float e = __builtin_amdgcn_exp2f((p[c] - mx) * kLog2e);
+        p[c] = e;
+        s += e;
+    }
+    s = block_sum(s, redf);
+    const float inv = s > 0.0f ? __fdiv_rn(1.0f, s) : 1.0f;
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+        const float pv = p[c] * inv;
+        p[c] = pv;
+        if (pv > bv) {
+            bv = pv;
+            bi = (int)c;
+        }
+    }
+    if (idx || maxprob) {
+        block_argmax(bv, bi, redf, redi);
+        if (threadIdx.x == 0) {
+            if (idx) idx[blockIdx.x] = bi;
+            if (maxprob) maxprob[blockIdx.x] = bv;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restrict__ x, int64_t cols,
+                                                          int32_t* __restrict__ idx, float* __restrict__ val) {
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    const float* p = x + (int64_t)blockIdx.x * cols;
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+        const float v = p[c];
+        if (v > bv) {
+            bv = v;
+            bi = (int)c;
+        }
+    }
+    block_argmax(bv, bi, redf, redi);
+    if (threadIdx.x == 0) {
+        idx[blockIdx.x] = bi;
+        val[blockIdx.x] = bv;
+    }
+}
+
+__global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restrict__ p_best,
+                                                          const float* __restrict__ p_sum,
+                                                          const int* __restrict__ p_idx, int64_t m, int nsplit,
+                                                          int32_t* __restrict__ idx, float* __restrict__ maxprob,
+                                                          float* __restrict__ row_max, float* __restrict__ row_inv) {
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= m) return;
+    RowStat s{-INFINITY, 0.0f, 0.0f, 0};
+    for (int c = 0; c < nsplit; ++c) {
+        RowStat o;
+        o.best = p_best[(int64_t)c * m + row];
+        o.sum = p_sum[(int64_t)c * m + row];
+        o.ref = (o.best == -INFINITY) ? 0.0f : o.best;  // partial sums are relative to their max
+        o.idx = p_idx[(int64_t)c * m + row];
+        s = stat_merge(s, o);
+    }
+    // s.sum is relative to s.best, so the maximum itself contributes exp2(0) = 1 and the
+    // sum is at least 1 (rounding of the rescaling could leave it an ulp below).
+    const float S = (s.best == -INFINITY) ? 0.0f : fmaxf(s.sum, 1.0f);
+    const float inv = S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
+    if (idx) idx[row] = s.idx;
+    if (maxprob) maxprob[row] = inv;
+    if (row_max) row_max[row] = s.best;
+    if (row_inv) row_inv[row] = inv;
+}
+
+// One wavefront per text line.  Steps are taken 64 at a time; the emit mask is a ballot,
+// emitted indices are compacted by prefix popcount, and the score is summed in step order
+// (every lane runs the same sequential sum over shuffled values).
+__global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restrict__ idx,
+                                                         const float* __restrict__ val,
+                                                         const int64_t* __restrict__ line_off, int64_t lines,
+                                                         int32_t blank, int32_t* __restrict__ seq,
+                                                         int64_t* __restrict__ seq_len, float* __restrict__ score) {
+    const int lane = threadIdx.x & 63;
+    const int64_t line = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (line >= lines) return;
+    const int64_t t0 = line_off[line], t1 = line_off[line + 1];
+    int64_t cnt = 0;
+    float sum = -0.0f;
+    for (int64_t base = t0; base < t1; base += 64) {
+        const int64_t t = base + lane;
+        const bool valid = t < t1;
+        const int32_t id = valid ? idx[t] : blank;
+        const int32_t prev = (valid && t > t0) ? idx[t - 1] : blank;
+        const bool emit = valid && id != blank && id != prev;
+        const float v = valid ? val[t] : 0.0f;
+        const uint64_t mask = __ballot(emit);
+        const int pos = __popcll(mask & ((1ull << lane) - 1ull));
+        if (emit) seq[t0 + cnt + pos] = id;
+        uint64_t mm = mask;
+        while (mm) {
+            const int src = __ffsll((unsigned long long)mm) - 1;
+            mm &= mm - 1;
+            sum += __shfl(v, src, 64);
+        }
+        cnt += __popcll(mask);
+    }
+    if (lane == 0) {
+        seq_len[line] = cnt;
+        score[line] = cnt ? sum / (float)cnt : 0.0f;
+    }
+}
+
+}  // namespace
+
+int launch_softmax_rows(float* x, int64_t rows, int64_t cols, int32_t* idx, float* maxprob, hipStream_t st) {
+    if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: negative shape");
+    if (rows == 0 || cols == 0) return PPOCR_OK;
+    if (rows > 0x7fffffffLL || cols > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: shape too large");
+    if (cols <= 256 * 8)
+        softmax_rows_kernel<8><<<(unsigned)rows, 256, 0, st>>>(x, rows, (int)cols, idx, maxprob);
+    else if (cols <= 256 * 80)
+        softmax_rows_kernel<80><<<(unsigned)rows, 256, 0, st>>>(x, rows, (int)cols, idx, maxprob);
+    else
+        softmax_rows_stream_kernel<<<(unsigned)rows, 256, 0, st>>>(x, rows, cols, idx, maxprob);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx, float* val, hipStream_t st) {
+    if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative shape");
+    if (rows == 0) return PPOCR_OK;
+    if (rows > 0x7fffffffLL || cols > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: shape too large");
+    argmax_rows_kernel<<<(unsigned)rows, 256, 0, st>>>(x, cols, idx, val);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
+                       int32_t* idx, float* maxprob, float* row_max, float* row_inv, hipStream_t st) {
+    if (m <= 0) return PPOCR_OK;
+    const int64_t blocks = (m + 255) / 256;
+    if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
+    merge_stats_kernel<<<(unsigned)blocks, 256, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max,
+                                                         row_inv);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* line_off, int64_t lines,
+                      int32_t blank, int32_t* seq, int64_t* seq_len, float* score, hipStream_t st) {
+    if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
+    if (lines == 0) return PPOCR_OK;
+    const int64_t blocks = (lines + 3) / 4;
+    if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
+    ctc_greedy_kernel<<<(unsigned)blocks, 256, 0, st>>>(idx, maxprob, line_off, lines, blank, seq, seq_len, score);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+}  // namespace ppocr

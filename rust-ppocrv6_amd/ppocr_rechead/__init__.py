@@ -1,0 +1,328 @@
+"""Host-side mirror of rust_ppocrv6's recognition-head operator API, on the MI355X library.
+
+The names, argument meaning and error behaviour follow the reference's operators so a
+caller (or a test) reads the same as against the Rust crate:
+
+    QuantizedWeight.from_f32_transposed   src/ops/matmul.rs:1173-1202
+    matmul_quantized_b                    src/ops/matmul.rs:1204-1336
+    matmul_transposed_b                   src/ops/matmul.rs:514-897
+    softmax / softmax_inplace             src/ops/softmax.rs:49-285
+    CtcDecoder                            src/postprocess/ctc.rs:7-258
+    RecHead.weight_footprint_bytes        src/engine/model.rs:651-667
+
+Every computation runs in libppocr_rechead.so (hand-written gfx950 kernels).  Errors
+come back as OcrError(op, msg), the shape of OcrError::OperatorError (src/error.rs).
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import (MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
+                   PPOCR_ERR_INVALID_ARG, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
+
+__all__ = [
+    "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "matmul_quantized_b", "matmul_transposed_b",
+    "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3",
+]
+
+
+class OcrError(Exception):
+    """OcrError::OperatorError { op, msg } (src/error.rs:4-27)."""
+
+    def __init__(self, op, msg, code=PPOCR_ERR_INVALID_ARG):
+        super().__init__(f"{op}: {msg}")
+        self.op = op
+        self.msg = msg
+        self.code = code
+
+
+def _check(rc):
+    if rc != PPOCR_OK:
+        text = _lib.last_error()
+        op, _, msg = text.partition(": ")
+        raise OcrError(op or "RecHeadHip", msg or text, rc)
+
+
+def _ptr(arr):
+    return None if arr is None else arr.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+class QuantizedWeight:
+    """Per-output-class symmetric INT8 weight (src/ops/matmul.rs:1165-1171).
+
+    data: int8 [rows][cols], one row per output class; scales: f32 [rows]."""
+
+    def __init__(self, data, scales):
+        self.data = np.ascontiguousarray(data, dtype=np.int8)
+        self.scales = np.ascontiguousarray(scales, dtype=np.float32)
+        self.rows, self.cols = self.data.shape
+
+    @classmethod
+    def from_f32_transposed(cls, w_t):
+        """Pack W^T [n][k] on the GPU, bit-exact with the reference packer."""
+        w_t = _f32(w_t)
+        if w_t.ndim != 2:
+            raise OcrError("QuantizedWeight", f"expected a 2-D [n, k] weight, got shape {list(w_t.shape)}")
+        n, k = w_t.shape
+        q = np.empty((n, k), np.int8)
+        s = np.empty(n, np.float32)
+        if n:
+            _check(_lib.lib().ppocr_rh_pack_int8(_ptr(w_t), n, k, _ptr(q), _ptr(s)))
+        return cls(q, s)
+
+    def nbytes(self):
+        return self.data.size + 4 * self.scales.size
+
+
+class RecHead:
+    """The head weight resident in HBM: what Model keeps for MatMul.12 plus its folded bias.
+
+    Build it once (INT8: from a QuantizedWeight; FP32: from W^T), then run any number of
+    batches.  `mode` picks the arithmetic (MODE_BF16X2 default for INT8, MODE_BF16X3 for
+    FP32)."""
+
+    def __init__(self, qw=None, bias=None, w_t=None, device=0):
+        self._h = ctypes.c_void_p()
+        bias_c = None if bias is None else _f32(bias)
+        if qw is not None:
+            if bias_c is not None and bias_c.size != qw.rows:
+                raise OcrError("MatMulQuantized", f"bias has {bias_c.size} elements but n is {qw.rows}")
+            self.quantized = True
+            self.n, self.k = qw.rows, qw.cols
+            _check(_lib.lib().ppocr_rh_create(_ptr(qw.data), _ptr(qw.scales), _ptr(bias_c), self.n, self.k, device,
+                                              ctypes.byref(self._h)))
+        else:
+            w_t = _f32(w_t)
+            if bias_c is not None and bias_c.size != w_t.shape[0]:
+                raise OcrError("MatMulTransposedB", f"bias has {bias_c.size} elements but n is {w_t.shape[0]}")
+            self.quantized = False
+            self.n, self.k = w_t.shape
+            _check(_lib.lib().ppocr_rh_create_f32(_ptr(w_t), _ptr(bias_c), self.n, self.k, device,
+                                                  ctypes.byref(self._h)))
+        self.default_mode = MODE_BF16X2 if self.quantized else MODE_BF16X3
+
+    def close(self):
+        if self._h:
+            _lib.lib().ppocr_rh_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def weight_footprint_bytes(self):
+        """This weight's share of Model::weight_footprint_bytes (src/engine/model.rs:651-667)."""
+        return int(_lib.lib().ppocr_rh_footprint_bytes(self._h))
+
+    def device_bytes(self):
+        return int(_lib.lib().ppocr_rh_device_bytes(self._h))
+
+    def workspace_bytes(self, m, mode=None):
+        return int(_lib.lib().ppocr_rh_workspace_bytes(self._h, m, self.default_mode if mode is None else mode))
+
+    def _rows(self, a, op):
+        a = _f32(a)
+        if a.ndim < 1:
+            raise OcrError(op, "Operand must have valid dimensions")
+        if a.shape[-1] != self.k:
+            raise OcrError(op, f"Inner dimensions must match: {a.shape[-1]} != {self.k}")
+        return a, a.size // self.k if self.k else 0
+
+    def logits(self, a, mode=None):
+        """MatMul.12: [.., m, k] -> [.., m, n] logits (matmul_quantized_b / matmul_transposed_b)."""
+        op = "MatMulQuantizedB" if self.quantized else "MatMulTransposedB"
+        a, rows = self._rows(a, op)
+        out_shape = list(a.shape[:-1]) + [self.n] if a.ndim > 1 else [1, self.n]
+        out = np.empty(out_shape, np.float32)
+        if rows:
+            _check(_lib.lib().ppocr_rh_logits(self._h, _ptr(a), rows, self.default_mode if mode is None else mode,
+                                              _ptr(out)))
+        return out
+
+    def probs(self, a, mode=None):
+        """MatMul.12 -> Softmax.2 in one call: [.., m, k] -> [.., m, n] probabilities."""
+        a, rows = self._rows(a, "RecHeadHip")
+        out = np.empty(list(a.shape[:-1]) + [self.n], np.float32)
+        if rows:
+            _check(_lib.lib().ppocr_rh_probs(self._h, _ptr(a), rows, self.default_mode if mode is None else mode,
+                                             _ptr(out)))
+        return out
+
+    def argmax(self, a, mode=None):
+        """Per row: first-index argmax of the softmax and the max probability."""
+        a, rows = self._rows(a, "RecHeadHip")
+        idx = np.empty(rows, np.int32)
+        mp = np.empty(rows, np.float32)
+        if rows:
+            _check(_lib.lib().ppocr_rh_argmax(self._h, _ptr(a), rows, self.default_mode if mode is None else mode,
+                                              _ptr(idx), _ptr(mp)))
+        return idx, mp
+
+    def decode(self, a, line_off, mode=None):
+        """Whole head over text lines packed back to back: index sequences and scores."""
+        a = _f32(a).reshape(-1, self.k) if self.k else _f32(a)
+        line_off = np.ascontiguousarray(line_off, dtype=np.int64)
+        lines = line_off.size - 1
+        m = int(line_off[-1]) if lines >= 0 else 0
+        if lines < 0:
+            raise OcrError("CtcDecode", "line offsets must hold at least one entry")
+        if m != a.shape[0]:
+            raise OcrError("CtcDecode", f"line offsets cover {m} rows but the input has {a.shape[0]}")
+        idx = np.empty(max(m, 1), np.int32)
+        mp = np.empty(max(m, 1), np.float32)
+        seq = np.zeros(max(m, 1), np.int32)
+        seq_len = np.zeros(max(lines, 1), np.int64)
+        score = np.zeros(max(lines, 1), np.float32)
+        if lines:
+            _check(_lib.lib().ppocr_rh_decode(self._h, _ptr(a), _ptr(line_off), lines,
+                                              self.default_mode if mode is None else mode, _ptr(idx), _ptr(mp),
+                                              _ptr(seq), _ptr(seq_len), _ptr(score)))
+        seqs = [seq[line_off[b]:line_off[b] + seq_len[b]].copy() for b in range(lines)]
+        return {"idx": idx[:m], "maxprob": mp[:m], "seqs": seqs, "score": score[:lines]}
+
+
+def matmul_quantized_b(a, qw, bias=None, mode=MODE_BF16X2):
+    """matmul_quantized_b(a, qw, bias) (src/ops/matmul.rs:1204-1336) on the GPU."""
+    a = _f32(a)
+    if a.ndim < 1:
+        raise OcrError("MatMulQuantizedB", "Operand must have valid dimensions")
+    if a.shape[-1] != qw.cols:
+        raise OcrError("MatMulQuantizedB", f"Inner dimensions must match: {a.shape[-1]} != {qw.cols}")
+    if bias is not None and np.asarray(bias).size != qw.rows:
+        raise OcrError("MatMulQuantized", f"bias has {np.asarray(bias).size} elements but n is {qw.rows}")
+    head = RecHead(qw=qw, bias=bias)
+    try:
+        return head.logits(a, mode)
+    finally:
+        head.close()
+
+
+def matmul_transposed_b(a, b_t, bias=None, mode=MODE_BF16X3):
+    """matmul_transposed_b(a, b_t, bias) (src/ops/matmul.rs:514-897) on the GPU."""
+    a = _f32(a)
+    b_t = _f32(b_t)
+    if a.ndim < 1 or b_t.ndim != 2:
+        raise OcrError("MatMulTransposedB", "Operands must have valid dimensions")
+    if a.shape[-1] != b_t.shape[1]:
+        raise OcrError("MatMulTransposedB", f"Inner dimensions must match: {a.shape[-1]} != {b_t.shape[1]}")
+    if bias is not None and np.asarray(bias).size != b_t.shape[0]:
+        raise OcrError("MatMulTransposedB", f"bias has {np.asarray(bias).size} elements but n is {b_t.shape[0]}")
+    head = RecHead(w_t=b_t, bias=bias)
+    try:
+        return head.logits(a, mode)
+    finally:
+        head.close()
+
+
+def _norm_axis(ndim, axis):
+    ax = axis + ndim if axis < 0 else axis
+    if ax < 0 or ax >= ndim:
+        raise OcrError("Softmax", f"Axis {axis} out of bounds for ndim {ndim}")
+    return ax
+
+
+def softmax_inplace(x, axis=-1):
+    """softmax_inplace(x, axis) (src/ops/softmax.rs:199-285) over the last axis, on the GPU."""
+    if not isinstance(x, np.ndarray) or x.dtype != np.float32 or not x.flags.c_contiguous:
+        raise OcrError("Softmax", "softmax_inplace needs a C-contiguous float32 numpy array")
+    ax = _norm_axis(x.ndim, axis)
+    if ax != x.ndim - 1:
+        raise OcrError("Softmax", "only the last axis (the classifier axis) is offloaded")
+    if x.size == 0:
+        return
+    cols = x.shape[-1]
+    _check(_lib.lib().ppocr_softmax_rows(_ptr(x), x.size // cols, cols))
+
+
+def softmax(x, axis=-1):
+    """softmax(x, axis) (src/ops/softmax.rs:49-197): a new array."""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    _norm_axis(x.ndim, axis)
+    softmax_inplace(x, axis)
+    return x
+
+
+class CtcDecoder:
+    """CTC greedy decoder (src/postprocess/ctc.rs:7-175); argmax and collapse on the GPU."""
+
+    def __init__(self, vocab):
+        self.vocab = list(vocab)
+
+    @classmethod
+    def from_file(cls, dict_path):
+        """vocab = ["blank"] + dictionary lines + [" "] (src/postprocess/ctc.rs:12-30)."""
+        try:
+            with open(dict_path, "r", encoding="utf-8") as f:
+                lines = f.read().split("\n")
+        except OSError as e:
+            raise OcrError("ModelError", f"Failed to open dict file: {e}")
+        if lines and lines[-1] == "":
+            lines = lines[:-1]
+        vocab = ["blank"] + [ln.rstrip("\r\n") for ln in lines] + [" "]
+        return cls(vocab)
+
+    @classmethod
+    def from_vocab(cls, vocab):
+        return cls(vocab)
+
+    def vocab_size(self):
+        return len(self.vocab)
+
+    def _check_preds(self, preds):
+        preds = np.asarray(preds)
+        if preds.ndim != 3:
+            raise OcrError("CtcDecode", f"Expected 3D tensor [batch, time, vocab], got shape {list(preds.shape)}")
+        if preds.shape[2] != len(self.vocab):
+            raise OcrError("CtcDecode", f"dictionary/model mismatch: model outputs {preds.shape[2]} classes but the "
+                                        f"dictionary has {len(self.vocab)} entries")
+        return _f32(preds)
+
+    def decode(self, preds):
+        """First line of decode_batch; ("", 0.0) for an empty batch (src/postprocess/ctc.rs:40-100)."""
+        preds = self._check_preds(preds)
+        if preds.shape[0] == 0 or preds.shape[1] == 0:
+            return "", 0.0
+        return self.decode_batch(preds)[0]
+
+    def decode_batch(self, preds):
+        """[batch, time, vocab] probabilities -> [(text, score)] (src/postprocess/ctc.rs:103-175)."""
+        preds = self._check_preds(preds)
+        b, t, c = preds.shape
+        if b == 0 or t == 0:
+            return []
+        rows = b * t
+        idx = np.empty(rows, np.int32)
+        val = np.empty(rows, np.float32)
+        _check(_lib.lib().ppocr_argmax_rows(_ptr(preds), rows, c, _ptr(idx), _ptr(val)))
+        line_off = np.arange(0, rows + 1, t, dtype=np.int64)
+        return self.decode_steps(idx, val, line_off)
+
+    def decode_steps(self, idx, maxprob, line_off):
+        """Collapse per-step (argmax, max probability) of lines given by offsets into text."""
+        seqs, scores = self.collapse(idx, maxprob, line_off)
+        return [("".join(self.vocab[j] for j in s), float(sc)) for s, sc in zip(seqs, scores)]
+
+    @staticmethod
+    def collapse(idx, maxprob, line_off, blank=0):
+        idx = np.ascontiguousarray(idx, dtype=np.int32)
+        maxprob = _f32(maxprob)
+        line_off = np.ascontiguousarray(line_off, dtype=np.int64)
+        lines = line_off.size - 1
+        seq = np.zeros(max(idx.size, 1), np.int32)
+        seq_len = np.zeros(max(lines, 1), np.int64)
+        score = np.zeros(max(lines, 1), np.float32)
+        if lines > 0:
+            _check(_lib.lib().ppocr_ctc_greedy(_ptr(idx), _ptr(maxprob), _ptr(line_off), lines, blank, _ptr(seq),
+                                               _ptr(seq_len), _ptr(score)))
+        return [seq[line_off[b]:line_off[b] + seq_len[b]].copy() for b in range(lines)], score[:max(lines, 0)].copy()

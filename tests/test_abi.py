@@ -1,0 +1,112 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function the header
+declares, and reports argument errors (the OcrError::OperatorError convention) without
+touching a GPU."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "ppocr_rechead.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ppocr_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree(rh):
+    names = declared_functions()
+    assert len(names) >= 20
+    assert set(names) == set(rh._lib.SIGNATURES), set(names) ^ set(rh._lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(rh):
+    L = rh._lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_library_is_built_for_gfx950_only():
+    """The embedded offload bundle of this repository's own build names gfx950 and no
+    other GPU target."""
+    lib = os.path.join(ROOT, "rust-ppocrv6_amd", "lib", "libppocr_rechead.so")
+    blob = open(lib, "rb").read()
+    targets = set(re.findall(rb"amdgcn-amd-amdhsa-+(gfx[0-9a-f]+)", blob))
+    assert targets == {b"gfx950"}, targets
+
+
+def test_argument_errors_do_not_need_a_device(rh):
+    L = rh._lib.lib()
+    rc = L.ppocr_rh_pack_int8(None, -1, 120, None, None)
+    assert rc == rh.PPOCR_ERR_INVALID_ARG
+    assert rh._lib.last_error() == "QuantizedWeight: negative shape"
+    assert L.ppocr_rh_pack_int8(None, 0, 120, None, None) == rh.PPOCR_OK
+    h = ctypes.c_void_p(123)
+    assert L.ppocr_rh_create(None, None, None, 10, 8, 0, ctypes.byref(h)) == rh.PPOCR_ERR_INVALID_ARG
+    assert h.value is None
+    assert "MatMulQuantizedB" in rh._lib.last_error()
+    assert L.ppocr_ctc_greedy(None, None, None, -1, 0, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
+    assert L.ppocr_ctc_greedy(None, None, None, 0, 0, None, None, None) == rh.PPOCR_OK
+    off = np.array([0, 3, 2], np.int64)
+    rc = L.ppocr_ctc_greedy(None, None, off.ctypes.data_as(ctypes.c_void_p), 2, 0, None,
+                            np.zeros(2, np.int64).ctypes.data_as(ctypes.c_void_p),
+                            np.zeros(2, np.float32).ctypes.data_as(ctypes.c_void_p))
+    assert rc == rh.PPOCR_ERR_INVALID_ARG and "non-decreasing" in rh._lib.last_error()
+    assert L.ppocr_softmax_rows(None, 0, 5) == rh.PPOCR_OK  # empty input is not an error
+    assert L.ppocr_softmax_rows(None, -1, 5) == rh.PPOCR_ERR_INVALID_ARG
+    assert L.ppocr_rh_footprint_bytes(None) == 0
+    assert L.ppocr_rh_logits(None, None, 1, 2, None) == rh.PPOCR_ERR_INVALID_ARG
+    assert rh._lib.last_error() == "MatMulQuantizedB: null head handle"
+
+
+def test_python_mirror_errors_match_the_reference_messages(rh):
+    with pytest.raises(rh.OcrError) as e:
+        rh.softmax(np.zeros((2, 3), np.float32), 2)
+    assert str(e.value) == "Softmax: Axis 2 out of bounds for ndim 2"
+    with pytest.raises(rh.OcrError):
+        rh.softmax(np.zeros((2, 3), np.float32), -3)
+    dec = rh.CtcDecoder.from_vocab(["blank", "a", " "])
+    with pytest.raises(rh.OcrError) as e:
+        dec.decode(np.zeros((1, 2, 4), np.float32))
+    assert "mismatch" in str(e.value)
+    with pytest.raises(rh.OcrError):
+        dec.decode(np.zeros((2, 2), np.float32))
+    # an empty batch decodes to ("", 0.0) (decode_handles_empty_batch_gracefully)
+    assert dec.decode(np.zeros((0, 5, 3), np.float32)) == ("", 0.0)
+    qw = rh.QuantizedWeight(np.zeros((16, 8), np.int8), np.ones(16, np.float32))
+    for n_bias in (0, 1, 15, 17):
+        with pytest.raises(rh.OcrError):
+            rh.matmul_quantized_b(np.zeros((1, 8), np.float32), qw, np.zeros(n_bias, np.float32))
+    with pytest.raises(rh.OcrError) as e:
+        rh.matmul_quantized_b(np.zeros((2, 3), np.float32), qw)
+    assert "Inner dimensions must match: 3 != 8" in str(e.value)
+
+
+def test_dictionary_loading(rh, tmp_path):
+    p = tmp_path / "keys.txt"
+    p.write_text("a\nb\r\nc\n", encoding="utf-8")
+    dec = rh.CtcDecoder.from_file(str(p))
+    assert dec.vocab == ["blank", "a", "b", "c", " "]
+    ref_keys = "/root/reference/models/ppocrv6_keys.txt"
+    if os.path.exists(ref_keys):
+        assert rh.CtcDecoder.from_file(ref_keys).vocab_size() == 18710
+
+
+def test_workloads_are_deterministic():
+    from ppocr_rechead import workloads as wl
+    w1, b1 = wl.weights()
+    w2, b2 = wl.weights()
+    assert w1.shape == (18710, 120) and np.array_equal(w1, w2) and np.array_equal(b1, b2)
+    lines = wl.lines_for("a4_page")
+    assert len(lines) == 29 and all(20 <= t <= 120 for t in lines)
+    assert sum(wl.lines_for("dense_256")) == 30720
+    assert sum(wl.lines_for("stress_1024")) == 245760
+    ws, _ = wl.weights(stress=True)
+    zero_rows = np.nonzero(~ws.any(axis=1))[0]
+    assert zero_rows.size == 18710 // 200
+    assert (np.abs(ws) == 5.0).sum() == 18710 // 200

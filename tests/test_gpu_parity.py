@@ -1,0 +1,336 @@
+"""GPU parity: every HIP entry point against the CPU oracle on the same seeded inputs.
+
+Bars: packed q and scales bit-exact; logits and probabilities within max-abs 1e-4
+(BF16X2, BF16X3, FP32_FMA); argmax and CTC sequences identical except at top-2 logit gaps
+below 1e-4, which are printed; CTC collapse bit-exact on identical per-step inputs."""
+import os
+
+import numpy as np
+import pytest
+
+from gpu_common import check_argmax, f64_logits_q, split_lines, top2_gap
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def head(orc):
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    q, s = orc.pack_int8(w_t)
+    return {"w_t": w_t, "bias": bias, "q": q, "s": s}
+
+
+@pytest.fixture(scope="module")
+def rhead(rh, head):
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    yield h
+    h.close()
+
+
+def test_pack_bit_exact_synthetic_and_stress(orc, rh):
+    from ppocr_rechead import workloads as wl
+    for stress in (False, True):
+        w_t, _ = wl.weights(stress=stress)
+        print(f"pack 18710x120 stress={stress}", flush=True)
+        qw = rh.QuantizedWeight.from_f32_transposed(w_t)
+        q, s = orc.pack_int8(w_t)
+        assert np.array_equal(qw.data, q)
+        assert np.array_equal(qw.scales.view(np.uint32), s.view(np.uint32))
+
+
+def test_pack_bit_exact_golden_rows(rh):
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "pack_rows.npz"))
+    for key in ("small_rec", "tiny_rec", "special"):
+        print(f"pack golden {key}", flush=True)
+        qw = rh.QuantizedWeight.from_f32_transposed(g[f"{key}_w_t"])
+        assert np.array_equal(qw.data, g[f"{key}_q"]), key
+        assert np.array_equal(qw.scales.view(np.uint32), g[f"{key}_scales"].view(np.uint32)), key
+
+
+def test_pack_edge_shapes(orc, rh):
+    rng = np.random.default_rng(5)
+    for n, k in ((1, 1), (3, 7), (5, 64), (2, 65), (7, 300)):
+        w = rng.standard_normal((n, k), dtype=np.float32)
+        w[0, 0] = np.nan
+        print(f"pack n={n} k={k}", flush=True)
+        qw = rh.QuantizedWeight.from_f32_transposed(w)
+        q, s = orc.pack_int8(w)
+        assert np.array_equal(qw.data, q) and np.array_equal(qw.scales.view(np.uint32), s.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("m", [1, 33, 120, 257])
+def test_int8_logits(orc, rh, head, rhead, mode, m):
+    rng = np.random.default_rng(100 + m)
+    a = rng.standard_normal((m, 120), dtype=np.float32)
+    print(f"int8 logits mode={mode} m={m}", flush=True)
+    got = rhead.logits(a, mode)
+    ref = orc.matmul_quantized_b(a, head["q"], head["s"], head["bias"], partition_threads=1)
+    err = np.abs(got - ref).max()
+    print(f"  max|gpu-oracle| = {err:.3e}")
+    assert got.shape == (m, 18710)
+    if mode == 1:
+        assert err < 2e-2  # a single bf16 term keeps ~8 bits of the activation
+    else:
+        assert err < TOL
+
+
+def test_int8_logits_no_bias_small_n(orc, rh):
+    rng = np.random.default_rng(7)
+    for n, k in ((100, 120), (1000, 120), (33, 117), (64, 80), (6906, 80)):
+        w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+        q, s = orc.pack_int8(w)
+        a = rng.standard_normal((70, k), dtype=np.float32)
+        head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=None)
+        for mode in (0, 2, 3):
+            print(f"int8 logits n={n} k={k} mode={mode} no bias", flush=True)
+            got = head.logits(a, mode)
+            ref = orc.matmul_quantized_b(a, q, s, None)
+            assert np.abs(got - ref).max() < TOL, (n, k, mode)
+        head.close()
+
+
+def test_tiny_head_real_rows(orc, rh):
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "pack_rows.npz"))
+    q, s = g["tiny_rec_q"], g["tiny_rec_scales"]
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((50, 80), dtype=np.float32)
+    bias = (rng.standard_normal(q.shape[0], dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    for mode in (0, 2, 3):
+        print(f"tiny real rows mode={mode}", flush=True)
+        got = head.logits(a, mode)
+        assert np.abs(got - orc.matmul_quantized_b(a, q, s, bias)).max() < TOL
+    head.close()
+
+
+@pytest.mark.parametrize("mode", [0, 1, 3])
+def test_fp32_head_logits(orc, rh, mode):
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal((300, 120), dtype=np.float32)
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    print(f"fp32 head mode={mode}", flush=True)
+    got = head.logits(a, mode)
+    ref = orc.matmul_transposed_b(a, w_t, bias, partition_threads=1)
+    err = np.abs(got - ref).max()
+    print(f"  max|gpu-oracle| = {err:.3e}")
+    assert err < (2e-2 if mode == 1 else TOL)
+    head.close()
+
+
+def test_fp32_head_rejects_bf16x2(rh):
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights(n=64)
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    with pytest.raises(rh.OcrError):
+        head.logits(np.zeros((2, 120), np.float32), 2)
+    head.close()
+
+
+def test_softmax_matches_oracle(orc, rh):
+    rng = np.random.default_rng(10)
+    for rows, cols in ((5, 18710), (3, 40), (2, 2049), (2, 30000), (1, 1), (4, 7)):
+        x = (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+        print(f"softmax {rows}x{cols}", flush=True)
+        got = x.copy()
+        rh.softmax_inplace(got)
+        ref = orc.softmax_rows(x)
+        assert np.abs(got - ref).max() < 1e-6
+    big = np.array([[1000, 1001, 999, 1000.5], [-1000, -999, -1001, -1000.5]], np.float32)
+    rh.softmax_inplace(big)
+    assert np.all(np.isfinite(big)) and np.all(np.abs(big.sum(axis=1) - 1) < 1e-5)
+    empty = np.zeros((3, 0), np.float32)
+    rh.softmax_inplace(empty)
+
+
+def test_softmax_dev_emits_argmax_of_probs(orc, rh, head):
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((64, 120), dtype=np.float32)
+    logits = orc.matmul_quantized_b(a, head["q"], head["s"], head["bias"])
+    d = DeviceArray.from_numpy(logits)
+    di = DeviceArray((64,), np.int32)
+    dp = DeviceArray((64,), np.float32)
+    L = rh._lib.lib()
+    print("softmax_dev + argmax", flush=True)
+    assert L.ppocr_softmax_rows_dev(d.p, 64, 18710, di.p, dp.p, None) == 0
+    synchronize()
+    probs = orc.softmax_rows(logits)
+    idx, val = orc.argmax_rows(probs)
+    gap = top2_gap(f64_logits_q(a, head["q"], head["s"], head["bias"]))
+    check_argmax(di.numpy(), idx, gap, label="softmax argmax")
+    assert np.abs(dp.numpy() - val).max() < 1e-6
+    assert np.abs(d.numpy() - probs).max() < 1e-6
+
+
+def test_argmax_rows_first_occurrence(orc, rh):
+    rng = np.random.default_rng(12)
+    x = rng.integers(0, 40, (300, 1000)).astype(np.float32)
+    x[5] = np.nan
+    x[6, :] = np.nan
+    x[6, 500] = 3.0
+    print("argmax rows", flush=True)
+    idx = np.empty(300, np.int32)
+    val = np.empty(300, np.float32)
+    rh._check(rh._lib.lib().ppocr_argmax_rows(rh._ptr(x), 300, 1000, rh._ptr(idx), rh._ptr(val)))
+    ridx, rval = orc.argmax_rows(x)
+    assert np.array_equal(idx, ridx)
+    assert np.array_equal(val, rval)
+    assert idx[5] == 0 and val[5] == -np.inf and idx[6] == 500
+
+
+def test_ctc_collapse_matches_oracle(orc, rh):
+    rng = np.random.default_rng(13)
+    lengths = [0, 1, 2, 63, 64, 65, 127, 128, 129, 240, 0, 17, 500]
+    off = np.zeros(len(lengths) + 1, np.int64)
+    off[1:] = np.cumsum(lengths)
+    steps = int(off[-1])
+    idx = rng.integers(0, 4, steps).astype(np.int32)  # many blanks and repeats
+    mask = rng.random(steps) < 0.3
+    idx[mask] = rng.integers(0, 18710, int(mask.sum())).astype(np.int32)
+    val = rng.random(steps).astype(np.float32)
+    print("ctc collapse", flush=True)
+    seqs, score = rh.CtcDecoder.collapse(idx, val, off)
+    rseqs, rscore = orc.ctc_collapse(idx, val, off)
+    assert all(np.array_equal(x, y) for x, y in zip(seqs, rseqs))
+    assert np.array_equal(score.view(np.uint32), rscore.view(np.uint32))
+    # the reference's known answers
+    dec = rh.CtcDecoder.from_vocab(["blank", "a", "b", " "])
+    t = np.zeros((1, 4, 4), np.float32)
+    for tt, c in ((0, 1), (1, 1), (2, 0), (3, 2)):
+        t[0, tt, c] = 1.0
+    text, sc = dec.decode(t)
+    assert text == "ab" and abs(sc - 1.0) < 1e-6
+    d = np.zeros((2, 2, 4), np.float32)
+    d[0, 0, 1] = d[0, 1, 2] = d[1, 0, 2] = d[1, 1, 0] = 1.0
+    assert [x[0] for x in dec.decode_batch(d)] == ["ab", "b"]
+
+
+@pytest.mark.parametrize("mode", [0, 2, 3])
+def test_fused_argmax_a4_page(orc, rh, head, rhead, mode):
+    from ppocr_rechead import workloads as wl
+    a = wl.activations("a4_page")
+    print(f"fused argmax a4_page mode={mode} m={a.shape[0]}", flush=True)
+    idx, mp = rhead.argmax(a, mode)
+    ref = orc.rechead_lines(a, wl.line_offsets(wl.lines_for("a4_page")), head["q"], head["s"], head["bias"])
+    gap = top2_gap(f64_logits_q(a, head["q"], head["s"], head["bias"]))
+    check_argmax(idx, ref["idx"], gap, label=f"a4_page mode {mode}")
+    err = np.abs(mp - ref["maxprob"]).max()
+    print(f"  max|maxprob gpu-oracle| = {err:.3e}")
+    assert err < TOL
+
+
+@pytest.mark.parametrize("mode", [0, 2, 3])
+def test_fused_probs_single_line(orc, rh, head, rhead, mode):
+    from ppocr_rechead import workloads as wl
+    a = wl.activations("single_line")
+    print(f"fused probs single_line mode={mode}", flush=True)
+    got = rhead.probs(a, mode)
+    ref = orc.rechead_lines(a, np.array([0, 120], np.int64), head["q"], head["s"], head["bias"], want_probs=True)
+    err = np.abs(got - ref["probs"]).max()
+    print(f"  max|probs gpu-oracle| = {err:.3e}")
+    assert err < TOL
+
+
+def test_decode_a4_page_end_to_end(orc, rh, head, rhead):
+    from ppocr_rechead import workloads as wl
+    a = wl.activations("a4_page")
+    off = wl.line_offsets(wl.lines_for("a4_page"))
+    print("decode a4_page", flush=True)
+    got = rhead.decode(a, off)
+    ref = orc.rechead_lines(a, off, head["q"], head["s"], head["bias"])
+    gap = top2_gap(f64_logits_q(a, head["q"], head["s"], head["bias"]))
+    exempt = set(check_argmax(got["idx"], ref["idx"], gap, label="decode a4_page").tolist())
+    for b in range(len(off) - 1):
+        if not any(off[b] <= r < off[b + 1] for r in exempt):
+            assert np.array_equal(got["seqs"][b], ref["seqs"][b]), b
+            assert abs(got["score"][b] - ref["score"][b]) < TOL
+
+
+def test_decode_dev_matches_unfused_path(orc, rh, head, rhead):
+    """MatMul.12 -> softmax_inplace -> argmax (three launches, logits through HBM) and the
+    fused head agree on the dense 256-line batch (m = 30720), row by row."""
+    from ppocr_rechead import workloads as wl
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    a = wl.activations("dense_256")
+    m = a.shape[0]
+    L = rh._lib.lib()
+    da = DeviceArray.from_numpy(a)
+    dl = DeviceArray((m, 18710), np.float32)
+    di1, dp1 = DeviceArray((m,), np.int32), DeviceArray((m,), np.float32)
+    di2, dp2 = DeviceArray((m,), np.int32), DeviceArray((m,), np.float32)
+    print("dense_256 unfused vs fused", flush=True)
+    rh._check(L.ppocr_rh_logits_dev(rhead.handle, da.p, m, 2, dl.p, None, 0, None))
+    rh._check(L.ppocr_softmax_rows_dev(dl.p, m, 18710, di1.p, dp1.p, None))
+    rh._check(L.ppocr_rh_argmax_dev(rhead.handle, da.p, m, 2, di2.p, dp2.p, None, 0, None))
+    synchronize()
+    i1, p1, i2, p2 = di1.numpy(), dp1.numpy(), di2.numpy(), dp2.numpy()
+    sample = np.random.default_rng(14).choice(m, 1024, replace=False)
+    gap_s = top2_gap(f64_logits_q(a[sample], head["q"], head["s"], head["bias"]))
+    diff = np.nonzero(i1 != i2)[0]
+    print(f"  fused/unfused argmax differences: {diff.size}; max|maxprob diff| {np.abs(p1 - p2).max():.3e}")
+    assert diff.size <= 5
+    assert np.abs(p1 - p2).max() < 1e-5
+    ref = orc.rechead_lines(a[sample], split_lines(sample.size), head["q"], head["s"], head["bias"])
+    check_argmax(i2[sample], ref["idx"], gap_s, label="dense_256 fused sample")
+    check_argmax(i1[sample], ref["idx"], gap_s, label="dense_256 unfused sample")
+    assert np.abs(p2[sample] - ref["maxprob"]).max() < TOL
+    probs_rows = dl.numpy()[sample[:64]]
+    ref_p = orc.rechead_lines(a[sample[:64]], np.array([0, 64], np.int64), head["q"], head["s"], head["bias"],
+                              want_probs=True)["probs"]
+    assert np.abs(probs_rows - ref_p).max() < TOL
+
+
+def test_stress_1024_fused(orc, rh):
+    """m = 245760, zero-weight rows, +-5 outliers, 1% rows x50, 2% near-tie rows."""
+    from ppocr_rechead import workloads as wl
+    print("stress_1024 build", flush=True)
+    wk = wl.make("stress_1024", pack=orc.pack_int8)
+    a, q, s, bias = wk["a"], wk["q"], wk["scales"], wk["bias"]
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    print("stress_1024 fused argmax", flush=True)
+    got = head.decode(a, wk["line_off"])
+    head.close()
+    m = a.shape[0]
+    assert got["idx"].min() >= 0 and got["idx"].max() < 18710
+    assert np.all((got["maxprob"] > 0) & (got["maxprob"] <= 1))
+    rng = np.random.default_rng(15)
+    sample = np.unique(np.concatenate([wk["scaled_rows"], wk["tie_rows"], rng.choice(m, 2000, replace=False)]))
+    ref = orc.rechead_lines(a[sample], split_lines(sample.size), q, s, bias)
+    gap = top2_gap(f64_logits_q(a[sample], q, s, bias))
+    exempt = check_argmax(got["idx"][sample], ref["idx"], gap, label="stress sample")
+    print(f"  near-tie rows built: {wk['tie_rows'].size}, exempt differences: {exempt.size}")
+    err = np.abs(got["maxprob"][sample] - ref["maxprob"])
+    scaled = np.isin(sample, wk["scaled_rows"])
+    print(f"  max|maxprob diff|: x50 rows {err[scaled].max():.3e}, other rows {err[~scaled].max():.3e}")
+    assert err.max() < TOL
+
+
+def test_precision_guard_on_large_activations(orc, rh):
+    """BF16X2 recomputes rows whose max|a| * max|w| exceeds the guard with three terms:
+    x50 rows against the stress weights (+-5 outliers) stay as accurate as BF16X3."""
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights(stress=True)
+    q, s = orc.pack_int8(w_t)
+    rng = np.random.default_rng(16)
+    a = rng.standard_normal((300, 120), dtype=np.float32)
+    big = rng.choice(300, 40, replace=False)
+    a[big] *= np.float32(50.0)
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    print("guard logits x2 vs x3 vs oracle", flush=True)
+    x2 = head.logits(a, 2)
+    x3 = head.logits(a, 3)
+    ref = orc.matmul_quantized_b(a, q, s, bias)
+    tol = 1e-4 + 1e-5 * np.abs(ref)  # f32 rounding of |logits| ~ 1e3 alone is ~1e-4
+    print(f"  max rel err x2 {np.max(np.abs(x2 - ref) / tol):.3f}, x3 {np.max(np.abs(x3 - ref) / tol):.3f}")
+    assert np.all(np.abs(x2 - ref) <= tol)
+    assert np.all(np.abs(x3 - ref) <= tol)
+    idx, mp = head.argmax(a, 2)
+    r = orc.rechead_lines(a, np.array([0, 300], np.int64), q, s, bias)
+    assert np.abs(mp - r["maxprob"]).max() < TOL
+    head.close()
