@@ -182,28 +182,28 @@ __device__ __forceinline__ void guard_append(float amax, float amax_limit, bool 
 // Global -> registers -> LDS staging of one tile record by 256 threads (16-byte chunks).
 // Every register is loaded unconditionally (indices clamped in bounds) so the staging
 // stays in registers and the load latency hides behind the MFMAs of the current tile.
-template <int REC>
+template <int REC, int NT = 256>
 struct Stage {
     static constexpr int CH = REC / 16;
-    static constexpr int PER = (CH + 255) / 256;
+    static constexpr int PER = (CH + NT - 1) / NT;
     static_assert(PER >= 1 && PER <= 4, "tile record too large");
     u32x4 v0, v1, v2, v3;
     __device__ __forceinline__ void load(const uint8_t* __restrict__ src, int tid) {
         const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
         v0 = s4[min(tid, CH - 1)];
-        if constexpr (PER > 1) v1 = s4[min(tid + 256, CH - 1)];
-        if constexpr (PER > 2) v2 = s4[min(tid + 512, CH - 1)];
-        if constexpr (PER > 3) v3 = s4[min(tid + 768, CH - 1)];
+        if constexpr (PER > 1) v1 = s4[min(tid + NT, CH - 1)];
+        if constexpr (PER > 2) v2 = s4[min(tid + 2 * NT, CH - 1)];
+        if constexpr (PER > 3) v3 = s4[min(tid + 3 * NT, CH - 1)];
     }
     __device__ __forceinline__ void store(uint8_t* dst, int tid) const {
         u32x4* d4 = reinterpret_cast<u32x4*>(dst);
-        if (CH >= 256 || tid < CH) d4[tid] = v0;
+        if (CH >= NT || tid < CH) d4[tid] = v0;
         if constexpr (PER > 1)
-            if (CH >= 512 || tid + 256 < CH) d4[tid + 256] = v1;
+            if (CH >= 2 * NT || tid + NT < CH) d4[tid + NT] = v1;
         if constexpr (PER > 2)
-            if (CH >= 768 || tid + 512 < CH) d4[tid + 512] = v2;
+            if (CH >= 3 * NT || tid + 2 * NT < CH) d4[tid + 2 * NT] = v2;
         if constexpr (PER > 3)
-            if (CH >= 1024 || tid + 768 < CH) d4[tid + 768] = v3;
+            if (CH >= 4 * NT || tid + 3 * NT < CH) d4[tid + 3 * NT] = v3;
     }
 };
 
@@ -325,45 +325,67 @@ __global__ __launch_bounds__(256, 2) void rows_mfma_kernel(
 // one fma with the record's scale*log2(e) and bias*log2(e).  The sum is kept relative to
 // `ref`, which stays 0 unless the row's maximum leaves [-64, 64]; then it follows the
 // maximum so the sum can neither overflow nor lose the maximum's term.
-__device__ __forceinline__ void stats_update(const f32x16& acc, const float* sl, const float* bl, int nrow0,
-                                             float& best, float& sum, float& ref, int& bidx, bool& refzero) {
-    float t[16];
+template <int MB>
+__device__ __forceinline__ void stats_update(const f32x16 (&acc)[MB], const float* sl, const float* bl, int nrow0,
+                                             float (&best)[MB], float (&sum)[MB], float (&ref)[MB],
+                                             int (&bidx)[MB], bool& refzero) {
+    float t[MB][16], tmax[MB];
+    bool better[MB];
+    bool anyb = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) t[r] = fmaf(acc[r], sl[r], bl[r]);
-    const float m01 = fmaxf(fmaxf(t[0], t[1]), t[2]);
-    const float m02 = fmaxf(fmaxf(t[3], t[4]), t[5]);
-    const float m03 = fmaxf(fmaxf(t[6], t[7]), t[8]);
-    const float m04 = fmaxf(fmaxf(t[9], t[10]), t[11]);
-    const float m05 = fmaxf(fmaxf(t[12], t[13]), t[14]);
-    const float tmax = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[15]));
-    const bool better = tmax > best;
-    if (__any(better)) {
-        if (better) {
-            int ri = 15;
+    for (int b = 0; b < MB; ++b) {
 #pragma unroll
-            for (int r = 14; r >= 0; --r) ri = (t[r] == tmax) ? r : ri;
-            best = tmax;
-            bidx = nrow0 + 8 * (ri >> 2) + (ri & 3);
-            if (best > ref + 64.0f || best < ref - 64.0f) {
-                sum = (sum == 0.0f) ? 0.0f : sum * __builtin_amdgcn_exp2f(ref - best);
-                ref = best;
-            }
-        }
-        refzero = refzero && !__any(ref != 0.0f);
+        for (int r = 0; r < 16; ++r) t[b][r] = fmaf(acc[b][r], sl[r], bl[r]);
+        const float m01 = fmaxf(fmaxf(t[b][0], t[b][1]), t[b][2]);
+        const float m02 = fmaxf(fmaxf(t[b][3], t[b][4]), t[b][5]);
+        const float m03 = fmaxf(fmaxf(t[b][6], t[b][7]), t[b][8]);
+        const float m04 = fmaxf(fmaxf(t[b][9], t[b][10]), t[b][11]);
+        const float m05 = fmaxf(fmaxf(t[b][12], t[b][13]), t[b][14]);
+        tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
+        better[b] = tmax[b] > best[b];
+        anyb = anyb || better[b];
     }
-    float e[16];
+    // Rare path (one uniform branch for all blocks): a new maximum.  Record its first
+    // index, and keep ref within 64 of the maximum.
+    if (__any(anyb)) {
+        bool shifted = false;
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            if (better[b]) {
+                int ri = 15;
+#pragma unroll
+                for (int r = 14; r >= 0; --r) ri = (t[b][r] == tmax[b]) ? r : ri;
+                best[b] = tmax[b];
+                bidx[b] = nrow0 + 8 * (ri >> 2) + (ri & 3);
+                if (best[b] > ref[b] + 64.0f || best[b] < ref[b] - 64.0f) {
+                    sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - best[b]);
+                    ref[b] = best[b];
+                }
+            }
+            shifted = shifted || ref[b] != 0.0f;
+        }
+        refzero = refzero && !__any(shifted);
+    }
+    float e[MB][16];
     if (refzero) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t[r]);
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) e[b][r] = __builtin_amdgcn_exp2f(t[b][r]);
     } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t[r] - ref);
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) e[b][r] = __builtin_amdgcn_exp2f(t[b][r] - ref[b]);
     }
 #pragma unroll
-    for (int r = 0; r < 8; ++r) e[r] += e[r + 8];
+    for (int b = 0; b < MB; ++b) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) e[r] += e[r + 4];
-    sum += (e[0] + e[2]) + (e[1] + e[3]);
+        for (int r = 0; r < 8; ++r) e[b][r] += e[b][r + 8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e[b][r] += e[b][r + 4];
+        sum[b] += (e[b][0] + e[b][2]) + (e[b][1] + e[b][3]);
+    }
 }
 
 // Fused projection + softmax statistics.  Each workgroup: 4 waves x MB blocks of 32
@@ -449,9 +471,7 @@ __global__ __launch_bounds__(256, 2) void stats_mfma_kernel(
                         bl[4 * q + e] = b4[e];
                     }
                 }
-#pragma unroll
-                for (int b = 0; b < MB; ++b)
-                    stats_update(acc[b], sl, bl, t * 32 + 4 * h, best[b], sum[b], ref[b], bidx[b], refzero);
+                stats_update<MB>(acc, sl, bl, t * 32 + 4 * h, best, sum, ref, bidx, refzero);
                 if (more) stg.store(lds + (cur ^ 1) * GE::BUF, tid);
                 __syncthreads();
             }
@@ -473,6 +493,305 @@ __global__ __launch_bounds__(256, 2) void stats_mfma_kernel(
     }
 }
 
+// Epilogue of one tile, common path: t = logit * log2(e), the tile maximum, and the
+// tile's sum of exp2(t - ref).  Branch-free, so the compiler can interleave it with the
+// next tile's MFMAs.
+template <int MB>
+__device__ __forceinline__ void epi_common(f32x16 (&acc)[MB], const float* __restrict__ ep, int h,
+                                           const float (&ref)[MB], float (&tmax)[MB], float (&tsum)[MB]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const f32x4 s4 = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[b][4 * q + e] = fmaf(acc[b][4 * q + e], s4[e], b4[e]);
+    }
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        const f32x16& t = acc[b];
+        const float m01 = fmaxf(fmaxf(t[0], t[1]), t[2]);
+        const float m02 = fmaxf(fmaxf(t[3], t[4]), t[5]);
+        const float m03 = fmaxf(fmaxf(t[6], t[7]), t[8]);
+        const float m04 = fmaxf(fmaxf(t[9], t[10]), t[11]);
+        const float m05 = fmaxf(fmaxf(t[12], t[13]), t[14]);
+        tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[15]));
+        float e[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t[r] - ref[b]);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) e[r] += e[r + 8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e[r] += e[r + 4];
+        tsum[b] = (e[0] + e[2]) + (e[1] + e[3]);
+    }
+}
+
+// Epilogue of one tile, rare path: a lane whose tile maximum beats its running maximum
+// records the first index of it; a maximum more than 64 above ref moves ref to it (the
+// tile's sum is recomputed, since exp2(t - old ref) may have overflowed).
+template <int MB>
+__device__ __forceinline__ void epi_rare(const f32x16 (&t)[MB], int nrow0, const float (&tmax)[MB],
+                                         float (&tsum)[MB], float (&best)[MB], float (&sum)[MB], float (&ref)[MB],
+                                         int (&bidx)[MB]) {
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        if (tmax[b] > best[b]) {
+            int ri = 15;
+#pragma unroll
+            for (int r = 14; r >= 0; --r) ri = (t[b][r] == tmax[b]) ? r : ri;
+            best[b] = tmax[b];
+            bidx[b] = nrow0 + 8 * (ri >> 2) + (ri & 3);
+            if (best[b] > ref[b] + 64.0f || best[b] < ref[b] - 64.0f) {
+                const float nr = best[b];
+                sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - nr);
+                float s = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(t[b][r] - nr);
+                tsum[b] = s;
+                ref[b] = nr;
+            }
+        }
+    }
+}
+
+// Software-pipelined fused projection + softmax statistics (main pass).  Each wave
+// issues the MFMAs of tile j+1 (into the second accumulator set) in the same
+// instruction stream as the epilogue of tile j, so the matrix core and the vector ALU
+// of a SIMD work at the same time within one wave, and two waves per SIMD keep both
+// busy.  Weight tiles go through a 3-deep LDS ring (tile j: epilogue constants, tile
+// j+1: MFMA fragments, tile j+2: being staged), one barrier per tile.
+template <int C, int G, int MB>
+__global__ __launch_bounds__(256, 2) void stats_sw_kernel(
+    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
+    int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
+    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows) {
+    using GE = Geo<C, G>;
+    constexpr int RPB = 128 * MB;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    int mbi, chunk;
+    map_block(blockIdx.x, nsplit, &mbi, &chunk);
+    if (mbi >= mblocks) return;
+    const int t0 = chunk * tiles_per_chunk;
+    const int t1 = min(t0 + tiles_per_chunk, tiles);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
+    const int64_t mrow0 = (int64_t)mbi * RPB + wave * (32 * MB);
+    if (tid < 96) reinterpret_cast<u32x4*>(lds + (tid >> 5) * GE::BUF + GE::REC)[tid & 31] = u32x4{0, 0, 0, 0};
+    const int lb = i * 16 + h * 512;
+
+    int64_t arow[MB];
+    bool valid[MB];
+    bf16x8 bf[MB][GE::S];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        arow[b] = mrow0 + 32 * b + i;
+        valid[b] = arow[b] < m;
+        float amax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < GE::S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
+        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
+    }
+
+    float best[MB], sum[MB], ref[MB];
+    int bidx[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        best[b] = -INFINITY;
+        sum[b] = 0.0f;
+        ref[b] = 0.0f;
+        bidx[b] = 0;
+    }
+
+    if (t0 < t1) {
+        Stage<GE::REC> stg;
+        stg.load(rec + (size_t)t0 * GE::REC, tid);
+        stg.store(lds, tid);
+        stg.load(rec + (size_t)min(t0 + 1, t1 - 1) * GE::REC, tid);
+        stg.store(lds + GE::BUF, tid);
+        __syncthreads();
+        f32x16 acc_a[MB], acc_b[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
+#pragma unroll
+        for (int s = 0; s < GE::S; ++s) {
+            const bf16x8 wf = weight_frag<C, G>(lds, s, lb, i * 16, h);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc_a[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc_a[b], 0, 0, 0);
+        }
+        // One tile: stage tile j+2, MFMAs of tile j+1 into accM interleaved with the
+        // epilogue of tile j on accE, then the rare path, then the barrier.  Past the end the
+        // MFMAs read a stale ring slot and the load repeats the last tile: harmless, and it
+        // keeps the body one basic block.
+        auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
+            const int rel = j - t0;
+            const int cur = rel % 3, nxt = (rel + 1) % 3, nn = (rel + 2) % 3;
+            stg.load(rec + (size_t)min(j + 2, t1 - 1) * GE::REC, tid);
+            const uint8_t* bufn = lds + nxt * GE::BUF;
+#pragma unroll
+            for (int b = 0; b < MB; ++b) accM[b] = f32x16{};
+#pragma unroll
+            for (int s = 0; s < GE::S; ++s) {
+                const bf16x8 wf = weight_frag<C, G>(bufn, s, lb, i * 16, h);
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                    accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], accM[b], 0, 0, 0);
+            }
+            float tmax[MB], tsum[MB];
+            epi_common<MB>(accE, reinterpret_cast<const float*>(lds + cur * GE::BUF + GE::FRAG), h, ref, tmax, tsum);
+            // interleave: per MFMA one DS read and a few VALU ops of the epilogue
+#pragma unroll
+            for (int x = 0; x < GE::S * MB; ++x) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
+            bool anyb = false;
+#pragma unroll
+            for (int b = 0; b < MB; ++b) anyb = anyb || tmax[b] > best[b];
+            if (__any(anyb)) epi_rare<MB>(accE, j * 32 + 4 * h, tmax, tsum, best, sum, ref, bidx);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) sum[b] += tsum[b];
+            stg.store(lds + nn * GE::BUF, tid);
+            __syncthreads();
+        };
+        int j = t0;
+        for (; j + 1 < t1; j += 2) {
+            step(j, acc_a, acc_b);
+            step(j + 1, acc_b, acc_a);
+        }
+        if (j < t1) step(j, acc_a, acc_b);
+    }
+
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        RowStat mine{best[b], sum[b], ref[b], bidx[b]};
+        RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
+                      __shfl_xor(bidx[b], 32, 64)};
+        const RowStat r = stat_merge(mine, other);
+        if (h == 0 && valid[b]) {
+            p_best[(int64_t)chunk * m + arow[b]] = r.best;
+            p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
+            p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
+        }
+    }
+}
+
+// Ping-pong variant of the fused projection + softmax statistics (main pass).  A
+// workgroup of 8 waves: waves w and w+4 share a SIMD (the dispatcher places the waves of
+// a workgroup round-robin over the 4 SIMDs), so group A = waves 0-3 and group B = waves
+// 4-7 alternate: in every half-step one group runs the MFMAs of a tile while the other
+// runs the softmax/argmax epilogue of its previous tile, and the matrix cores and the
+// vector ALUs of each SIMD work at the same time.  Weight tiles are shared by both groups
+// through a 2-deep LDS ring; one barrier per half-step.
+//   half-step 2j:   A  MFMA(tile j)      B  epilogue(tile j-1)
+//   half-step 2j+1: A  epilogue(tile j)  B  MFMA(tile j)
+template <int C, int G, int MB>
+__global__ __launch_bounds__(512, 2) void stats_pp_kernel(
+    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
+    int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
+    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows) {
+    using GE = Geo<C, G>;
+    constexpr int RPB = 256 * MB;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    int mbi, chunk;
+    map_block(blockIdx.x, nsplit, &mbi, &chunk);
+    if (mbi >= mblocks) return;
+    const int t0 = chunk * tiles_per_chunk;
+    const int T = max(min(t0 + tiles_per_chunk, tiles) - t0, 0);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2, i = lane & 31, h = lane >> 5;
+    const int64_t mrow0 = (int64_t)mbi * RPB + wave * (32 * MB);
+    zero_blocks(lds, GE::BUF, GE::REC, tid);
+    const int lb = i * 16 + h * 512;
+
+    int64_t arow[MB];
+    bool valid[MB];
+    bf16x8 bf[MB][GE::S];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        arow[b] = mrow0 + 32 * b + i;
+        valid[b] = arow[b] < m;
+        float amax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < GE::S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
+        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
+    }
+
+    float best[MB], sum[MB], ref[MB];
+    int bidx[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        best[b] = -INFINITY;
+        sum[b] = 0.0f;
+        ref[b] = 0.0f;
+        bidx[b] = 0;
+    }
+    bool refzero = true;
+
+    if (T > 0) {
+        Stage<GE::REC, 512> stg;
+        stg.load(rec + (size_t)t0 * GE::REC, tid);
+        stg.store(lds, tid);
+        __syncthreads();
+        f32x16 acc[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[b] = f32x16{};
+        for (int hs = 0; hs <= 2 * T; ++hs) {
+            const int tt = hs >> 1;
+            const bool odd = hs & 1;
+            if (!odd && tt + 1 < T) stg.load(rec + (size_t)(t0 + tt + 1) * GE::REC, tid);
+            const bool do_mfma = grp == 0 ? (!odd && tt < T) : odd;
+            const bool do_epi = grp == 0 ? odd : (!odd && hs >= 2);
+            if (do_mfma) {
+                const uint8_t* buf = lds + (tt & 1) * GE::BUF;
+#pragma unroll
+                for (int b = 0; b < MB; ++b) acc[b] = f32x16{};
+#pragma unroll
+                for (int s = 0; s < GE::S; ++s) {
+                    const bf16x8 wf = weight_frag<C, G>(buf, s, lb, i * 16, h);
+#pragma unroll
+                    for (int b = 0; b < MB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc[b], 0, 0, 0);
+                }
+            } else if (do_epi) {
+                const int te = grp == 0 ? tt : tt - 1;
+                const float* ep = reinterpret_cast<const float*>(lds + (te & 1) * GE::BUF + GE::FRAG);
+                float sl[16], bl[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
+                    const f32x4 b4 = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sl[4 * q + e] = s4[e];
+                        bl[4 * q + e] = b4[e];
+                    }
+                }
+                stats_update<MB>(acc, sl, bl, (t0 + te) * 32 + 4 * h, best, sum, ref, bidx, refzero);
+            }
+            if (odd && tt + 1 < T) stg.store(lds + ((tt + 1) & 1) * GE::BUF, tid);
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        RowStat mine{best[b], sum[b], ref[b], bidx[b]};
+        RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
+                      __shfl_xor(bidx[b], 32, 64)};
+        const RowStat r = stat_merge(mine, other);
+        if (h == 0 && valid[b]) {
+            p_best[(int64_t)chunk * m + arow[b]] = r.best;
+            p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
+            p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
+        }
+    }
+}
+
 __global__ void guard_reset_kernel(int* guard_count) { *guard_count = 0; }
 
 // ============================================================ launchers
@@ -481,6 +800,7 @@ static constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1) ? 2 : 1;
 }
 
+// Rows per workgroup of the main statistics pass and of the rescue pass (4 waves).
 int stats_rows_per_block_mfma(int cfg) {
     switch (cfg) {
         case CFG_Q1: return 128 * mb_of<CFG_Q1>();
@@ -490,6 +810,7 @@ int stats_rows_per_block_mfma(int cfg) {
         default: return 128 * mb_of<CFG_F3>();
     }
 }
+static int rescue_rows_per_block(int cfg) { return 128 * (cfg == CFG_Q3 || cfg == CFG_F3 ? 1 : 2); }
 
 // Vocabulary chunks per row block: at least 8 (one slice of the weights per XCD L2), more
 // when there are too few row blocks to give every CU two workgroups.
@@ -612,16 +933,15 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
         constexpr int LDS = 2 * Geo<C, G>::BUF;
-        stats_mfma_kernel<C, G, mb_of<C>()><<<grid, 256, LDS, st>>>(
+        stats_sw_kernel<C, G, mb_of<C>()><<<grid, 256, 3 * Geo<C, G>::BUF, st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
-            guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
-            nullptr, nullptr);
+            guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
     if (e || !guarded) return e;
     // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
-    const int rrpb = stats_rows_per_block_mfma(rcfg);
+    const int rrpb = rescue_rows_per_block(rcfg);
     const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, 64);
     const int rgrid = grid_blocks(slots, nsplit);
     return dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
