@@ -297,15 +297,14 @@ int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* 
     float* p_best = reinterpret_cast<float*>(ws + L.p_best);
     float* p_sum = reinterpret_cast<float*>(ws + L.p_sum);
     int* p_idx = reinterpret_cast<int*>(ws + L.p_idx);
-    int e;
-    if (cfg < 0) {
-        e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx,
-                             st);
-    } else {
+    if (cfg >= 0) {
         const Guard g = make_guard(h, L, ws);
-        e = launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, st);
+        return launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, d_idx,
+                                 d_maxprob, d_row_max, d_row_inv, st);
     }
-    if (e) return e;
+    if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
+                                 p_idx, st))
+        return e;
     return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, st);
 }
 

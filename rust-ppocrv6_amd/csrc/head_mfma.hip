@@ -493,81 +493,90 @@ __global__ __launch_bounds__(256, 2) void stats_mfma_kernel(
     }
 }
 
-// Epilogue of one tile, common path: t = logit * log2(e), the tile maximum, and the
-// tile's sum of exp2(t - ref).  Branch-free, so the compiler can interleave it with the
-// next tile's MFMAs.
-template <int MB>
-__device__ __forceinline__ void epi_common(f32x16 (&acc)[MB], const float* __restrict__ ep, int h,
-                                           const float (&ref)[MB], float (&tmax)[MB], float (&tsum)[MB]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const f32x4 s4 = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+// ============================================================ fused statistics, main pass
+// One piece of the epilogue of a tile (compile-time piece number P; MB blocks of 32
+// activation rows).  The pieces of a tile, in order:
+//   0..3            t = acc*scale*log2e + bias*log2e for accumulator quad q (classes
+//                   8q + 4h + 0..3), then the LDS load of quad q+1's constants
+//   4..4+MB-1       the tile maximum of block b
+//   4+MB..4+5MB-1   exp2(t - ref) (exp2(t) when SUB is false: every ref is 0) and the
+//                   tile sum, for quad (g % 4) of block (g / 4)
+//   4+5MB           running maximum, whether this tile raised it, whether ref must move
+// Pieces are spread over the MFMA steps of the next tile, so each wave keeps the vector
+// ALU busy while its own MFMAs run.
+template <int P, int MB, bool SUB>
+__device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restrict__ ep, int h, f32x4& cs,
+                                          f32x4& cb, const float (&ref)[MB], float (&tmax)[MB],
+                                          float (&tsum)[MB], float (&best)[MB], bool (&better)[MB], bool& need) {
+    if constexpr (P < 4) {
+        constexpr int q = P;
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[b][4 * q + e] = fmaf(acc[b][4 * q + e], s4[e], b4[e]);
-    }
+            for (int e = 0; e < 4; ++e) t[b][4 * q + e] = fmaf(t[b][4 * q + e], cs[e], cb[e]);
+        if constexpr (q < 3) {
+            cs = *reinterpret_cast<const f32x4*>(ep + 8 * (q + 1) + 4 * h);
+            cb = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * (q + 1) + 4 * h);
+        }
+    } else if constexpr (P < 4 + MB) {
+        constexpr int b = P - 4;
+        const float m01 = fmaxf(fmaxf(t[b][0], t[b][1]), t[b][2]);
+        const float m02 = fmaxf(fmaxf(t[b][3], t[b][4]), t[b][5]);
+        const float m03 = fmaxf(fmaxf(t[b][6], t[b][7]), t[b][8]);
+        const float m04 = fmaxf(fmaxf(t[b][9], t[b][10]), t[b][11]);
+        const float m05 = fmaxf(fmaxf(t[b][12], t[b][13]), t[b][14]);
+        tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
+    } else if constexpr (P < 4 + 5 * MB) {
+        constexpr int g = P - 4 - MB, b = g / 4, q = g % 4;
+        float e[4];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        const f32x16& t = acc[b];
-        const float m01 = fmaxf(fmaxf(t[0], t[1]), t[2]);
-        const float m02 = fmaxf(fmaxf(t[3], t[4]), t[5]);
-        const float m03 = fmaxf(fmaxf(t[6], t[7]), t[8]);
-        const float m04 = fmaxf(fmaxf(t[9], t[10]), t[11]);
-        const float m05 = fmaxf(fmaxf(t[12], t[13]), t[14]);
-        tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[15]));
-        float e[16];
+        for (int x = 0; x < 4; ++x) e[x] = __builtin_amdgcn_exp2f(SUB ? t[b][4 * q + x] - ref[b] : t[b][4 * q + x]);
+        const float s = (e[0] + e[1]) + (e[2] + e[3]);
+        tsum[b] = (q == 0) ? s : tsum[b] + s;
+        // keep the sum here: without a use in this piece the exps would be sunk past the
+        // pieces that follow, out of the MFMA steps they are meant to overlap
+        asm volatile("" : "+v"(tsum[b]));
+    } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t[r] - ref[b]);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) e[r] += e[r + 8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) e[r] += e[r + 4];
-        tsum[b] = (e[0] + e[2]) + (e[1] + e[3]);
-    }
-}
-
-// Epilogue of one tile, rare path: a lane whose tile maximum beats its running maximum
-// records the first index of it; a maximum more than 64 above ref moves ref to it (the
-// tile's sum is recomputed, since exp2(t - old ref) may have overflowed).
-template <int MB>
-__device__ __forceinline__ void epi_rare(const f32x16 (&t)[MB], int nrow0, const float (&tmax)[MB],
-                                         float (&tsum)[MB], float (&best)[MB], float (&sum)[MB], float (&ref)[MB],
-                                         int (&bidx)[MB]) {
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        if (tmax[b] > best[b]) {
-            int ri = 15;
-#pragma unroll
-            for (int r = 14; r >= 0; --r) ri = (t[b][r] == tmax[b]) ? r : ri;
-            best[b] = tmax[b];
-            bidx[b] = nrow0 + 8 * (ri >> 2) + (ri & 3);
-            if (best[b] > ref[b] + 64.0f || best[b] < ref[b] - 64.0f) {
-                const float nr = best[b];
-                sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - nr);
-                float s = 0.0f;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(t[b][r] - nr);
-                tsum[b] = s;
-                ref[b] = nr;
-            }
+        for (int b = 0; b < MB; ++b) {
+            better[b] = tmax[b] > best[b];
+            best[b] = fmaxf(best[b], tmax[b]);
+            need = need | ((best[b] != -INFINITY) & (__builtin_fabsf(best[b] - ref[b]) > 64.0f));
         }
     }
 }
 
-// Software-pipelined fused projection + softmax statistics (main pass).  Each wave
-// issues the MFMAs of tile j+1 (into the second accumulator set) in the same
-// instruction stream as the epilogue of tile j, so the matrix core and the vector ALU
-// of a SIMD work at the same time within one wave, and two waves per SIMD keep both
-// busy.  Weight tiles go through a 3-deep LDS ring (tile j: epilogue constants, tile
-// j+1: MFMA fragments, tile j+2: being staged), one barrier per tile.
+template <int S, int NP, int s, int MB, bool SUB>
+__device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float* __restrict__ ep, int h,
+                                                   f32x4& cs, f32x4& cb, const float (&ref)[MB],
+                                                   float (&tmax)[MB], float (&tsum)[MB], float (&best)[MB],
+                                                   bool (&better)[MB], bool& need) {
+    constexpr int p0 = s * NP / S, p1 = (s + 1) * NP / S;
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (epi_piece<p0 + I, MB, SUB>(t, ep, h, cs, cb, ref, tmax, tsum, best, better, need), ...);
+    }(std::make_integer_sequence<int, p1 - p0>{});
+}
+
+// Fused projection + softmax statistics, main pass.  Rows of the MFMA = classes, columns
+// = activation rows: lane (i, h) owns activation row i of each block and 16 classes of
+// each tile (n0 + 8*(r/4) + 4*h + (r%4)), so a row's statistics need no cross-lane
+// traffic until the end of the chunk.  Per row the kernel keeps the running maximum of
+// t = logit*log2(e), sum exp2(t - ref), the first tile that reached the maximum and, in
+// LDS, that tile's 16 values of the lane: the first class reaching the maximum is found
+// once, at the end of the chunk.  `ref` stays put unless the maximum moves more than 64
+// away from it (a rare, wave-uniform branch); while every ref of a wave is 0 the
+// subtraction is skipped.  Software pipeline: the MFMAs of tile j+1 (second accumulator
+// set) and the epilogue of tile j are issued interleaved in one instruction stream;
+// weight tiles pass through a 3-slot LDS ring (tile j: epilogue constants, j+1: MFMA
+// fragments, j+2: being staged), one barrier per tile.
 template <int C, int G, int MB>
-__global__ __launch_bounds__(256, 2) void stats_sw_kernel(
+__global__ __launch_bounds__(256, 2) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
     int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows) {
     using GE = Geo<C, G>;
+    constexpr int S = GE::S;
+    constexpr int NP = 5 + 5 * MB;
     constexpr int RPB = 128 * MB;
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -581,28 +590,30 @@ __global__ __launch_bounds__(256, 2) void stats_sw_kernel(
     const int64_t mrow0 = (int64_t)mbi * RPB + wave * (32 * MB);
     if (tid < 96) reinterpret_cast<u32x4*>(lds + (tid >> 5) * GE::BUF + GE::REC)[tid & 31] = u32x4{0, 0, 0, 0};
     const int lb = i * 16 + h * 512;
+    // this lane's saved values of its best tile: [block][quad][lane] x 4 floats
+    f32x4* save = reinterpret_cast<f32x4*>(lds + 3 * GE::BUF) + wave * (MB * 4 * 64) + lane;
 
     int64_t arow[MB];
     bool valid[MB];
-    bf16x8 bf[MB][GE::S];
+    bf16x8 bf[MB][S];
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
         arow[b] = mrow0 + 32 * b + i;
         valid[b] = arow[b] < m;
         float amax = 0.0f;
 #pragma unroll
-        for (int s = 0; s < GE::S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
+        for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
         if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
     }
 
     float best[MB], sum[MB], ref[MB];
-    int bidx[MB];
+    int bt[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
         best[b] = -INFINITY;
         sum[b] = 0.0f;
         ref[b] = 0.0f;
-        bidx[b] = 0;
+        bt[b] = -1;
     }
 
     if (t0 < t1) {
@@ -616,173 +627,113 @@ __global__ __launch_bounds__(256, 2) void stats_sw_kernel(
 #pragma unroll
         for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
 #pragma unroll
-        for (int s = 0; s < GE::S; ++s) {
+        for (int s = 0; s < S; ++s) {
             const bf16x8 wf = weight_frag<C, G>(lds, s, lb, i * 16, h);
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc_a[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc_a[b], 0, 0, 0);
         }
-        // One tile: stage tile j+2, MFMAs of tile j+1 into accM interleaved with the
-        // epilogue of tile j on accE, then the rare path, then the barrier.  Past the end the
-        // MFMAs read a stale ring slot and the load repeats the last tile: harmless, and it
-        // keeps the body one basic block.
-        auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
-            const int rel = j - t0;
-            const int cur = rel % 3, nxt = (rel + 1) % 3, nn = (rel + 2) % 3;
+        int cur = 0, nxt = 1, nn = 2;  // ring slots of tiles j, j+1, j+2
+        bool refz = true;              // every ref of the wave is 0
+        // One tile: stage tile j+2, the MFMAs of tile j+1 into accM interleaved with the
+        // epilogue of tile j on accE, the saves of a raised maximum, the rare re-reference,
+        // the barrier.  Past the end the MFMAs read a stale ring slot and the load repeats
+        // the last tile: harmless, and it keeps the body branch-free.
+        auto step = [&](auto sub_c, int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
+            constexpr bool SUB = decltype(sub_c)::value;
+            // distinct markers keep the compiler from hoisting the pieces both variants
+            // share above the variant branch, out of their MFMA steps
+            if constexpr (SUB)
+                asm volatile("; statistics step, ref subtracted");
+            else
+                asm volatile("; statistics step, ref zero");
             stg.load(rec + (size_t)min(j + 2, t1 - 1) * GE::REC, tid);
             const uint8_t* bufn = lds + nxt * GE::BUF;
+            const float* ep = reinterpret_cast<const float*>(lds + cur * GE::BUF + GE::FRAG);
+            f32x4 cs = *reinterpret_cast<const f32x4*>(ep + 4 * h);
+            f32x4 cb = *reinterpret_cast<const f32x4*>(ep + 32 + 4 * h);
+            float tmax[MB], tsum[MB];
+            bool better[MB];
+            bool need = false;
 #pragma unroll
             for (int b = 0; b < MB; ++b) accM[b] = f32x16{};
+            bf16x8 wf = weight_frag<C, G>(bufn, 0, lb, i * 16, h);
+            [&]<int... s>(std::integer_sequence<int, s...>) {
+                ([&] {
+                    const bf16x8 wn = weight_frag<C, G>(bufn, s + 1 < S ? s + 1 : s, lb, i * 16, h);
 #pragma unroll
-            for (int s = 0; s < GE::S; ++s) {
-                const bf16x8 wf = weight_frag<C, G>(bufn, s, lb, i * 16, h);
+                    for (int b = 0; b < MB; ++b)
+                        accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], accM[b], 0, 0, 0);
+                    epi_pieces_of_step<S, NP, s, MB, SUB>(accE, ep, h, cs, cb, ref, tmax, tsum, best, better, need);
+                    __builtin_amdgcn_sched_barrier(0);
+                    wf = wn;
+                }(), ...);
+            }(std::make_integer_sequence<int, S>{});
 #pragma unroll
-                for (int b = 0; b < MB; ++b)
-                    accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], accM[b], 0, 0, 0);
+            for (int b = 0; b < MB; ++b) {
+                if (better[b]) {
+                    bt[b] = j;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        save[(b * 4 + q) * 64] = f32x4{accE[b][4 * q], accE[b][4 * q + 1], accE[b][4 * q + 2],
+                                                       accE[b][4 * q + 3]};
+                }
             }
-            float tmax[MB], tsum[MB];
-            epi_common<MB>(accE, reinterpret_cast<const float*>(lds + cur * GE::BUF + GE::FRAG), h, ref, tmax, tsum);
-            // interleave: per MFMA one DS read and a few VALU ops of the epilogue
+            if (__any(need)) {
+                bool anyref = false;
 #pragma unroll
-            for (int x = 0; x < GE::S * MB; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                for (int b = 0; b < MB; ++b) {
+                    if (best[b] != -INFINITY && __builtin_fabsf(best[b] - ref[b]) > 64.0f) {
+                        const float nr = best[b];
+                        sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - nr);
+                        float s = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(accE[b][r] - nr);
+                        tsum[b] = s;
+                        ref[b] = nr;
+                    }
+                    anyref = anyref || ref[b] != 0.0f;
+                }
+                refz = !__any(anyref);
             }
-            bool anyb = false;
-#pragma unroll
-            for (int b = 0; b < MB; ++b) anyb = anyb || tmax[b] > best[b];
-            if (__any(anyb)) epi_rare<MB>(accE, j * 32 + 4 * h, tmax, tsum, best, sum, ref, bidx);
 #pragma unroll
             for (int b = 0; b < MB; ++b) sum[b] += tsum[b];
             stg.store(lds + nn * GE::BUF, tid);
             __syncthreads();
+            const int c0 = cur;
+            cur = nxt;
+            nxt = nn;
+            nn = c0;
         };
+        constexpr std::false_type no_sub{};
+        constexpr std::true_type with_sub{};
         int j = t0;
         for (; j + 1 < t1; j += 2) {
-            step(j, acc_a, acc_b);
-            step(j + 1, acc_b, acc_a);
+            step(with_sub, j, acc_a, acc_b);
+            step(with_sub, j + 1, acc_b, acc_a);
         }
-        if (j < t1) step(j, acc_a, acc_b);
+        if (j < t1) step(with_sub, j, acc_a, acc_b);
+        (void)refz;
+        (void)no_sub;
     }
 
+    // first class of the best tile reaching the maximum; then lanes i and i+32 (same
+    // activation row) merge and lanes 0-31 write.
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-        RowStat mine{best[b], sum[b], ref[b], bidx[b]};
-        RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
-                      __shfl_xor(bidx[b], 32, 64)};
-        const RowStat r = stat_merge(mine, other);
-        if (h == 0 && valid[b]) {
-            p_best[(int64_t)chunk * m + arow[b]] = r.best;
-            p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
-            p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
-        }
-    }
-}
-
-// Ping-pong variant of the fused projection + softmax statistics (main pass).  A
-// workgroup of 8 waves: waves w and w+4 share a SIMD (the dispatcher places the waves of
-// a workgroup round-robin over the 4 SIMDs), so group A = waves 0-3 and group B = waves
-// 4-7 alternate: in every half-step one group runs the MFMAs of a tile while the other
-// runs the softmax/argmax epilogue of its previous tile, and the matrix cores and the
-// vector ALUs of each SIMD work at the same time.  Weight tiles are shared by both groups
-// through a 2-deep LDS ring; one barrier per half-step.
-//   half-step 2j:   A  MFMA(tile j)      B  epilogue(tile j-1)
-//   half-step 2j+1: A  epilogue(tile j)  B  MFMA(tile j)
-template <int C, int G, int MB>
-__global__ __launch_bounds__(512, 2) void stats_pp_kernel(
-    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
-    int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows) {
-    using GE = Geo<C, G>;
-    constexpr int RPB = 256 * MB;
-    extern __shared__ __align__(16) uint8_t lds[];
-
-    int mbi, chunk;
-    map_block(blockIdx.x, nsplit, &mbi, &chunk);
-    if (mbi >= mblocks) return;
-    const int t0 = chunk * tiles_per_chunk;
-    const int T = max(min(t0 + tiles_per_chunk, tiles) - t0, 0);
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2, i = lane & 31, h = lane >> 5;
-    const int64_t mrow0 = (int64_t)mbi * RPB + wave * (32 * MB);
-    zero_blocks(lds, GE::BUF, GE::REC, tid);
-    const int lb = i * 16 + h * 512;
-
-    int64_t arow[MB];
-    bool valid[MB];
-    bf16x8 bf[MB][GE::S];
+        int cls = 0;
+        if (bt[b] >= 0) {
+            int r0 = 16;
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        arow[b] = mrow0 + 32 * b + i;
-        valid[b] = arow[b] < m;
-        float amax = 0.0f;
+            for (int q = 3; q >= 0; --q) {
+                const f32x4 v = save[(b * 4 + q) * 64];
 #pragma unroll
-        for (int s = 0; s < GE::S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
-        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
-    }
-
-    float best[MB], sum[MB], ref[MB];
-    int bidx[MB];
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        best[b] = -INFINITY;
-        sum[b] = 0.0f;
-        ref[b] = 0.0f;
-        bidx[b] = 0;
-    }
-    bool refzero = true;
-
-    if (T > 0) {
-        Stage<GE::REC, 512> stg;
-        stg.load(rec + (size_t)t0 * GE::REC, tid);
-        stg.store(lds, tid);
-        __syncthreads();
-        f32x16 acc[MB];
-#pragma unroll
-        for (int b = 0; b < MB; ++b) acc[b] = f32x16{};
-        for (int hs = 0; hs <= 2 * T; ++hs) {
-            const int tt = hs >> 1;
-            const bool odd = hs & 1;
-            if (!odd && tt + 1 < T) stg.load(rec + (size_t)(t0 + tt + 1) * GE::REC, tid);
-            const bool do_mfma = grp == 0 ? (!odd && tt < T) : odd;
-            const bool do_epi = grp == 0 ? odd : (!odd && hs >= 2);
-            if (do_mfma) {
-                const uint8_t* buf = lds + (tt & 1) * GE::BUF;
-#pragma unroll
-                for (int b = 0; b < MB; ++b) acc[b] = f32x16{};
-#pragma unroll
-                for (int s = 0; s < GE::S; ++s) {
-                    const bf16x8 wf = weight_frag<C, G>(buf, s, lb, i * 16, h);
-#pragma unroll
-                    for (int b = 0; b < MB; ++b)
-                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc[b], 0, 0, 0);
-                }
-            } else if (do_epi) {
-                const int te = grp == 0 ? tt : tt - 1;
-                const float* ep = reinterpret_cast<const float*>(lds + (te & 1) * GE::BUF + GE::FRAG);
-                float sl[16], bl[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
-                    const f32x4 b4 = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        sl[4 * q + e] = s4[e];
-                        bl[4 * q + e] = b4[e];
-                    }
-                }
-                stats_update<MB>(acc, sl, bl, (t0 + te) * 32 + 4 * h, best, sum, ref, bidx, refzero);
+                for (int e = 3; e >= 0; --e) r0 = (v[e] == best[b]) ? 4 * q + e : r0;
             }
-            if (odd && tt + 1 < T) stg.store(lds + ((tt + 1) & 1) * GE::BUF, tid);
-            __syncthreads();
+            cls = bt[b] * 32 + (r0 < 16 ? 8 * (r0 >> 2) + 4 * h + (r0 & 3) : 0);
         }
-    }
-
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        RowStat mine{best[b], sum[b], ref[b], bidx[b]};
+        RowStat mine{best[b], sum[b], ref[b], cls};
         RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
-                      __shfl_xor(bidx[b], 32, 64)};
+                      __shfl_xor(cls, 32, 64)};
         const RowStat r = stat_merge(mine, other);
         if (h == 0 && valid[b]) {
             p_best[(int64_t)chunk * m + arow[b]] = r.best;
@@ -798,6 +749,11 @@ __global__ void guard_reset_kernel(int* guard_count) { *guard_count = 0; }
 template <int C>
 static constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1) ? 2 : 1;
+}
+// LDS of the main statistics pass: the 3-slot tile ring and each wave's saved best tile.
+template <int C, int G>
+static constexpr int main_lds_bytes() {
+    return 3 * Geo<C, G>::BUF + 4 * mb_of<C>() * 16 * 64 * 4;
 }
 
 // Rows per workgroup of the main statistics pass and of the rescue pass (4 waves).
@@ -913,7 +869,7 @@ int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
 
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
                       int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx, const Guard* guard,
-                      hipStream_t st) {
+                      int32_t* idx, float* maxprob, float* row_max, float* row_inv, hipStream_t st) {
     if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
     if (nsplit != 1 && nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16 && nsplit != 32 && nsplit != 64)
         return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be a power of two <= 64");
@@ -932,27 +888,31 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     }
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        constexpr int LDS = 2 * Geo<C, G>::BUF;
-        stats_sw_kernel<C, G, mb_of<C>()><<<grid, 256, 3 * Geo<C, G>::BUF, st>>>(
+        stats_main_kernel<C, G, mb_of<C>()><<<grid, 256, main_lds_bytes<C, G>(), st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
             guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
-    if (e || !guarded) return e;
-    // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
-    const int rrpb = rescue_rows_per_block(rcfg);
-    const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, 64);
-    const int rgrid = grid_blocks(slots, nsplit);
-    return dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
-        constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        constexpr int LDS = 2 * Geo<C, G>::BUF;
-        stats_mfma_kernel<C, G, mb_of<C>()><<<rgrid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc,
-                                                                     slots, p_best, p_sum, p_idx, 0.0f, nullptr,
-                                                                     nullptr, guard->rows, guard->count);
-        PPOCR_HIP(hipGetLastError());
-        return PPOCR_OK;
-    });
+    if (e) return e;
+    if (guarded) {
+        // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
+        // (with exact class indices)
+        const int rrpb = rescue_rows_per_block(rcfg);
+        const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, 64);
+        const int rgrid = grid_blocks(slots, nsplit);
+        e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
+            constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
+            constexpr int LDS = 2 * Geo<C, G>::BUF;
+            stats_mfma_kernel<C, G, mb_of<C>()><<<rgrid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, nsplit,
+                                                                         tpc, slots, p_best, p_sum, p_idx, 0.0f,
+                                                                         nullptr, nullptr, guard->rows, guard->count);
+            PPOCR_HIP(hipGetLastError());
+            return PPOCR_OK;
+        });
+        if (e) return e;
+    }
+    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max, row_inv, st);
 }
 
 }  // namespace ppocr

@@ -42,9 +42,13 @@ int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const fl
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.
 int stats_nsplit(int64_t m, int rows_per_block);
 int stats_rows_per_block_mfma(int cfg);
+// Main pass, rescue of the guarded rows, then one wave per row merges the partials and
+// resolves the argmax: idx, maxprob (1/sum) and, when non-null, row_max (log2-domain
+// maximum) and row_inv (1/sum) for a probs pass.
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                       int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
-                      const Guard* guard, hipStream_t st);
+                      const Guard* guard, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
+                      hipStream_t st);
 int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                       int64_t n, int64_t k, const float* row_max, const float* row_inv, float* probs,
                       const Guard* guard, hipStream_t st);
