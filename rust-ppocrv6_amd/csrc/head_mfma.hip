@@ -207,6 +207,47 @@ struct Stage {
     }
 };
 
+// Global -> LDS staging of one tile record without registers: each wave issues direct
+// 16-byte-per-lane loads into LDS (wave w, instruction x covers 16-byte chunks
+// x*NT + 64*w .. +63).  Completion is awaited by the workgroup barrier that follows
+// (its fence waits for the wave's outstanding loads), before any wave reads the slot.
+template <int REC, int NT = 256>
+__device__ __forceinline__ void stage_direct(const uint8_t* __restrict__ src, uint8_t* dst, int tid) {
+    constexpr int CH = REC / 16;
+    constexpr int PER = (CH + NT - 1) / NT;
+    static_assert(REC % 16 == 0 && PER >= 1 && PER <= 4, "tile record size");
+    const int wave_chunk = tid & ~63;  // 64 * wave
+#pragma unroll
+    for (int x = 0; x < PER; ++x) {
+        const int c0 = x * NT + wave_chunk;  // first chunk of this wave's instruction (uniform)
+        if (CH % NT == 0 || c0 + (tid & 63) < CH)
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src + (size_t)(c0 + (tid & 63)) * 16),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(dst + (size_t)c0 * 16)),
+                16, 0, 0);
+    }
+}
+
+// Number of direct-load instructions every wave issues per staged tile record (waves past
+// the end of a partial last round issue one fewer).
+template <int REC, int NT = 256>
+constexpr int stage_direct_min_ops() {
+    return (REC / 16) / NT;
+}
+
+// Workgroup barrier for a ring whose newest N direct loads per wave may still be in
+// flight: wait until at most N of this wave's loads are outstanding (so every older tile
+// is in LDS) and all of its LDS accesses are done, then synchronise.  The barrier is
+// written as an asm statement with a memory clobber: the compiler keeps every memory
+// access on its side, and adds no wait for the newest loads (a fence would wait for all).
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+    static_assert(N >= 0 && N < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0x0 << 8));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ void zero_blocks(uint8_t* lds, int buf_bytes, int rec_bytes, int tid) {
     if (tid < 64) reinterpret_cast<u32x4*>(lds + (tid >> 5) * buf_bytes + rec_bytes)[tid & 31] = u32x4{0, 0, 0, 0};
 }
@@ -497,26 +538,34 @@ __global__ __launch_bounds__(256, 2) void stats_mfma_kernel(
 // One piece of the epilogue of a tile (compile-time piece number P; MB blocks of 32
 // activation rows).  The pieces of a tile, in order:
 //   0..3            t = acc*scale*log2e + bias*log2e for accumulator quad q (classes
-//                   8q + 4h + 0..3), then the LDS load of quad q+1's constants
-//   4..4+MB-1       the tile maximum of block b
-//   4+MB..4+5MB-1   exp2(t - ref) (exp2(t) when SUB is false: every ref is 0) and the
-//                   tile sum, for quad (g % 4) of block (g / 4)
-//   4+5MB           running maximum, whether this tile raised it, whether ref must move
+//                   8q + 4h + 0..3), then the LDS load of quad q+2's constants
+//   4..4+MB-1       the tile maximum of block b, and whether it beats the running maximum
+//   4+MB..4+5MB-1   exp2(t - ref) and the tile sum, for quad (g % 4) of block (g / 4)
+//   4+5MB           a lane whose maximum was beaten saves the tile's 16 values of its rows
+//                   and the tile number (masked LDS stores)
+//   5+5MB           running maximum, and whether ref must move
 // Pieces are spread over the MFMA steps of the next tile, so each wave keeps the vector
-// ALU busy while its own MFMAs run.
-template <int P, int MB, bool SUB>
-__device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restrict__ ep, int h, f32x4& cs,
-                                          f32x4& cb, const float (&ref)[MB], float (&tmax)[MB],
-                                          float (&tsum)[MB], float (&best)[MB], bool (&better)[MB], bool& need) {
+// ALU and the LDS busy while its own MFMAs run.
+template <int MB>
+struct EpiState {
+    float tmax[MB], tsum[MB];
+    bool better[MB];
+    bool need;
+};
+
+template <int P, int MB>
+__device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
+                                          f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
+                                          float (&best)[MB], int (&bt)[MB], f32x4* save, EpiState<MB>& st) {
     if constexpr (P < 4) {
         constexpr int q = P;
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t[b][4 * q + e] = fmaf(t[b][4 * q + e], cs[e], cb[e]);
-        if constexpr (q < 3) {
-            cs = *reinterpret_cast<const f32x4*>(ep + 8 * (q + 1) + 4 * h);
-            cb = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * (q + 1) + 4 * h);
+            for (int e = 0; e < 4; ++e) t[b][4 * q + e] = fmaf(t[b][4 * q + e], cs[q & 1][e], cb[q & 1][e]);
+        if constexpr (q < 2) {
+            cs[q & 1] = *reinterpret_cast<const f32x4*>(ep + 8 * (q + 2) + 4 * h);
+            cb[q & 1] = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * (q + 2) + 4 * h);
         }
     } else if constexpr (P < 4 + MB) {
         constexpr int b = P - 4;
@@ -525,35 +574,51 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
         const float m03 = fmaxf(fmaxf(t[b][6], t[b][7]), t[b][8]);
         const float m04 = fmaxf(fmaxf(t[b][9], t[b][10]), t[b][11]);
         const float m05 = fmaxf(fmaxf(t[b][12], t[b][13]), t[b][14]);
-        tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
+        st.tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
+        st.better[b] = st.tmax[b] > best[b];
     } else if constexpr (P < 4 + 5 * MB) {
         constexpr int g = P - 4 - MB, b = g / 4, q = g % 4;
         float e[4];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) e[x] = __builtin_amdgcn_exp2f(SUB ? t[b][4 * q + x] - ref[b] : t[b][4 * q + x]);
+        for (int x = 0; x < 4; ++x) e[x] = __builtin_amdgcn_exp2f(t[b][4 * q + x] - ref[b]);
         const float s = (e[0] + e[1]) + (e[2] + e[3]);
-        tsum[b] = (q == 0) ? s : tsum[b] + s;
+        st.tsum[b] = (q == 0) ? s : st.tsum[b] + s;
         // keep the sum here: without a use in this piece the exps would be sunk past the
         // pieces that follow, out of the MFMA steps they are meant to overlap
-        asm volatile("" : "+v"(tsum[b]));
+        asm volatile("" : "+v"(st.tsum[b]));
+    } else if constexpr (P == 4 + 5 * MB) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            if (st.better[b]) {
+                bt[b] = j;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    save[(b * 4 + q) * 64] = f32x4{t[b][4 * q], t[b][4 * q + 1], t[b][4 * q + 2], t[b][4 * q + 3]};
+            }
+        }
     } else {
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
-            better[b] = tmax[b] > best[b];
-            best[b] = fmaxf(best[b], tmax[b]);
-            need = need | ((best[b] != -INFINITY) & (__builtin_fabsf(best[b] - ref[b]) > 64.0f));
+            best[b] = fmaxf(best[b], st.tmax[b]);
+            st.need = st.need | ((best[b] != -INFINITY) & (__builtin_fabsf(best[b] - ref[b]) > 64.0f));
         }
     }
 }
 
-template <int S, int NP, int s, int MB, bool SUB>
-__device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float* __restrict__ ep, int h,
-                                                   f32x4& cs, f32x4& cb, const float (&ref)[MB],
-                                                   float (&tmax)[MB], float (&tsum)[MB], float (&best)[MB],
-                                                   bool (&better)[MB], bool& need) {
+template <int MB>
+constexpr int epi_pieces() {
+    return 6 + 5 * MB;
+}
+
+template <int S, int s, int MB>
+__device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
+                                                   f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
+                                                   float (&best)[MB], int (&bt)[MB], f32x4* save,
+                                                   EpiState<MB>& st) {
+    constexpr int NP = epi_pieces<MB>();
     constexpr int p0 = s * NP / S, p1 = (s + 1) * NP / S;
     [&]<int... I>(std::integer_sequence<int, I...>) {
-        (epi_piece<p0 + I, MB, SUB>(t, ep, h, cs, cb, ref, tmax, tsum, best, better, need), ...);
+        (epi_piece<p0 + I, MB>(t, ep, h, j, cs, cb, ref, best, bt, save, st), ...);
     }(std::make_integer_sequence<int, p1 - p0>{});
 }
 
@@ -564,11 +629,14 @@ __device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float*
 // t = logit*log2(e), sum exp2(t - ref), the first tile that reached the maximum and, in
 // LDS, that tile's 16 values of the lane: the first class reaching the maximum is found
 // once, at the end of the chunk.  `ref` stays put unless the maximum moves more than 64
-// away from it (a rare, wave-uniform branch); while every ref of a wave is 0 the
-// subtraction is skipped.  Software pipeline: the MFMAs of tile j+1 (second accumulator
-// set) and the epilogue of tile j are issued interleaved in one instruction stream;
-// weight tiles pass through a 3-slot LDS ring (tile j: epilogue constants, j+1: MFMA
-// fragments, j+2: being staged), one barrier per tile.
+// away from it (a rare, wave-uniform branch).  Software pipeline: the MFMAs of tile j+1
+// (second accumulator set) and the epilogue of tile j are issued interleaved in one
+// instruction stream; weight tiles pass through a 4-slot LDS ring (tile j: epilogue
+// constants, j+1: MFMA fragments, j+2 and j+3: being loaded straight from global memory
+// into LDS), one barrier per tile.
+constexpr int kPrefetch = 2;
+constexpr int kRing = 4;  // LDS tile slots of the main statistics pass (a power of two)
+
 template <int C, int G, int MB>
 __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
@@ -576,7 +644,6 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
-    constexpr int NP = 5 + 5 * MB;
     constexpr int RPB = 128 * MB;
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -588,10 +655,11 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
     const int64_t mrow0 = (int64_t)mbi * RPB + wave * (32 * MB);
-    if (tid < 96) reinterpret_cast<u32x4*>(lds + (tid >> 5) * GE::BUF + GE::REC)[tid & 31] = u32x4{0, 0, 0, 0};
+    if (tid < 32 * kRing)
+        reinterpret_cast<u32x4*>(lds + (tid >> 5) * GE::BUF + GE::REC)[tid & 31] = u32x4{0, 0, 0, 0};
     const int lb = i * 16 + h * 512;
     // this lane's saved values of its best tile: [block][quad][lane] x 4 floats
-    f32x4* save = reinterpret_cast<f32x4*>(lds + 3 * GE::BUF) + wave * (MB * 4 * 64) + lane;
+    f32x4* save = reinterpret_cast<f32x4*>(lds + kRing * GE::BUF) + wave * (MB * 4 * 64) + lane;
 
     int64_t arow[MB];
     bool valid[MB];
@@ -617,12 +685,11 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     }
 
     if (t0 < t1) {
-        Stage<GE::REC> stg;
-        stg.load(rec + (size_t)t0 * GE::REC, tid);
-        stg.store(lds, tid);
-        stg.load(rec + (size_t)min(t0 + 1, t1 - 1) * GE::REC, tid);
-        stg.store(lds + GE::BUF, tid);
-        __syncthreads();
+        constexpr int kOps = stage_direct_min_ops<GE::REC>();
+#pragma unroll
+        for (int x = 0; x < kRing - 1; ++x)
+            stage_direct<GE::REC>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
+        ring_barrier<kOps>();  // tiles t0 and t0+1 are in LDS
         f32x16 acc_a[MB], acc_b[MB];
 #pragma unroll
         for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
@@ -632,54 +699,44 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc_a[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc_a[b], 0, 0, 0);
         }
-        int cur = 0, nxt = 1, nn = 2;  // ring slots of tiles j, j+1, j+2
-        bool refz = true;              // every ref of the wave is 0
-        // One tile: stage tile j+2, the MFMAs of tile j+1 into accM interleaved with the
-        // epilogue of tile j on accE, the saves of a raised maximum, the rare re-reference,
-        // the barrier.  Past the end the MFMAs read a stale ring slot and the load repeats
-        // the last tile: harmless, and it keeps the body branch-free.
-        auto step = [&](auto sub_c, int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
-            constexpr bool SUB = decltype(sub_c)::value;
-            // distinct markers keep the compiler from hoisting the pieces both variants
-            // share above the variant branch, out of their MFMA steps
-            if constexpr (SUB)
-                asm volatile("; statistics step, ref subtracted");
-            else
-                asm volatile("; statistics step, ref zero");
-            stg.load(rec + (size_t)min(j + 2, t1 - 1) * GE::REC, tid);
-            const uint8_t* bufn = lds + nxt * GE::BUF;
-            const float* ep = reinterpret_cast<const float*>(lds + cur * GE::BUF + GE::FRAG);
-            f32x4 cs = *reinterpret_cast<const f32x4*>(ep + 4 * h);
-            f32x4 cb = *reinterpret_cast<const f32x4*>(ep + 32 + 4 * h);
-            float tmax[MB], tsum[MB];
-            bool better[MB];
-            bool need = false;
+        // One tile: start loading tile j+3, the MFMAs of tile j+1 into accM interleaved
+        // with the epilogue of tile j on accE, the saves of a raised maximum, the rare
+        // re-reference, the barrier (after which tile j+2 is in LDS).  Past the end the
+        // MFMAs read a stale ring slot and the load repeats the last tile: harmless, and it
+        // keeps the body branch-free.
+        auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
+            const unsigned rel = (unsigned)(j - t0);
+            stage_direct<GE::REC>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
+                                  lds + ((rel + kRing - 1) & (kRing - 1)) * GE::BUF, tid);
+            const uint8_t* bufn = lds + ((rel + 1) & (kRing - 1)) * GE::BUF;
+            const float* ep = reinterpret_cast<const float*>(lds + (rel & (kRing - 1)) * GE::BUF + GE::FRAG);
+            f32x4 cs[2], cb[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                cs[q] = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
+                cb[q] = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+            }
+            EpiState<MB> st;
+            st.need = false;
 #pragma unroll
             for (int b = 0; b < MB; ++b) accM[b] = f32x16{};
-            bf16x8 wf = weight_frag<C, G>(bufn, 0, lb, i * 16, h);
+            // weight fragments are read kPrefetch MFMA steps ahead of their use, so a wave
+            // never waits on LDS with epilogue work queued behind the wait
+            bf16x8 wq[kPrefetch];
+#pragma unroll
+            for (int x = 0; x < kPrefetch; ++x) wq[x] = weight_frag<C, G>(bufn, x < S ? x : S - 1, lb, i * 16, h);
             [&]<int... s>(std::integer_sequence<int, s...>) {
                 ([&] {
-                    const bf16x8 wn = weight_frag<C, G>(bufn, s + 1 < S ? s + 1 : s, lb, i * 16, h);
+                    epi_pieces_of_step<S, s, MB>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
 #pragma unroll
                     for (int b = 0; b < MB; ++b)
-                        accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], accM[b], 0, 0, 0);
-                    epi_pieces_of_step<S, NP, s, MB, SUB>(accE, ep, h, cs, cb, ref, tmax, tsum, best, better, need);
+                        accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[b][s], accM[b], 0, 0, 0);
+                    if constexpr (s + kPrefetch < S)
+                        wq[s % kPrefetch] = weight_frag<C, G>(bufn, s + kPrefetch, lb, i * 16, h);
                     __builtin_amdgcn_sched_barrier(0);
-                    wf = wn;
                 }(), ...);
             }(std::make_integer_sequence<int, S>{});
-#pragma unroll
-            for (int b = 0; b < MB; ++b) {
-                if (better[b]) {
-                    bt[b] = j;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        save[(b * 4 + q) * 64] = f32x4{accE[b][4 * q], accE[b][4 * q + 1], accE[b][4 * q + 2],
-                                                       accE[b][4 * q + 3]};
-                }
-            }
-            if (__any(need)) {
-                bool anyref = false;
+            if (__any(st.need)) {
 #pragma unroll
                 for (int b = 0; b < MB; ++b) {
                     if (best[b] != -INFINITY && __builtin_fabsf(best[b] - ref[b]) > 64.0f) {
@@ -688,32 +745,23 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
                         float s = 0.0f;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(accE[b][r] - nr);
-                        tsum[b] = s;
+                        st.tsum[b] = s;
                         ref[b] = nr;
                     }
-                    anyref = anyref || ref[b] != 0.0f;
                 }
-                refz = !__any(anyref);
             }
 #pragma unroll
-            for (int b = 0; b < MB; ++b) sum[b] += tsum[b];
-            stg.store(lds + nn * GE::BUF, tid);
-            __syncthreads();
-            const int c0 = cur;
-            cur = nxt;
-            nxt = nn;
-            nn = c0;
+            for (int b = 0; b < MB; ++b) sum[b] += st.tsum[b];
+            ring_barrier<kOps>();
         };
-        constexpr std::false_type no_sub{};
-        constexpr std::true_type with_sub{};
         int j = t0;
         for (; j + 1 < t1; j += 2) {
-            step(with_sub, j, acc_a, acc_b);
-            step(with_sub, j + 1, acc_b, acc_a);
+            step(j, acc_a, acc_b);
+            step(j + 1, acc_b, acc_a);
         }
-        if (j < t1) step(with_sub, j, acc_a, acc_b);
-        (void)refz;
-        (void)no_sub;
+        if (j < t1) step(j, acc_a, acc_b);
+        // the ring's last loads (repeats of the last tile) land before the workgroup ends
+        __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
     }
 
     // first class of the best tile reaching the maximum; then lanes i and i+32 (same
@@ -750,10 +798,10 @@ template <int C>
 static constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1) ? 2 : 1;
 }
-// LDS of the main statistics pass: the 3-slot tile ring and each wave's saved best tile.
+// LDS of the main statistics pass: the tile ring and each wave's saved best tile.
 template <int C, int G>
 static constexpr int main_lds_bytes() {
-    return 3 * Geo<C, G>::BUF + 4 * mb_of<C>() * 16 * 64 * 4;
+    return kRing * Geo<C, G>::BUF + 4 * mb_of<C>() * 16 * 64 * 4;
 }
 
 // Rows per workgroup of the main statistics pass and of the rescue pass (4 waves).
