@@ -36,6 +36,7 @@ def parse():
     p.add_argument("--workload", default="dense_256")
     p.add_argument("--mode", type=int, default=2, help="0 fp32 FMA, 1/2/3 bf16 terms")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-others", action="store_true", help="skip the other configurations")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default="", help="fused|unfused|probs (profiling runs)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -118,6 +119,73 @@ def copy_probe(mib):
             "GBps_read_plus_write": round(2 * nbytes / (ms / 1e3) / 1e9, 1)}
 
 
+def make_workload(name):
+    """A workload by name; the stress batch packs its weights with the GPU packer first
+    (its near-tie rows are placed on the dequantised weights)."""
+    import ppocr_rechead as rh
+    from ppocr_rechead import workloads as wl
+
+    def pack(w_t):
+        qw = rh.QuantizedWeight.from_f32_transposed(w_t)
+        return qw.data, qw.scales
+
+    return wl.make(name, pack=pack if name == "stress_1024" else None)
+
+
+def other_config(name, modes, steps, warmup):
+    """Fused decode step (argmax + CTC) of another configuration, per mode; for an FP32
+    head also the logits kernel alone (the unfused projection)."""
+    import ppocr_rechead as rh
+    from ppocr_rechead import workloads as wl
+    from ppocr_rechead.hip import DeviceArray, Stream
+    L = rh._lib.lib()
+    wk = make_workload(name)
+    a = wk["a"]
+    m, k = a.shape
+    n = wl.N_CLASSES
+    lines = len(wk["line_off"]) - 1
+    if wk["quantized"]:
+        qw = (rh.QuantizedWeight(wk["q"], wk["scales"]) if "q" in wk
+              else rh.QuantizedWeight.from_f32_transposed(wk["w_t"]))
+        head = rh.RecHead(qw=qw, bias=wk["bias"])
+    else:
+        head = rh.RecHead(w_t=wk["w_t"], bias=wk["bias"])
+    stream = Stream()
+    st = stream.h
+    da = DeviceArray.from_numpy(a)
+    doff = DeviceArray.from_numpy(wk["line_off"])
+    didx, dmp, dseq = DeviceArray((m,), np.int32), DeviceArray((m,), np.float32), DeviceArray((m,), np.int32)
+    dlen, dscore = DeviceArray((lines,), np.int64), DeviceArray((lines,), np.float32)
+    res = {"rows": m, "lines": lines, "head": "int8" if wk["quantized"] else "fp32"}
+    for mode in modes:
+        ws = head.workspace_bytes(m, mode)
+        dws = DeviceArray((max(ws, 1),), np.uint8)
+
+        def step():
+            rh._check(L.ppocr_rh_argmax_dev(head.handle, da.p, m, mode, didx.p, dmp.p, dws.p, ws, st))
+            rh._check(L.ppocr_ctc_greedy_dev(didx.p, dmp.p, doff.p, lines, 0, dseq.p, dlen.p, dscore.p, st))
+
+        ms, _ = timed(step, stream, steps, warmup)
+        flops = 2.0 * m * n * k
+        r = {"ms_per_step": round(ms, 4), "rows_per_s": round(m / (ms / 1e3), 1),
+             "TFLOPs": round(flops / (ms / 1e3) / 1e12, 2)}
+        if not wk["quantized"]:
+            dlog = DeviceArray((m, n), np.float32)
+
+            def logits():
+                rh._check(L.ppocr_rh_logits_dev(head.handle, da.p, m, mode, dlog.p, dws.p, ws, st))
+
+            ms_l, _ = timed(logits, stream, max(3, steps // 2), 2)
+            lb = 4.0 * m * n + 4.0 * m * k + 4.0 * n * k + 4.0 * n
+            r["logits_ms"] = round(ms_l, 4)
+            r["logits_GBps"] = round(lb / (ms_l / 1e3) / 1e9, 1)
+            dlog.free()
+        res[{0: "fp32_fma", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3"}[mode]] = r
+        dws.free()
+    head.close()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -130,7 +198,7 @@ def main():
     from ppocr_rechead.hip import DeviceArray, Stream, synchronize
 
     L = rh._lib.lib()
-    wk = wl.make(args.workload) if args.workload != "stress_1024" else None
+    wk = make_workload(args.workload)
     a = wk["a"]
     m, k = a.shape
     n = wl.N_CLASSES
@@ -209,6 +277,13 @@ def main():
 
     copy = copy_probe(args.copy_probe) if args.copy_probe > 0 else None
 
+    others = None
+    if args.only == "" and not args.no_others:
+        others = {"single_line": other_config("single_line", (2,), args.steps, args.warmup),
+                  "a4_page": other_config("a4_page", (2, 3), args.steps, args.warmup),
+                  "fp32_64": other_config("fp32_64", (0, 3), args.steps, args.warmup),
+                  "stress_1024": other_config("stress_1024", (2,), max(3, args.steps // 4), 2)}
+
     cpu = None
     if not args.no_cpu and args.only == "":
         cpu = cpu_baseline(wk, qw.data, qw.scales, args.cpu_seconds)
@@ -243,6 +318,7 @@ def main():
             "unfused": unf,
             "probs_fused": probs,
             "cpu_baseline": cpu,
+            "other_configs": others,
         }
         if copy:
             line["copy_probe"] = copy
