@@ -847,13 +847,21 @@ static int vec_ok(const float* a, int64_t k) {
     return ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (k & 3) == 0) ? 1 : 0;
 }
 
-// Vocabulary chunks of the write-bound kernels: a multiple of 8 (one weight slice per
-// XCD), more only when there are too few row blocks to fill the GPU.
+// Vocabulary chunks of the write-bound kernels.  HBM write bandwidth falls with the
+// number of row segments written at once (measured on the logits layout, 30720 x 18710
+// fp32: 4.3 TB/s with one chunk per row, 3.0 with two, 2.6 with eight), so a large batch
+// walks each row in one pass; small batches split the vocabulary to fill the GPU.
 static int rows_nsplit(int64_t mblocks) {
-    int ns = 8;
-    while (mblocks * ns < 1024 && ns < 64) ns *= 2;
+    if (mblocks >= 128) return 1;
+    int ns = 1;
+    while (mblocks * ns < 256 && ns < 64) ns *= 2;
     return ns;
 }
+
+// Row-block slots of a rescue pass: its grid is sized before the number of guarded rows
+// is known (it is on the device), so it is kept small; each slot walks the row list in
+// strides.
+constexpr int kRescueSlots = 8;
 
 // Configuration that recomputes the rows flagged by the precision guard of `cfg`
 // (-1: the configuration has no guard).
@@ -890,7 +898,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     });
     if (e || !guarded) return e;
     // rescue: the flagged rows again, one more activation term, every column
-    const int slots = (int)std::min<int64_t>(mblocks, 64);
+    const int slots = (int)std::min<int64_t>(mblocks, kRescueSlots);
     const int rgrid = grid_blocks(slots, nsplit);
     return dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
@@ -947,7 +955,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
         // (with exact class indices)
         const int rrpb = rescue_rows_per_block(rcfg);
-        const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, 64);
+        const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, kRescueSlots);
         const int rgrid = grid_blocks(slots, nsplit);
         e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
             constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
