@@ -359,181 +359,6 @@ __global__ __launch_bounds__(256, 2) void rows_mfma_kernel(
     }
 }
 
-// ============================================================ online statistics epilogue
-// Rows of the MFMA = classes, columns = activation rows: lane (i, h) owns activation row
-// i and 16 classes n0 + 8*(r/4) + 4*h + (r%4), so a row's max/argmax/sum over its classes
-// needs no cross-lane traffic until the end of the chunk.  t = logit * log2(e) comes from
-// one fma with the record's scale*log2(e) and bias*log2(e).  The sum is kept relative to
-// `ref`, which stays 0 unless the row's maximum leaves [-64, 64]; then it follows the
-// maximum so the sum can neither overflow nor lose the maximum's term.
-template <int MB>
-__device__ __forceinline__ void stats_update(const f32x16 (&acc)[MB], const float* sl, const float* bl, int nrow0,
-                                             float (&best)[MB], float (&sum)[MB], float (&ref)[MB],
-                                             int (&bidx)[MB], bool& refzero) {
-    float t[MB][16], tmax[MB];
-    bool better[MB];
-    bool anyb = false;
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) t[b][r] = fmaf(acc[b][r], sl[r], bl[r]);
-        const float m01 = fmaxf(fmaxf(t[b][0], t[b][1]), t[b][2]);
-        const float m02 = fmaxf(fmaxf(t[b][3], t[b][4]), t[b][5]);
-        const float m03 = fmaxf(fmaxf(t[b][6], t[b][7]), t[b][8]);
-        const float m04 = fmaxf(fmaxf(t[b][9], t[b][10]), t[b][11]);
-        const float m05 = fmaxf(fmaxf(t[b][12], t[b][13]), t[b][14]);
-        tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
-        better[b] = tmax[b] > best[b];
-        anyb = anyb || better[b];
-    }
-    // Rare path (one uniform branch for all blocks): a new maximum.  Record its first
-    // index, and keep ref within 64 of the maximum.
-    if (__any(anyb)) {
-        bool shifted = false;
-#pragma unroll
-        for (int b = 0; b < MB; ++b) {
-            if (better[b]) {
-                int ri = 15;
-#pragma unroll
-                for (int r = 14; r >= 0; --r) ri = (t[b][r] == tmax[b]) ? r : ri;
-                best[b] = tmax[b];
-                bidx[b] = nrow0 + 8 * (ri >> 2) + (ri & 3);
-                if (best[b] > ref[b] + 64.0f || best[b] < ref[b] - 64.0f) {
-                    sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - best[b]);
-                    ref[b] = best[b];
-                }
-            }
-            shifted = shifted || ref[b] != 0.0f;
-        }
-        refzero = refzero && !__any(shifted);
-    }
-    float e[MB][16];
-    if (refzero) {
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) e[b][r] = __builtin_amdgcn_exp2f(t[b][r]);
-    } else {
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) e[b][r] = __builtin_amdgcn_exp2f(t[b][r] - ref[b]);
-    }
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) e[b][r] += e[b][r + 8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) e[b][r] += e[b][r + 4];
-        sum[b] += (e[b][0] + e[b][2]) + (e[b][1] + e[b][3]);
-    }
-}
-
-// Fused projection + softmax statistics.  Each workgroup: 4 waves x MB blocks of 32
-// activation rows, one vocabulary chunk; writes per-row partial (max, sum, argmax).
-template <int C, int G, int MB>
-__global__ __launch_bounds__(256, 2) void stats_mfma_kernel(
-    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
-    int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows,
-    const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
-    using GE = Geo<C, G>;
-    constexpr int RPB = 128 * MB;
-    extern __shared__ __align__(16) uint8_t lds[];
-
-    int mbi, chunk;
-    map_block(blockIdx.x, nsplit, &mbi, &chunk);
-    if (mbi >= mblocks) return;
-    const int t0 = chunk * tiles_per_chunk;
-    const int t1 = min(t0 + tiles_per_chunk, tiles);
-    const RowSource src{gather_rows, gather_rows ? *gather_count : 0};
-    const int64_t nblocks = gather_rows ? ((int64_t)src.count + RPB - 1) / RPB : mblocks;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    zero_blocks(lds, GE::BUF, GE::REC, tid);
-    const int lb = i * 16 + h * 512;
-
-    for (int64_t blk = mbi; blk < nblocks; blk += mblocks) {
-        const int64_t j0 = blk * RPB + wave * (32 * MB);
-        int64_t arow[MB];
-        bool valid[MB];
-        bf16x8 bf[MB][GE::S];
-#pragma unroll
-        for (int b = 0; b < MB; ++b) {
-            arow[b] = src.row(j0 + 32 * b + i, m, valid[b]);
-            float amax = 0.0f;
-#pragma unroll
-            for (int s = 0; s < GE::S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
-            if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
-        }
-
-        float best[MB], sum[MB], ref[MB];
-        int bidx[MB];
-#pragma unroll
-        for (int b = 0; b < MB; ++b) {
-            best[b] = -INFINITY;
-            sum[b] = 0.0f;
-            ref[b] = 0.0f;
-            bidx[b] = 0;
-        }
-        bool refzero = true;
-
-        if (t0 < t1) {
-            Stage<GE::REC> stg;
-            stg.load(rec + (size_t)t0 * GE::REC, tid);
-            __syncthreads();  // previous block's last tile is no longer being read
-            stg.store(lds, tid);
-            __syncthreads();
-
-            for (int t = t0; t < t1; ++t) {
-                const int cur = (t - t0) & 1;
-                const bool more = t + 1 < t1;
-                if (more) stg.load(rec + (size_t)(t + 1) * GE::REC, tid);
-                const uint8_t* buf = lds + cur * GE::BUF;
-                f32x16 acc[MB];
-#pragma unroll
-                for (int b = 0; b < MB; ++b) acc[b] = f32x16{};
-#pragma unroll
-                for (int s = 0; s < GE::S; ++s) {
-                    const bf16x8 wf = weight_frag<C, G>(buf, s, lb, i * 16, h);
-#pragma unroll
-                    for (int b = 0; b < MB; ++b)
-                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc[b], 0, 0, 0);
-                }
-                const float* ep = reinterpret_cast<const float*>(buf + GE::FRAG);
-                float sl[16], bl[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
-                    const f32x4 b4 = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        sl[4 * q + e] = s4[e];
-                        bl[4 * q + e] = b4[e];
-                    }
-                }
-                stats_update<MB>(acc, sl, bl, t * 32 + 4 * h, best, sum, ref, bidx, refzero);
-                if (more) stg.store(lds + (cur ^ 1) * GE::BUF, tid);
-                __syncthreads();
-            }
-        }
-
-        // lanes i and i+32 hold the same activation row: merge, then lanes 0-31 write.
-#pragma unroll
-        for (int b = 0; b < MB; ++b) {
-            RowStat mine{best[b], sum[b], ref[b], bidx[b]};
-            RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
-                          __shfl_xor(bidx[b], 32, 64)};
-            const RowStat r = stat_merge(mine, other);
-            if (h == 0 && valid[b]) {
-                p_best[(int64_t)chunk * m + arow[b]] = r.best;
-                p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
-                p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
-            }
-        }
-    }
-}
-
 // ============================================================ fused statistics, main pass
 // One piece of the epilogue of a tile (compile-time piece number P; MB blocks of 32
 // activation rows).  The pieces of a tile, in order:
@@ -637,11 +462,12 @@ __device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float*
 constexpr int kPrefetch = 2;
 constexpr int kRing = 4;  // LDS tile slots of the main statistics pass (a power of two)
 
-template <int C, int G, int MB>
+template <int C, int G, int MB, bool GATHER>
 __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows) {
+    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows,
+    const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
     constexpr int RPB = 128 * MB;
@@ -652,142 +478,153 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     if (mbi >= mblocks) return;
     const int t0 = chunk * tiles_per_chunk;
     const int t1 = min(t0 + tiles_per_chunk, tiles);
+    // one row block, or (GATHER) the row blocks of a device-side row list, mblocks apart
+    const RowSource src{GATHER ? gather_rows : nullptr, GATHER ? *gather_count : 0};
+    const int64_t blk_end = GATHER ? ((int64_t)src.count + RPB - 1) / RPB : (int64_t)mbi + 1;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    const int64_t mrow0 = (int64_t)mbi * RPB + wave * (32 * MB);
     if (tid < 32 * kRing)
         reinterpret_cast<u32x4*>(lds + (tid >> 5) * GE::BUF + GE::REC)[tid & 31] = u32x4{0, 0, 0, 0};
     const int lb = i * 16 + h * 512;
     // this lane's saved values of its best tile: [block][quad][lane] x 4 floats
     f32x4* save = reinterpret_cast<f32x4*>(lds + kRing * GE::BUF) + wave * (MB * 4 * 64) + lane;
 
-    int64_t arow[MB];
-    bool valid[MB];
-    bf16x8 bf[MB][S];
+    auto row_block = [&](int64_t blk) {
+        const int64_t mrow0 = blk * RPB + wave * (32 * MB);
+        int64_t arow[MB];
+        bool valid[MB];
+        bf16x8 bf[MB][S];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        arow[b] = mrow0 + 32 * b + i;
-        valid[b] = arow[b] < m;
-        float amax = 0.0f;
+        for (int b = 0; b < MB; ++b) {
+            arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
+            float amax = 0.0f;
 #pragma unroll
-        for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
-        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
-    }
-
-    float best[MB], sum[MB], ref[MB];
-    int bt[MB];
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        best[b] = -INFINITY;
-        sum[b] = 0.0f;
-        ref[b] = 0.0f;
-        bt[b] = -1;
-    }
-
-    if (t0 < t1) {
-        constexpr int kOps = stage_direct_min_ops<GE::REC>();
-#pragma unroll
-        for (int x = 0; x < kRing - 1; ++x)
-            stage_direct<GE::REC>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
-        ring_barrier<kOps>();  // tiles t0 and t0+1 are in LDS
-        f32x16 acc_a[MB], acc_b[MB];
-#pragma unroll
-        for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const bf16x8 wf = weight_frag<C, G>(lds, s, lb, i * 16, h);
-#pragma unroll
-            for (int b = 0; b < MB; ++b) acc_a[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc_a[b], 0, 0, 0);
+            for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
+            if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
         }
-        // One tile: start loading tile j+3, the MFMAs of tile j+1 into accM interleaved
-        // with the epilogue of tile j on accE, the saves of a raised maximum, the rare
-        // re-reference, the barrier (after which tile j+2 is in LDS).  Past the end the
-        // MFMAs read a stale ring slot and the load repeats the last tile: harmless, and it
-        // keeps the body branch-free.
-        auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
-            const unsigned rel = (unsigned)(j - t0);
-            stage_direct<GE::REC>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
-                                  lds + ((rel + kRing - 1) & (kRing - 1)) * GE::BUF, tid);
-            const uint8_t* bufn = lds + ((rel + 1) & (kRing - 1)) * GE::BUF;
-            const float* ep = reinterpret_cast<const float*>(lds + (rel & (kRing - 1)) * GE::BUF + GE::FRAG);
-            f32x4 cs[2], cb[2];
+
+        float best[MB], sum[MB], ref[MB];
+        int bt[MB];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                cs[q] = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
-                cb[q] = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+        for (int b = 0; b < MB; ++b) {
+            best[b] = -INFINITY;
+            sum[b] = 0.0f;
+            ref[b] = 0.0f;
+            bt[b] = -1;
+        }
+
+        if (t0 < t1) {
+            constexpr int kOps = stage_direct_min_ops<GE::REC>();
+            if constexpr (GATHER) ring_barrier<0>();  // a previous row block's tiles are no longer read
+#pragma unroll
+            for (int x = 0; x < kRing - 1; ++x)
+                stage_direct<GE::REC>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
+            ring_barrier<kOps>();  // tiles t0 and t0+1 are in LDS
+            f32x16 acc_a[MB], acc_b[MB];
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const bf16x8 wf = weight_frag<C, G>(lds, s, lb, i * 16, h);
+#pragma unroll
+                for (int b = 0; b < MB; ++b) acc_a[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], acc_a[b], 0, 0, 0);
             }
-            EpiState<MB> st;
-            st.need = false;
+            // One tile: start loading tile j+3, the MFMAs of tile j+1 into accM interleaved
+            // with the epilogue of tile j on accE, the saves of a raised maximum, the rare
+            // re-reference, the barrier (after which tile j+2 is in LDS).  Past the end the
+            // MFMAs read a stale ring slot and the load repeats the last tile: harmless, and it
+            // keeps the body branch-free.
+            auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
+                const unsigned rel = (unsigned)(j - t0);
+                stage_direct<GE::REC>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
+                                      lds + ((rel + kRing - 1) & (kRing - 1)) * GE::BUF, tid);
+                const uint8_t* bufn = lds + ((rel + 1) & (kRing - 1)) * GE::BUF;
+                const float* ep = reinterpret_cast<const float*>(lds + (rel & (kRing - 1)) * GE::BUF + GE::FRAG);
+                f32x4 cs[2], cb[2];
 #pragma unroll
-            for (int b = 0; b < MB; ++b) accM[b] = f32x16{};
-            // weight fragments are read kPrefetch MFMA steps ahead of their use, so a wave
-            // never waits on LDS with epilogue work queued behind the wait
-            bf16x8 wq[kPrefetch];
+                for (int q = 0; q < 2; ++q) {
+                    cs[q] = *reinterpret_cast<const f32x4*>(ep + 8 * q + 4 * h);
+                    cb[q] = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * q + 4 * h);
+                }
+                EpiState<MB> st;
+                st.need = false;
 #pragma unroll
-            for (int x = 0; x < kPrefetch; ++x) wq[x] = weight_frag<C, G>(bufn, x < S ? x : S - 1, lb, i * 16, h);
-            [&]<int... s>(std::integer_sequence<int, s...>) {
-                ([&] {
-                    epi_pieces_of_step<S, s, MB>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
+                for (int b = 0; b < MB; ++b) accM[b] = f32x16{};
+                // weight fragments are read kPrefetch MFMA steps ahead of their use, so a wave
+                // never waits on LDS with epilogue work queued behind the wait
+                bf16x8 wq[kPrefetch];
 #pragma unroll
-                    for (int b = 0; b < MB; ++b)
-                        accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[b][s], accM[b], 0, 0, 0);
-                    if constexpr (s + kPrefetch < S)
-                        wq[s % kPrefetch] = weight_frag<C, G>(bufn, s + kPrefetch, lb, i * 16, h);
-                    __builtin_amdgcn_sched_barrier(0);
-                }(), ...);
-            }(std::make_integer_sequence<int, S>{});
-            if (__any(st.need)) {
+                for (int x = 0; x < kPrefetch; ++x) wq[x] = weight_frag<C, G>(bufn, x < S ? x : S - 1, lb, i * 16, h);
+                [&]<int... s>(std::integer_sequence<int, s...>) {
+                    ([&] {
+                        epi_pieces_of_step<S, s, MB>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
 #pragma unroll
-                for (int b = 0; b < MB; ++b) {
-                    if (best[b] != -INFINITY && __builtin_fabsf(best[b] - ref[b]) > 64.0f) {
-                        const float nr = best[b];
-                        sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - nr);
-                        float s = 0.0f;
+                        for (int b = 0; b < MB; ++b)
+                            accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[b][s], accM[b], 0, 0, 0);
+                        if constexpr (s + kPrefetch < S)
+                            wq[s % kPrefetch] = weight_frag<C, G>(bufn, s + kPrefetch, lb, i * 16, h);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }(), ...);
+                }(std::make_integer_sequence<int, S>{});
+                if (__any(st.need)) {
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(accE[b][r] - nr);
-                        st.tsum[b] = s;
-                        ref[b] = nr;
+                    for (int b = 0; b < MB; ++b) {
+                        if (best[b] != -INFINITY && __builtin_fabsf(best[b] - ref[b]) > 64.0f) {
+                            const float nr = best[b];
+                            sum[b] = (sum[b] == 0.0f) ? 0.0f : sum[b] * __builtin_amdgcn_exp2f(ref[b] - nr);
+                            float s = 0.0f;
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(accE[b][r] - nr);
+                            st.tsum[b] = s;
+                            ref[b] = nr;
+                        }
                     }
                 }
-            }
 #pragma unroll
-            for (int b = 0; b < MB; ++b) sum[b] += st.tsum[b];
-            ring_barrier<kOps>();
-        };
-        int j = t0;
-        for (; j + 1 < t1; j += 2) {
-            step(j, acc_a, acc_b);
-            step(j + 1, acc_b, acc_a);
+                for (int b = 0; b < MB; ++b) sum[b] += st.tsum[b];
+                ring_barrier<kOps>();
+            };
+            int j = t0;
+            for (; j + 1 < t1; j += 2) {
+                step(j, acc_a, acc_b);
+                step(j + 1, acc_b, acc_a);
+            }
+            if (j < t1) step(j, acc_a, acc_b);
+            // the ring's last loads (repeats of the last tile) land before the workgroup ends
+            __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
         }
-        if (j < t1) step(j, acc_a, acc_b);
-        // the ring's last loads (repeats of the last tile) land before the workgroup ends
-        __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
-    }
 
-    // first class of the best tile reaching the maximum; then lanes i and i+32 (same
-    // activation row) merge and lanes 0-31 write.
+        // first class of the best tile reaching the maximum; then lanes i and i+32 (same
+        // activation row) merge and lanes 0-31 write.
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        int cls = 0;
-        if (bt[b] >= 0) {
-            int r0 = 16;
+        for (int b = 0; b < MB; ++b) {
+            int cls = 0;
+            if (bt[b] >= 0) {
+                int r0 = 16;
 #pragma unroll
-            for (int q = 3; q >= 0; --q) {
-                const f32x4 v = save[(b * 4 + q) * 64];
+                for (int q = 3; q >= 0; --q) {
+                    const f32x4 v = save[(b * 4 + q) * 64];
 #pragma unroll
-                for (int e = 3; e >= 0; --e) r0 = (v[e] == best[b]) ? 4 * q + e : r0;
+                    for (int e = 3; e >= 0; --e) r0 = (v[e] == best[b]) ? 4 * q + e : r0;
+                }
+                cls = bt[b] * 32 + (r0 < 16 ? 8 * (r0 >> 2) + 4 * h + (r0 & 3) : 0);
             }
-            cls = bt[b] * 32 + (r0 < 16 ? 8 * (r0 >> 2) + 4 * h + (r0 & 3) : 0);
+            RowStat mine{best[b], sum[b], ref[b], cls};
+            RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
+                          __shfl_xor(cls, 32, 64)};
+            const RowStat r = stat_merge(mine, other);
+            if (h == 0 && valid[b]) {
+                p_best[(int64_t)chunk * m + arow[b]] = r.best;
+                p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
+                p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
+            }
         }
-        RowStat mine{best[b], sum[b], ref[b], cls};
-        RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
-                      __shfl_xor(cls, 32, 64)};
-        const RowStat r = stat_merge(mine, other);
-        if (h == 0 && valid[b]) {
-            p_best[(int64_t)chunk * m + arow[b]] = r.best;
-            p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
-            p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
-        }
+    };
+    if constexpr (GATHER) {
+        for (int64_t blk = mbi; blk < blk_end; blk += mblocks) row_block(blk);
+    } else {
+        (void)blk_end;
+        row_block(mbi);
     }
 }
 
@@ -814,15 +651,29 @@ int stats_rows_per_block_mfma(int cfg) {
         default: return 128 * mb_of<CFG_F3>();
     }
 }
-static int rescue_rows_per_block(int cfg) { return 128 * (cfg == CFG_Q3 || cfg == CFG_F3 ? 1 : 2); }
 
-// Vocabulary chunks per row block: at least 8 (one slice of the weights per XCD L2), more
-// when there are too few row blocks to give every CU two workgroups.
-int stats_nsplit(int64_t m, int rows_per_block) {
+// Vocabulary chunks per row block.  The grid runs in rounds of kStatsSlots workgroups
+// (2 per CU on the 256 CUs of an MI355X), and a workgroup costs a fixed start and finish
+// (its rows' activations, the pipeline fill, the partials) worth about kChunkFixedTiles
+// tiles of the main loop (measured on the MI355X: 30720 rows run 5% faster in 4 chunks of
+// 147 tiles, one round, than in 8 chunks of 74, two rounds).  The chunk count from 4 to
+// 64 minimising rounds x (fixed + tiles per chunk) is taken.  At least 4 chunks keep each
+// XCD's slice of the weight records (the chunks of workgroup id mod 8) within its L2.
+constexpr int64_t kStatsSlots = 512;
+constexpr int64_t kChunkFixedTiles = 8;
+int stats_nsplit(int64_t m, int rows_per_block, int tiles) {
     const int64_t mblocks = (m + rows_per_block - 1) / rows_per_block;
-    int ns = 8;
-    while (mblocks * ns < 512 && ns < 64) ns *= 2;
-    return ns;
+    int best = 4;
+    int64_t best_cost = -1;
+    for (int ns = 4; ns <= 64; ns *= 2) {
+        const int64_t rounds = (mblocks * ns + kStatsSlots - 1) / kStatsSlots;
+        const int64_t cost = rounds * (kChunkFixedTiles + (tiles + ns - 1) / ns);
+        if (best_cost < 0 || cost < best_cost) {
+            best = ns;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 template <typename F>
@@ -859,9 +710,10 @@ static int rows_nsplit(int64_t mblocks) {
 }
 
 // Row-block slots of a rescue pass: its grid is sized before the number of guarded rows
-// is known (it is on the device), so it is kept small; each slot walks the row list in
-// strides.
-constexpr int kRescueSlots = 8;
+// is known (it is on the device); each slot walks the row list in strides.  An empty
+// rescue costs the launch whatever the grid, and a heavy one (a head with large weight
+// outliers guards many rows) needs the whole GPU.
+constexpr int kRescueSlots = 128;
 
 // Configuration that recomputes the rows flagged by the precision guard of `cfg`
 // (-1: the configuration has no guard).
@@ -944,9 +796,10 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     }
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        stats_main_kernel<C, G, mb_of<C>()><<<grid, 256, main_lds_bytes<C, G>(), st>>>(
+        stats_main_kernel<C, G, mb_of<C>(), false><<<grid, 256, main_lds_bytes<C, G>(), st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
-            guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr);
+            guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
+            nullptr, nullptr);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
@@ -954,15 +807,14 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     if (guarded) {
         // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
         // (with exact class indices)
-        const int rrpb = rescue_rows_per_block(rcfg);
+        const int rrpb = stats_rows_per_block_mfma(rcfg);
         const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, kRescueSlots);
         const int rgrid = grid_blocks(slots, nsplit);
         e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
             constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-            constexpr int LDS = 2 * Geo<C, G>::BUF;
-            stats_mfma_kernel<C, G, mb_of<C>()><<<rgrid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, nsplit,
-                                                                         tpc, slots, p_best, p_sum, p_idx, 0.0f,
-                                                                         nullptr, nullptr, guard->rows, guard->count);
+            stats_main_kernel<C, G, mb_of<C>(), true><<<rgrid, 256, main_lds_bytes<C, G>(), st>>>(
+                a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, slots, p_best, p_sum, p_idx, 0.0f, nullptr, nullptr,
+                guard->rows, guard->count);
             PPOCR_HIP(hipGetLastError());
             return PPOCR_OK;
         });

@@ -40,7 +40,7 @@ int launch_pack_int8(const float* w_t, int64_t n, int64_t k, int8_t* q, float* s
 int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                        int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.
-int stats_nsplit(int64_t m, int rows_per_block);
+int stats_nsplit(int64_t m, int rows_per_block, int tiles);
 int stats_rows_per_block_mfma(int cfg);
 // Main pass, rescue of the guarded rows, then one wave per row merges the partials and
 // resolves the argmax: idx, maxprob (1/sum) and, when non-null, row_max (log2-domain

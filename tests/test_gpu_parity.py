@@ -286,6 +286,30 @@ def test_decode_dev_matches_unfused_path(orc, rh, head, rhead):
     assert np.abs(probs_rows - ref_p).max() < TOL
 
 
+def test_large_batch_logits_and_probs_single_pass(orc, rh, head, rhead):
+    """m = 16461 rows: enough row blocks for the writers to walk each row's vocabulary in
+    one pass, with a partial last row block; logits and probabilities of sampled rows
+    (including the last 77) against the oracle."""
+    rng = np.random.default_rng(21)
+    m = 16384 + 77
+    a = rng.standard_normal((m, 120), dtype=np.float32)
+    sample = np.unique(np.concatenate([rng.choice(m - 77, 183, replace=False), np.arange(m - 77, m)]))
+    print(f"large-batch logits m={m}", flush=True)
+    got = rhead.logits(a, 2)
+    ref = orc.matmul_quantized_b(a[sample], head["q"], head["s"], head["bias"])
+    err = np.abs(got[sample] - ref).max()
+    print(f"  max|logits gpu-oracle| = {err:.3e}")
+    assert err < TOL
+    del got
+    print(f"large-batch probs m={m}", flush=True)
+    gotp = rhead.probs(a, 2)
+    refp = orc.rechead_lines(a[sample], split_lines(sample.size), head["q"], head["s"], head["bias"],
+                             want_probs=True)["probs"]
+    errp = np.abs(gotp[sample] - refp).max()
+    print(f"  max|probs gpu-oracle| = {errp:.3e}")
+    assert errp < TOL
+
+
 def test_stress_1024_fused(orc, rh):
     """m = 245760, zero-weight rows, +-5 outliers, 1% rows x50, 2% near-tie rows."""
     from ppocr_rechead import workloads as wl
