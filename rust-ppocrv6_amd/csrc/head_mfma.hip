@@ -179,38 +179,10 @@ __device__ __forceinline__ void guard_append(float amax, float amax_limit, bool 
     }
 }
 
-// Global -> registers -> LDS staging of one tile record by 256 threads (16-byte chunks).
-// Every register is loaded unconditionally (indices clamped in bounds) so the staging
-// stays in registers and the load latency hides behind the MFMAs of the current tile.
-template <int REC, int NT = 256>
-struct Stage {
-    static constexpr int CH = REC / 16;
-    static constexpr int PER = (CH + NT - 1) / NT;
-    static_assert(PER >= 1 && PER <= 4, "tile record too large");
-    u32x4 v0, v1, v2, v3;
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ src, int tid) {
-        const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
-        v0 = s4[min(tid, CH - 1)];
-        if constexpr (PER > 1) v1 = s4[min(tid + NT, CH - 1)];
-        if constexpr (PER > 2) v2 = s4[min(tid + 2 * NT, CH - 1)];
-        if constexpr (PER > 3) v3 = s4[min(tid + 3 * NT, CH - 1)];
-    }
-    __device__ __forceinline__ void store(uint8_t* dst, int tid) const {
-        u32x4* d4 = reinterpret_cast<u32x4*>(dst);
-        if (CH >= NT || tid < CH) d4[tid] = v0;
-        if constexpr (PER > 1)
-            if (CH >= 2 * NT || tid + NT < CH) d4[tid + NT] = v1;
-        if constexpr (PER > 2)
-            if (CH >= 3 * NT || tid + 2 * NT < CH) d4[tid + 2 * NT] = v2;
-        if constexpr (PER > 3)
-            if (CH >= 4 * NT || tid + 3 * NT < CH) d4[tid + 3 * NT] = v3;
-    }
-};
-
-// Global -> LDS staging of one tile record without registers: each wave issues direct
-// 16-byte-per-lane loads into LDS (wave w, instruction x covers 16-byte chunks
-// x*NT + 64*w .. +63).  Completion is awaited by the workgroup barrier that follows
-// (its fence waits for the wave's outstanding loads), before any wave reads the slot.
+// Global -> LDS staging of one tile record by all NT threads of a workgroup, without
+// registers: each wave issues direct 16-byte-per-lane loads into LDS (wave w, instruction
+// x covers 16-byte chunks x*NT + 64*w .. +63).  The loads count in each wave's vmcnt;
+// ring_barrier below waits for them before any wave reads the slot.
 template <int REC, int NT = 256>
 __device__ __forceinline__ void stage_direct(const uint8_t* __restrict__ src, uint8_t* dst, int tid) {
     constexpr int CH = REC / 16;
@@ -236,6 +208,13 @@ constexpr int stage_direct_min_ops() {
     return (REC / 16) / NT;
 }
 
+// Wait until at most N of this wave's global memory operations are outstanding.  They
+// complete in issue order, so every older one has completed.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));  // vmcnt(N) only
+}
 // Workgroup barrier for a ring whose newest N direct loads per wave may still be in
 // flight: wait until at most N of this wave's loads are outstanding (so every older tile
 // is in LDS) and all of its LDS accesses are done, then synchronise.  The barrier is
@@ -243,120 +222,9 @@ constexpr int stage_direct_min_ops() {
 // access on its side, and adds no wait for the newest loads (a fence would wait for all).
 template <int N>
 __device__ __forceinline__ void ring_barrier() {
-    static_assert(N >= 0 && N < 16, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0x0 << 8));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));  // vmcnt(N) lgkmcnt(0)
     asm volatile("s_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ void zero_blocks(uint8_t* lds, int buf_bytes, int rec_bytes, int tid) {
-    if (tid < 64) reinterpret_cast<u32x4*>(lds + (tid >> 5) * buf_bytes + rec_bytes)[tid & 31] = u32x4{0, 0, 0, 0};
-}
-
-// ============================================================ logits: out = (a w^T)*scale + bias
-// Rows of the MFMA = activation rows, columns = classes: a lane owns one class of each
-// tile, so a store instruction writes 32 consecutive classes (128 bytes) in each of two
-// rows.  Each workgroup (4 waves x 32 rows) walks one vocabulary chunk.
-template <int C, int G, int EPI>  // EPI 0: logits, 1: probabilities
-__global__ __launch_bounds__(256, 2) void rows_mfma_kernel(
-    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles, int n,
-    int nsplit, int tiles_per_chunk, int mblocks, const float* __restrict__ row_max,
-    const float* __restrict__ row_inv, float* __restrict__ out, float amax_limit, int* __restrict__ guard_count,
-    int* __restrict__ guard_rows, const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
-    using GE = Geo<C, G>;
-    extern __shared__ __align__(16) uint8_t lds[];
-
-    int mbi, chunk;
-    map_block(blockIdx.x, nsplit, &mbi, &chunk);
-    if (mbi >= mblocks) return;
-    const int t0 = chunk * tiles_per_chunk;
-    const int t1 = min(t0 + tiles_per_chunk, tiles);
-    if (t0 >= t1) return;
-    const RowSource src{gather_rows, gather_rows ? *gather_count : 0};
-    const int64_t nblocks = gather_rows ? ((int64_t)src.count + 127) / 128 : mblocks;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    zero_blocks(lds, GE::BUF, GE::REC, tid);
-    const int lb = i * 16 + h * 512;
-
-    for (int64_t blk = mbi; blk < nblocks; blk += mblocks) {
-        const int64_t j0 = blk * 128 + wave * 32;
-        bool valid;
-        const int64_t arow = src.row(j0 + i, m, valid);
-        float amax = 0.0f;
-        bf16x8 bf[GE::S];
-#pragma unroll
-        for (int s = 0; s < GE::S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec != 0, s, h, amax);
-        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid, arow, h, guard_count, guard_rows);
-
-        // rows of this lane's 16 accumulators (r -> activation-row slot 8*(r/4) + 4*h + (r%4))
-        int64_t orow[16];
-        bool ovalid[16];
-        bool all_valid = true;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            bool v;
-            orow[r] = src.row(j0 + 8 * (r >> 2) + 4 * h + (r & 3), m, v);
-            ovalid[r] = v;
-            all_valid = all_valid && v;
-        }
-        all_valid = __all(all_valid);
-        float rmax[16], rinv[16];
-        if (EPI == 1) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                rmax[r] = ovalid[r] ? row_max[orow[r]] : 0.0f;
-                rinv[r] = ovalid[r] ? row_inv[orow[r]] : 0.0f;
-            }
-        }
-
-        Stage<GE::REC> stg;
-        stg.load(rec + (size_t)t0 * GE::REC, tid);
-        __syncthreads();  // previous block's last tile is no longer being read
-        stg.store(lds, tid);
-        __syncthreads();
-
-        for (int t = t0; t < t1; ++t) {
-            const int cur = (t - t0) & 1;
-            const bool more = t + 1 < t1;
-            if (more) stg.load(rec + (size_t)(t + 1) * GE::REC, tid);
-            const uint8_t* buf = lds + cur * GE::BUF;
-            f32x16 acc = {};
-#pragma unroll
-            for (int s = 0; s < GE::S; ++s)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[s], weight_frag<C, G>(buf, s, lb, i * 16, h), acc, 0,
-                                                              0, 0);
-            const float* ep = reinterpret_cast<const float*>(buf + GE::FRAG);
-            float c0, c1;
-            if (EPI == 0) {
-                c0 = ep[64 + i];  // scale
-                c1 = ep[96 + i];  // bias
-            } else {
-                c0 = ep[i];       // scale * log2(e)
-                c1 = ep[32 + i];  // bias * log2(e)
-            }
-            const int col = t * 32 + i;
-            float v[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if (EPI == 0) {
-#pragma clang fp contract(off)
-                    v[r] = acc[r] * c0 + c1;  // (sum * scale) + bias, two roundings (src/ops/matmul.rs:1396-1409)
-                } else {
-                    v[r] = __builtin_amdgcn_exp2f(fmaf(acc[r], c0, c1) - rmax[r]) * rinv[r];
-                }
-            }
-            if (all_valid && t * 32 + 32 <= n) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) out[orow[r] * n + col] = v[r];
-            } else if (col < n) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (ovalid[r]) out[orow[r] * n + col] = v[r];
-            }
-            if (more) stg.store(lds + (cur ^ 1) * GE::BUF, tid);
-            __syncthreads();
-        }
-    }
 }
 
 // ============================================================ fused statistics, main pass
@@ -628,6 +496,202 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     }
 }
 
+constexpr int kWriterWaves = 4;  // consumer waves of the writer, 32 rows each
+
+// ============================================================ logits / probabilities writer
+// One producer wave loads weight tiles from global memory straight into LDS; the consumer
+// waves compute and store.  Every access by one wave to global memory counts in its one
+// in-order vmcnt, so a wave that both stored results and loaded tiles would wait for its
+// own stores each time it waited for a tile.  Here the producer never stores, and the
+// consumers never wait for memory: their stores stay in flight while they compute the
+// next tiles.  Direct loads of one wave (64 lanes x 16 bytes per instruction):
+template <int REC>
+__device__ __forceinline__ void stage_wave(const uint8_t* __restrict__ src, uint8_t* dst, int lane) {
+    constexpr int CH = REC / 16;
+    constexpr int PER = (CH + 63) / 64;
+    static_assert(REC % 16 == 0, "tile record size");
+#pragma unroll
+    for (int x = 0; x < PER; ++x) {
+        // the last instruction of a record that is not a multiple of 1 KiB has some lanes off,
+        // never all of them, so each instruction counts once in vmcnt
+        if (CH % 64 == 0 || x * 64 + lane < CH)
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src + (size_t)(x * 64 + lane) * 16),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(dst + (size_t)x * 1024)),
+                16, 0, 0);
+    }
+}
+template <int REC>
+constexpr int stage_wave_ops() {
+    return (REC / 16 + 63) / 64;
+}
+__device__ __forceinline__ void barrier_lds() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Ring depth of the writer: tiles held in LDS, limited by the vmcnt range of the
+// producer's wait (R - 2 tiles of loads in flight).
+template <int REC>
+constexpr int writer_ring() {
+    return 2 + 63 / stage_wave_ops<REC>() < 8 ? 2 + 63 / stage_wave_ops<REC>() : 8;
+}
+
+// Projection writing logits (EPI 0) or softmax probabilities (EPI 1).  A workgroup owns
+// 32 * NC activation rows.  Waves 0..NC-1 are consumers, one 32-row block each; wave NC is
+// the producer: it keeps a ring of R weight tiles in LDS, R - 1 tiles ahead of the
+// consumers, so every tile read from L2 serves 32 * NC rows.  Each step all consumers
+// take the same tile and write its 32 classes of their rows, rows front to back.
+// Orientation: rows of the MFMA = activation rows, columns = classes; a lane holds one
+// class of 16 rows, so each store instruction writes 32 consecutive classes of two rows.
+// `gather_rows`: the rows are entries of a device list (the rescue of guarded rows); a
+// workgroup then takes several row blocks and the producer streams the tiles once per block.
+template <int C, int G, int EPI, bool GATHER>
+__global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
+    const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles, int n,
+    int nsplit, int tiles_per_chunk, int mblocks, const float* __restrict__ row_max,
+    const float* __restrict__ row_inv, float* __restrict__ out, float amax_limit, int* __restrict__ guard_count,
+    int* __restrict__ guard_rows, const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
+    using GE = Geo<C, G>;
+    constexpr int S = GE::S;
+    constexpr int NC = kWriterWaves;
+    constexpr int R = writer_ring<GE::REC>();
+    constexpr int ROWS = 32 * NC;
+    extern __shared__ __align__(16) uint8_t lds[];  // [R tiles] x BUF
+
+    int mbi, chunk;
+    map_block(blockIdx.x, nsplit, &mbi, &chunk);
+    if (mbi >= mblocks) return;
+    const int t0 = chunk * tiles_per_chunk;
+    const int t1 = min(t0 + tiles_per_chunk, tiles);
+    if (t0 >= t1) return;
+    const RowSource src{GATHER ? gather_rows : nullptr, GATHER ? *gather_count : 0};
+    const int64_t blk_end = GATHER ? ((int64_t)src.count + ROWS - 1) / ROWS : (int64_t)mbi + 1;
+    const int64_t nblk = (blk_end - mbi + mblocks - 1) / mblocks;  // row blocks of this workgroup
+    if (nblk <= 0) return;
+    const int ntiles = t1 - t0;
+    const int64_t total = nblk * ntiles;
+
+    const int tid = threadIdx.x, lane = tid & 63, i = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    if (wave == NC) {
+        // ---- producer: the g-th tile of the sequence goes to ring slot g % R
+        constexpr int kOps = stage_wave_ops<GE::REC>();
+        int pt = t0, pslot = 0;  // next tile to stage and its ring slot
+        auto stage_next = [&] {
+            stage_wave<GE::REC>(rec + (size_t)pt * GE::REC, lds + pslot * GE::BUF, lane);
+            pt = pt + 1 == t1 ? t0 : pt + 1;
+            pslot = pslot + 1 == R ? 0 : pslot + 1;
+        };
+#pragma unroll
+        for (int g = 0; g < R - 1; ++g) stage_next();
+        vm_wait<kOps * (R - 2)>();  // tile 0 is in LDS
+        barrier_lds();
+        for (int64_t g = 0; g < total; ++g) {
+            // tile g + R - 1 goes to the slot read at step g - 1, which every consumer has
+            // finished; past the end the loads repeat tiles into slots nobody reads
+            stage_next();
+            vm_wait<kOps * (R - 2)>();  // tile g + 1 is in LDS
+            barrier_lds();
+        }
+        vm_wait<0>();  // the ring's last loads land before the workgroup ends
+        return;
+    }
+
+    // ---- consumers
+    // the zero block after each of the R slots
+    for (int x = tid >> 5; x < R; x += 2 * NC)
+        reinterpret_cast<u32x4*>(lds + x * GE::BUF + GE::REC)[tid & 31] = u32x4{0, 0, 0, 0};
+    barrier_lds();  // zero blocks written; tile 0 is in LDS
+    int cslot = 0;  // ring slot of the current tile
+    auto row_block = [&](int64_t blk) {
+        const int64_t j0 = blk * ROWS + wave * 32;
+        bool valid;
+        const int64_t arow = src.row(j0 + i, m, valid);
+        float amax = 0.0f;
+        bf16x8 bf[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec != 0, s, h, amax);
+        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid, arow, h, guard_count, guard_rows);
+        // rows of this lane's 16 accumulators (r -> row slot 8*(r/4) + 4*h + (r%4))
+        int64_t orow[16];
+        bool ovalid[16];
+        bool all_valid = true;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            bool v;
+            orow[r] = src.row(j0 + 8 * (r >> 2) + 4 * h + (r & 3), m, v);
+            ovalid[r] = v;
+            all_valid = all_valid && v;
+        }
+        all_valid = __all(all_valid);
+        float rmax[16], rinv[16];
+        if constexpr (EPI == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                rmax[r] = ovalid[r] ? row_max[orow[r]] : 0.0f;
+                rinv[r] = ovalid[r] ? row_inv[orow[r]] : 0.0f;
+            }
+        }
+
+        for (int t = t0; t < t1; ++t) {
+            const uint8_t* buf = lds + cslot * GE::BUF;
+            cslot = cslot + 1 == R ? 0 : cslot + 1;
+            // weight fragments are read kAhead MFMA steps ahead of their use, so the LDS reads
+            // overlap instead of each MFMA waiting on its own
+            constexpr int kAhead = S < 8 ? S : 8;
+            bf16x8 wq[kAhead];
+#pragma unroll
+            for (int x = 0; x < kAhead; ++x) wq[x] = weight_frag<C, G>(buf, x, i * 16 + h * 512, i * 16, h);
+            f32x16 acc = {};
+            [&]<int... st>(std::integer_sequence<int, st...>) {
+                ([&] {
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[st], wq[st % kAhead], acc, 0, 0, 0);
+                    if constexpr (st + kAhead < S)
+                        wq[st % kAhead] = weight_frag<C, G>(buf, st + kAhead, i * 16 + h * 512, i * 16, h);
+                    __builtin_amdgcn_sched_barrier(0);
+                }(), ...);
+            }(std::make_integer_sequence<int, S>{});
+            const float* ep = reinterpret_cast<const float*>(buf + GE::FRAG);
+            float c0, c1;
+            if constexpr (EPI == 0) {
+                c0 = ep[64 + i];  // scale
+                c1 = ep[96 + i];  // bias
+            } else {
+                c0 = ep[i];       // scale * log2(e)
+                c1 = ep[32 + i];  // bias * log2(e)
+            }
+            const int col = t * 32 + i;
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if constexpr (EPI == 0) {
+#pragma clang fp contract(off)
+                    v[r] = acc[r] * c0 + c1;  // (sum * scale) + bias, two roundings (src/ops/matmul.rs:1396-1409)
+                } else {
+                    v[r] = __builtin_amdgcn_exp2f(fmaf(acc[r], c0, c1) - rmax[r]) * rinv[r];
+                }
+            }
+            if (all_valid && t * 32 + 32 <= n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) out[orow[r] * n + col] = v[r];
+            } else if (col < n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (ovalid[r]) out[orow[r] * n + col] = v[r];
+            }
+            barrier_lds();  // this slot is read; tile g + 1 is in LDS
+        }
+    };
+    if constexpr (GATHER) {
+        for (int64_t blk = mbi; blk < blk_end; blk += mblocks) row_block(blk);
+    } else {
+        row_block(mbi);
+    }
+}
+
 __global__ void guard_reset_kernel(int* guard_count) { *guard_count = 0; }
 
 // ============================================================ launchers
@@ -698,14 +762,14 @@ static int vec_ok(const float* a, int64_t k) {
     return ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (k & 3) == 0) ? 1 : 0;
 }
 
-// Vocabulary chunks of the write-bound kernels.  HBM write bandwidth falls with the
-// number of row segments written at once (measured on the logits layout, 30720 x 18710
-// fp32: 4.3 TB/s with one chunk per row, 3.0 with two, 2.6 with eight), so a large batch
-// walks each row in one pass; small batches split the vocabulary to fill the GPU.
+// Vocabulary chunks of the writer (128-row workgroups, one per CU).  HBM write bandwidth
+// falls with the number of row segments written at once (measured on the logits layout,
+// 30720 x 18710 fp32: 4.3 TB/s with one chunk per row, 3.0 with two, 2.6 with eight), so a
+// batch with enough rows to fill the GPU walks each row's vocabulary in one pass; small
+// batches split the vocabulary to fill it.
 static int rows_nsplit(int64_t mblocks) {
-    if (mblocks >= 128) return 1;
     int ns = 1;
-    while (mblocks * ns < 256 && ns < 64) ns *= 2;
+    while (mblocks * ns < 192 && ns < 64) ns *= 2;
     return ns;
 }
 
@@ -724,7 +788,8 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
                        const Guard* guard, hipStream_t st) {
     if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: tile geometry mismatch");
     if (m <= 0 || n <= 0) return PPOCR_OK;
-    const int64_t mblocks = (m + 127) / 128;
+    constexpr int ROWS = 32 * kWriterWaves;
+    const int64_t mblocks = (m + ROWS - 1) / ROWS;
     if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
     const int nsplit = rows_nsplit(mblocks);
     const int tpc = (tg.tiles + nsplit - 1) / nsplit;
@@ -739,9 +804,9 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     }
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        constexpr int LDS = 2 * Geo<C, G>::BUF;
-        auto kern = epi == 0 ? rows_mfma_kernel<C, G, 0> : rows_mfma_kernel<C, G, 1>;
-        kern<<<(unsigned)grid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, (int)mblocks,
+        constexpr int LDS = writer_ring<Geo<C, G>::REC>() * Geo<C, G>::BUF;
+        auto kern = epi == 0 ? rows_w_kernel<C, G, 0, false> : rows_w_kernel<C, G, 1, false>;
+        kern<<<(unsigned)grid, 64 * (kWriterWaves + 1), LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, (int)mblocks,
                                               row_max, row_inv, out, guarded ? guard->amax_limit : 0.0f,
                                               guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
                                               nullptr, nullptr);
@@ -754,11 +819,10 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     const int rgrid = grid_blocks(slots, nsplit);
     return dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        constexpr int LDS = 2 * Geo<C, G>::BUF;
-        auto kern = epi == 0 ? rows_mfma_kernel<C, G, 0> : rows_mfma_kernel<C, G, 1>;
-        kern<<<(unsigned)rgrid, 256, LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, slots,
-                                               row_max, row_inv, out, 0.0f, nullptr, nullptr, guard->rows,
-                                               guard->count);
+        constexpr int LDS = writer_ring<Geo<C, G>::REC>() * Geo<C, G>::BUF;
+        auto kern = epi == 0 ? rows_w_kernel<C, G, 0, true> : rows_w_kernel<C, G, 1, true>;
+        kern<<<(unsigned)rgrid, 64 * (kWriterWaves + 1), LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, slots, row_max,
+                                               row_inv, out, 0.0f, nullptr, nullptr, guard->rows, guard->count);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
