@@ -42,6 +42,10 @@ struct ppocr_rh {
     // three terms.  16 / (largest |dequantised weight|): a single product then carries at
     // most 16 * 2^-17 of split residual.
     float amax_limit = INFINITY;
+    // Rows with max|a| at most this have every logit in [-kLogitBound, kLogitBound]:
+    // |logit| <= max|a| * max_c sum_k |w_ck| + max_c |b_c|.  Also at most amax_limit.
+    float stats_amax_limit = 0.0f;
+    bool stats_noref = false;
 };
 
 namespace {
@@ -195,6 +199,21 @@ int create_common(const int8_t* q, const float* w_t, const float* scales, const 
             wmax = std::max(wmax, (float)qm * scales[j]);
         }
         h->amax_limit = wmax > 0.0f ? 16.0f / wmax : INFINITY;
+        // logit range bound: the largest L1 norm of a dequantised weight row and the
+        // largest |bias| (in double, rounded up by a small margin)
+        double w1 = 0.0, bmax = 0.0;
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t l1 = 0;
+            for (int64_t kk = 0; kk < k; ++kk) l1 += std::abs((int)q[j * k + kk]);
+            w1 = std::max(w1, (double)l1 * (double)scales[j]);
+            if (bias) bmax = std::max(bmax, std::fabs((double)bias[j]));
+        }
+        const double room = (double)kLogitBound - bmax * 1.001;
+        if (room > 0.0 && std::isfinite(w1) && std::isfinite(bmax)) {
+            const double lim = w1 > 0.0 ? room / (w1 * 1.001) : INFINITY;
+            h->stats_amax_limit = (float)std::min((double)h->amax_limit, lim);
+            h->stats_noref = true;
+        }
     }
 
     std::vector<float> sc_host;
@@ -286,7 +305,8 @@ WsLayout ws_layout(int64_t m, int nsplit) {
 }
 
 Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws) {
-    return Guard{h->amax_limit, reinterpret_cast<int*>(ws + L.guard_count), reinterpret_cast<int*>(ws + L.guard_rows)};
+    return Guard{h->amax_limit, reinterpret_cast<int*>(ws + L.guard_count), reinterpret_cast<int*>(ws + L.guard_rows),
+                 h->stats_amax_limit, h->stats_noref};
 }
 
 // Projection + softmax statistics + merge, on device pointers.

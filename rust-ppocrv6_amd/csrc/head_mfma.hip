@@ -246,7 +246,7 @@ struct EpiState {
     bool need;
 };
 
-template <int P, int MB>
+template <int P, int MB, bool NOREF>
 __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
                                           f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
                                           float (&best)[MB], int (&bt)[MB], f32x4* save, EpiState<MB>& st) {
@@ -273,7 +273,7 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
         constexpr int g = P - 4 - MB, b = g / 4, q = g % 4;
         float e[4];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) e[x] = __builtin_amdgcn_exp2f(t[b][4 * q + x] - ref[b]);
+        for (int x = 0; x < 4; ++x) e[x] = __builtin_amdgcn_exp2f(NOREF ? t[b][4 * q + x] : t[b][4 * q + x] - ref[b]);
         const float s = (e[0] + e[1]) + (e[2] + e[3]);
         st.tsum[b] = (q == 0) ? s : st.tsum[b] + s;
         // keep the sum here: without a use in this piece the exps would be sunk past the
@@ -293,7 +293,8 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
             best[b] = fmaxf(best[b], st.tmax[b]);
-            st.need = st.need | ((best[b] != -INFINITY) & (__builtin_fabsf(best[b] - ref[b]) > 64.0f));
+            if constexpr (!NOREF)
+                st.need = st.need | ((best[b] != -INFINITY) & (__builtin_fabsf(best[b] - ref[b]) > 64.0f));
         }
     }
 }
@@ -303,7 +304,7 @@ constexpr int epi_pieces() {
     return 6 + 5 * MB;
 }
 
-template <int S, int s, int MB>
+template <int S, int s, int MB, bool NOREF>
 __device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
                                                    f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
                                                    float (&best)[MB], int (&bt)[MB], f32x4* save,
@@ -311,7 +312,7 @@ __device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float*
     constexpr int NP = epi_pieces<MB>();
     constexpr int p0 = s * NP / S, p1 = (s + 1) * NP / S;
     [&]<int... I>(std::integer_sequence<int, I...>) {
-        (epi_piece<p0 + I, MB>(t, ep, h, j, cs, cb, ref, best, bt, save, st), ...);
+        (epi_piece<p0 + I, MB, NOREF>(t, ep, h, j, cs, cb, ref, best, bt, save, st), ...);
     }(std::make_integer_sequence<int, p1 - p0>{});
 }
 
@@ -330,7 +331,7 @@ __device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float*
 constexpr int kPrefetch = 2;
 constexpr int kRing = 4;  // LDS tile slots of the main statistics pass (a power of two)
 
-template <int C, int G, int MB, bool GATHER>
+template <int C, int G, int MB, bool GATHER, bool NOREF>
 __global__ __launch_bounds__(256, 2) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
@@ -425,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
                 for (int x = 0; x < kPrefetch; ++x) wq[x] = weight_frag<C, G>(bufn, x < S ? x : S - 1, lb, i * 16, h);
                 [&]<int... s>(std::integer_sequence<int, s...>) {
                     ([&] {
-                        epi_pieces_of_step<S, s, MB>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
+                        epi_pieces_of_step<S, s, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
 #pragma unroll
                         for (int b = 0; b < MB; ++b)
                             accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[b][s], accM[b], 0, 0, 0);
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
                         __builtin_amdgcn_sched_barrier(0);
                     }(), ...);
                 }(std::make_integer_sequence<int, S>{});
-                if (__any(st.need)) {
+                if (!NOREF && __any(st.need)) {
 #pragma unroll
                     for (int b = 0; b < MB; ++b) {
                         if (best[b] != -INFINITY && __builtin_fabsf(best[b] - ref[b]) > 64.0f) {
@@ -858,12 +859,19 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         guard_reset_kernel<<<1, 1, 0, st>>>(guard->count);
         PPOCR_HIP(hipGetLastError());
     }
+    // With the guard, rows whose logits could leave [-kLogitBound, kLogitBound] go to the
+    // rescue pass, so the main pass may skip the reference shift (NOREF).
+    const bool noref = guarded && guard->stats_noref;
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        stats_main_kernel<C, G, mb_of<C>(), false><<<grid, 256, main_lds_bytes<C, G>(), st>>>(
+        auto kern = stats_main_kernel<C, G, mb_of<C>(), false, false>;
+        if constexpr (C == CFG_Q2) {
+            if (noref) kern = stats_main_kernel<C, G, mb_of<C>(), false, true>;
+        }
+        kern<<<grid, 256, main_lds_bytes<C, G>(), st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
-            guarded ? guard->amax_limit : 0.0f, guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
-            nullptr, nullptr);
+            guarded ? (noref ? guard->stats_amax_limit : guard->amax_limit) : 0.0f,
+            guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr, nullptr, nullptr);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
@@ -876,7 +884,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         const int rgrid = grid_blocks(slots, nsplit);
         e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
             constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-            stats_main_kernel<C, G, mb_of<C>(), true><<<rgrid, 256, main_lds_bytes<C, G>(), st>>>(
+            stats_main_kernel<C, G, mb_of<C>(), true, false><<<rgrid, 256, main_lds_bytes<C, G>(), st>>>(
                 a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, slots, p_best, p_sum, p_idx, 0.0f, nullptr, nullptr,
                 guard->rows, guard->count);
             PPOCR_HIP(hipGetLastError());

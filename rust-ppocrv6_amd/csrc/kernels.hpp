@@ -25,10 +25,17 @@ enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4 };
 
 // Precision guard of the split-activation modes: rows whose max |a| exceeds amax_limit
 // are collected in rows[0 .. *count) and recomputed with one more activation term.
+// The statistics pass may use a lower limit, stats_amax_limit, under which every logit of
+// the row lies in [-kLogitBound, kLogitBound]; its main pass then skips the reference
+// shift of the softmax sum (stats_noref), and the rescue pass, which keeps it, takes the
+// other rows.
+constexpr float kLogitBound = 60.0f;
 struct Guard {
     float amax_limit;
     int* count;
     int* rows;
+    float stats_amax_limit;
+    bool stats_noref;
 };
 
 // Supported group counts (k = 113..120 and k = 73..80, the PP-OCRv6 small and tiny heads).

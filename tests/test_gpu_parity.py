@@ -358,3 +358,31 @@ def test_precision_guard_on_large_activations(orc, rh):
     r = orc.rechead_lines(a, np.array([0, 300], np.int64), q, s, bias)
     assert np.abs(mp - r["maxprob"]).max() < TOL
     head.close()
+
+
+@pytest.mark.parametrize("bias_shift", [0.0, 55.0, 70.0])
+def test_logit_range_guard(orc, rh, head, bias_shift):
+    """The statistics pass skips its reference shift for rows whose logits are bounded by
+    max|a| * max_c sum_k |w_ck| + max|b| <= 60; other rows go to the rescue pass.  Rows
+    scaled x1 .. x48 straddle that limit and the precision limit; a bias shift of 55 leaves
+    almost no room (nearly every row rescued), 70 none (the shift-keeping main pass).  A
+    constant bias shift leaves the probabilities and the argmax unchanged."""
+    rng = np.random.default_rng(21)
+    factors = np.repeat(np.array([1, 2, 4, 8, 12, 16, 24, 48], np.float32), 16)
+    a = rng.standard_normal((factors.size, 120), dtype=np.float32) * factors[:, None]
+    bias = (head["bias"] + np.float32(bias_shift)).astype(np.float32)
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=bias)
+    print(f"range guard bias_shift={bias_shift}", flush=True)
+    idx, mp = h.argmax(a, 2)
+    probs = h.probs(a[::8], 2)
+    h.close()
+    ref = orc.rechead_lines(a, split_lines(a.shape[0], 16), head["q"], head["s"], bias)
+    gap = top2_gap(f64_logits_q(a, head["q"], head["s"], bias))
+    check_argmax(idx, ref["idx"], gap, label=f"range guard shift {bias_shift}")
+    err = np.abs(mp - ref["maxprob"])
+    print(f"  max|maxprob diff| per factor: {[f'{e:.1e}' for e in err.reshape(8, 16).max(axis=1)]}")
+    assert err.max() < TOL
+    refp = orc.rechead_lines(a[::8], split_lines(a[::8].shape[0], 8), head["q"], head["s"], bias, want_probs=True)
+    errp = np.abs(probs - refp["probs"]).max()
+    print(f"  max|probs diff| = {errp:.3e}")
+    assert errp < TOL
