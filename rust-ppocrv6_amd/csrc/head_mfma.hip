@@ -246,22 +246,43 @@ struct EpiState {
     bool need;
 };
 
+// Epilogue of one tile on the accumulators t of MB row blocks, cut into NP = 13 * MB + 2
+// pieces of at most two exps each, in dependency order:
+//   for each quad q of the lane's 16 values: the fma of quad q of every block (after the
+//   last one, the constants of quad q + 2 are loaded into that quad's slot), then the exps
+//   and sums of quad q, two values per piece;
+//   then the tile maximum of each block, the saves of a raised maximum, the running maximum.
+template <int MB>
+constexpr int epi_pieces() {
+    return 13 * MB + 2;
+}
+
 template <int P, int MB, bool NOREF>
 __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
                                           f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
                                           float (&best)[MB], int (&bt)[MB], f32x4* save, EpiState<MB>& st) {
-    if constexpr (P < 4) {
-        constexpr int q = P;
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
+    constexpr int per_q = 3 * MB;
+    if constexpr (P < 4 * per_q) {
+        constexpr int q = P / per_q, x = P % per_q;
+        if constexpr (x < MB) {
+            constexpr int b = x;
 #pragma unroll
             for (int e = 0; e < 4; ++e) t[b][4 * q + e] = fmaf(t[b][4 * q + e], cs[q & 1][e], cb[q & 1][e]);
-        if constexpr (q < 2) {
-            cs[q & 1] = *reinterpret_cast<const f32x4*>(ep + 8 * (q + 2) + 4 * h);
-            cb[q & 1] = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * (q + 2) + 4 * h);
+            if constexpr (b == MB - 1 && q < 2) {
+                cs[q & 1] = *reinterpret_cast<const f32x4*>(ep + 8 * (q + 2) + 4 * h);
+                cb[q & 1] = *reinterpret_cast<const f32x4*>(ep + 32 + 8 * (q + 2) + 4 * h);
+            }
+        } else {
+            constexpr int y = x - MB, b = y / 2, r = 4 * q + 2 * (y % 2);
+            const float e0 = __builtin_amdgcn_exp2f(NOREF ? t[b][r] : t[b][r] - ref[b]);
+            const float e1 = __builtin_amdgcn_exp2f(NOREF ? t[b][r + 1] : t[b][r + 1] - ref[b]);
+            st.tsum[b] = (r == 0) ? e0 + e1 : st.tsum[b] + (e0 + e1);
+            // keep the sum here: without a use in this piece the exps would be sunk past the
+            // pieces that follow, out of the MFMA steps they are meant to overlap
+            asm volatile("" : "+v"(st.tsum[b]));
         }
-    } else if constexpr (P < 4 + MB) {
-        constexpr int b = P - 4;
+    } else if constexpr (P < 4 * per_q + MB) {
+        constexpr int b = P - 4 * per_q;
         const float m01 = fmaxf(fmaxf(t[b][0], t[b][1]), t[b][2]);
         const float m02 = fmaxf(fmaxf(t[b][3], t[b][4]), t[b][5]);
         const float m03 = fmaxf(fmaxf(t[b][6], t[b][7]), t[b][8]);
@@ -269,17 +290,7 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
         const float m05 = fmaxf(fmaxf(t[b][12], t[b][13]), t[b][14]);
         st.tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
         st.better[b] = st.tmax[b] > best[b];
-    } else if constexpr (P < 4 + 5 * MB) {
-        constexpr int g = P - 4 - MB, b = g / 4, q = g % 4;
-        float e[4];
-#pragma unroll
-        for (int x = 0; x < 4; ++x) e[x] = __builtin_amdgcn_exp2f(NOREF ? t[b][4 * q + x] : t[b][4 * q + x] - ref[b]);
-        const float s = (e[0] + e[1]) + (e[2] + e[3]);
-        st.tsum[b] = (q == 0) ? s : st.tsum[b] + s;
-        // keep the sum here: without a use in this piece the exps would be sunk past the
-        // pieces that follow, out of the MFMA steps they are meant to overlap
-        asm volatile("" : "+v"(st.tsum[b]));
-    } else if constexpr (P == 4 + 5 * MB) {
+    } else if constexpr (P == 4 * per_q + MB) {
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
             if (st.better[b]) {
@@ -299,18 +310,15 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
     }
 }
 
-template <int MB>
-constexpr int epi_pieces() {
-    return 6 + 5 * MB;
-}
-
-template <int S, int s, int MB, bool NOREF>
-__device__ __forceinline__ void epi_pieces_of_step(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
+// The pieces of half-step x of H: each MFMA step of a tile is two half-steps, one after
+// the MFMA of block 0 and one after the MFMAs of the other blocks.
+template <int H, int x, int MB, bool NOREF>
+__device__ __forceinline__ void epi_pieces_of_half(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
                                                    f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
                                                    float (&best)[MB], int (&bt)[MB], f32x4* save,
                                                    EpiState<MB>& st) {
     constexpr int NP = epi_pieces<MB>();
-    constexpr int p0 = s * NP / S, p1 = (s + 1) * NP / S;
+    constexpr int p0 = x * NP / H, p1 = (x + 1) * NP / H;
     [&]<int... I>(std::integer_sequence<int, I...>) {
         (epi_piece<p0 + I, MB, NOREF>(t, ep, h, j, cs, cb, ref, best, bt, save, st), ...);
     }(std::make_integer_sequence<int, p1 - p0>{});
@@ -424,14 +432,22 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
                 bf16x8 wq[kPrefetch];
 #pragma unroll
                 for (int x = 0; x < kPrefetch; ++x) wq[x] = weight_frag<C, G>(bufn, x < S ? x : S - 1, lb, i * 16, h);
+                // each MFMA step: the MFMA of block 0, half of the step's epilogue work, the
+                // MFMAs of the other blocks and the fragment prefetch, the other half; so a
+                // wave always has vector work to issue while its MFMAs run
                 [&]<int... s>(std::integer_sequence<int, s...>) {
                     ([&] {
-                        epi_pieces_of_step<S, s, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
+                        accM[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[0][s], accM[0], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        epi_pieces_of_half<2 * S, 2 * s, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int b = 0; b < MB; ++b)
+                        for (int b = 1; b < MB; ++b)
                             accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[b][s], accM[b], 0, 0, 0);
                         if constexpr (s + kPrefetch < S)
                             wq[s % kPrefetch] = weight_frag<C, G>(bufn, s + kPrefetch, lb, i * 16, h);
+                        __builtin_amdgcn_sched_barrier(0);
+                        epi_pieces_of_half<2 * S, 2 * s + 1, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
                         __builtin_amdgcn_sched_barrier(0);
                     }(), ...);
                 }(std::make_integer_sequence<int, S>{});
