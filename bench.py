@@ -162,8 +162,8 @@ def other_config(name, modes, steps, warmup):
         dws = DeviceArray((max(ws, 1),), np.uint8)
 
         def step():
-            rh._check(L.ppocr_rh_argmax_dev(head.handle, da.p, m, mode, didx.p, dmp.p, dws.p, ws, st))
-            rh._check(L.ppocr_ctc_greedy_dev(didx.p, dmp.p, doff.p, lines, 0, dseq.p, dlen.p, dscore.p, st))
+            rh._check(L.ppocr_rh_decode_dev(head.handle, da.p, m, doff.p, lines, mode, didx.p, dmp.p, dseq.p,
+                                            dlen.p, dscore.p, dws.p, ws, st))
 
         ms, _ = timed(step, stream, steps, warmup)
         flops = 2.0 * m * n * k
@@ -227,8 +227,10 @@ def main():
         rh._check(L.ppocr_ctc_greedy_dev(didx.p, dmp.p, doff.p, lines, 0, dseq.p, dlen.p, dscore.p, st))
 
     def fused_step():
-        fused_argmax()
-        ctc()
+        # the whole head as one call: projection + softmax statistics, then the chunk merge
+        # and the CTC collapse in one kernel
+        rh._check(L.ppocr_rh_decode_dev(head.handle, da.p, m, doff.p, lines, mode, didx.p, dmp.p, dseq.p, dlen.p,
+                                        dscore.p, dws.p, ws_bytes, st))
 
     out = {}
     flops = 2.0 * m * n * k

@@ -154,6 +154,18 @@ int ppocr_ctc_greedy_dev(const int32_t* d_idx, const float* d_maxprob, const int
 int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off, int64_t lines,
                     int mode, int32_t* idx, float* maxprob, int32_t* seq, int64_t* seq_len,
                     float* score);
+/* The same on device pointers, enqueued on `stream` (the engine-level fused hook of the
+ * recognition head, with the compact CTC entry: CtcDecoder::decode_batch,
+ * src/postprocess/ctc.rs:144-172, on (argmax, max probability) rows).  m is the number of
+ * activation rows, d_a [m][k]; d_line_off [lines + 1] is a device array with
+ * d_line_off[lines] = m, read on the device (offsets are clamped into [0, m]; a line whose
+ * end precedes its start is empty).  d_idx and d_maxprob may be NULL.  The workspace is the
+ * one of ppocr_rh_argmax_dev (ppocr_rh_workspace_bytes(h, m, mode)).  The merge of the
+ * vocabulary chunks and the CTC collapse run as one kernel. */
+int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off,
+                        int64_t lines, int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq,
+                        int64_t* d_seq_len, float* d_score, void* d_workspace,
+                        size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -309,9 +309,9 @@ Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws) {
                  h->stats_amax_limit, h->stats_noref};
 }
 
-// Projection + softmax statistics + merge, on device pointers.
+// Projection + softmax statistics + merge (+ the CTC collapse with `ctc`), on device pointers.
 int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* d_idx, float* d_maxprob,
-              float* d_row_max, float* d_row_inv, uint8_t* ws, hipStream_t st) {
+              float* d_row_max, float* d_row_inv, uint8_t* ws, hipStream_t st, const CtcOut* ctc = nullptr) {
     const int nsplit = nsplit_for(h, m, cfg);
     const WsLayout L = ws_layout(m, nsplit);
     float* p_best = reinterpret_cast<float*>(ws + L.p_best);
@@ -320,11 +320,12 @@ int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* 
     if (cfg >= 0) {
         const Guard g = make_guard(h, L, ws);
         return launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, d_idx,
-                                 d_maxprob, d_row_max, d_row_inv, st);
+                                 d_maxprob, d_row_max, d_row_inv, ctc, st);
     }
     if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
                                  p_idx, st))
         return e;
+    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, d_idx, d_maxprob, st);
     return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, st);
 }
 
@@ -635,6 +636,27 @@ int ppocr_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* li
     return PPOCR_OK;
 }
 
+int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off, int64_t lines,
+                        int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq, int64_t* d_seq_len,
+                        float* d_score, void* d_workspace, size_t workspace_bytes, void* stream) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (lines == 0) return PPOCR_OK;
+    if (!d_line_off || !d_seq_len || !d_score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    if (m > 0 && (!d_a || !d_seq)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    hipStream_t st = (hipStream_t)stream;
+    const CtcOut ctc{d_line_off, lines, 0, d_seq, d_seq_len, d_score};
+    if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, st);
+    const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;
+    return run_stats(h, cfg, d_a, m, d_idx, d_maxprob, nullptr, nullptr, ws.p, st, &ctc);
+}
+
 int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off, int64_t lines, int mode,
                     int32_t* idx, float* maxprob, int32_t* seq, int64_t* seq_len, float* score) {
     if (int e = check_head(h, "RecHeadHip")) return e;
@@ -658,15 +680,11 @@ int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off
     if (int e = dseq.alloc((size_t)m * 4)) return e;
     if (int e = dlen.alloc((size_t)lines * 8)) return e;
     if (int e = dsc.alloc((size_t)lines * 4)) return e;
-    if (m > 0) {
-        PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
-        if (int e = ppocr_rh_argmax_dev(h, da.as<float>(), m, mode, di.as<int32_t>(), dp.as<float>(), dws.p, wsb,
-                                        nullptr))
-            return e;
-    }
+    if (m > 0) PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
     PPOCR_HIP(hipMemcpy(doff.p, line_off, (size_t)(lines + 1) * 8, hipMemcpyHostToDevice));
-    if (int e = launch_ctc_greedy(di.as<int32_t>(), dp.as<float>(), doff.as<int64_t>(), lines, 0, dseq.as<int32_t>(),
-                                  dlen.as<int64_t>(), dsc.as<float>(), nullptr))
+    if (int e = ppocr_rh_decode_dev(h, da.as<float>(), m, doff.as<int64_t>(), lines, mode, di.as<int32_t>(),
+                                    dp.as<float>(), dseq.as<int32_t>(), dlen.as<int64_t>(), dsc.as<float>(), dws.p,
+                                    wsb, nullptr))
         return e;
     PPOCR_HIP(hipMemcpy(seq_len, dlen.p, (size_t)lines * 8, hipMemcpyDeviceToHost));
     PPOCR_HIP(hipMemcpy(score, dsc.p, (size_t)lines * 4, hipMemcpyDeviceToHost));

@@ -858,7 +858,8 @@ int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
 
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
                       int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx, const Guard* guard,
-                      int32_t* idx, float* maxprob, float* row_max, float* row_inv, hipStream_t st) {
+                      int32_t* idx, float* maxprob, float* row_max, float* row_inv, const CtcOut* ctc,
+                      hipStream_t st) {
     if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
     if (nsplit != 1 && nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16 && nsplit != 32 && nsplit != 64)
         return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be a power of two <= 64");
@@ -908,6 +909,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         });
         if (e) return e;
     }
+    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, idx, maxprob, st);
     return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max, row_inv, st);
 }
 

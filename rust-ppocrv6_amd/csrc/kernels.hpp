@@ -52,10 +52,22 @@ int stats_rows_per_block_mfma(int cfg);
 // Main pass, rescue of the guarded rows, then one wave per row merges the partials and
 // resolves the argmax: idx, maxprob (1/sum) and, when non-null, row_max (log2-domain
 // maximum) and row_inv (1/sum) for a probs pass.
+// CTC collapse of text lines fused into the statistics merge (device pointers): line i is
+// rows line_off[i] .. line_off[i+1]; outputs as ppocr_ctc_greedy.
+struct CtcOut {
+    const int64_t* line_off;
+    int64_t lines;
+    int32_t blank;
+    int32_t* seq;
+    int64_t* seq_len;
+    float* score;
+};
+
+// With `ctc`, the final merge also runs the CTC collapse (row_max and row_inv unused).
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                       int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
                       const Guard* guard, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
-                      hipStream_t st);
+                      const CtcOut* ctc, hipStream_t st);
 int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                       int64_t n, int64_t k, const float* row_max, const float* row_inv, float* probs,
                       const Guard* guard, hipStream_t st);
@@ -84,5 +96,9 @@ int launch_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx,
 int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* line_off,
                       int64_t lines, int32_t blank, int32_t* seq, int64_t* seq_len, float* score,
                       hipStream_t st);
+// Merge of the vocabulary-chunk partials and the CTC collapse in one kernel; idx and
+// maxprob (per row) may be null.
+int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
+                     const CtcOut& ctc, int32_t* idx, float* maxprob, hipStream_t st);
 
 }  // namespace ppocr

@@ -168,6 +168,42 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
     }
 }
 
+// A row's statistics merged over its vocabulary chunks: first-index argmax and
+// 1 / sum exp2(t - max) (the maximum probability).
+__device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, const float* __restrict__ p_sum,
+                                              const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
+                                              float* inv_out) {
+    RowStat s{-INFINITY, 0.0f, 0.0f, 0};
+    int c = 0;
+    // eight chunks' loads in flight at a time (nsplit is a power of two)
+    for (; c + 8 <= nsplit; c += 8) {
+        float b[8], sm[8];
+        int ix[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            b[u] = p_best[(int64_t)(c + u) * m + row];
+            sm[u] = p_sum[(int64_t)(c + u) * m + row];
+            ix[u] = p_idx[(int64_t)(c + u) * m + row];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)  // partial sums are relative to their max
+            s = stat_merge(s, RowStat{b[u], sm[u], (b[u] == -INFINITY) ? 0.0f : b[u], ix[u]});
+    }
+    for (; c < nsplit; ++c) {
+        RowStat o;
+        o.best = p_best[(int64_t)c * m + row];
+        o.sum = p_sum[(int64_t)c * m + row];
+        o.ref = (o.best == -INFINITY) ? 0.0f : o.best;
+        o.idx = p_idx[(int64_t)c * m + row];
+        s = stat_merge(s, o);
+    }
+    // s.sum is relative to s.best, so the maximum itself contributes exp2(0) = 1 and the
+    // sum is at least 1 (rounding of the rescaling could leave it an ulp below).
+    const float S = (s.best == -INFINITY) ? 0.0f : fmaxf(s.sum, 1.0f);
+    *inv_out = S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
+    return s;
+}
+
 __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restrict__ p_best,
                                                           const float* __restrict__ p_sum,
                                                           const int* __restrict__ p_idx, int64_t m, int nsplit,
@@ -175,19 +211,8 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
                                                           float* __restrict__ row_max, float* __restrict__ row_inv) {
     const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (row >= m) return;
-    RowStat s{-INFINITY, 0.0f, 0.0f, 0};
-    for (int c = 0; c < nsplit; ++c) {
-        RowStat o;
-        o.best = p_best[(int64_t)c * m + row];
-        o.sum = p_sum[(int64_t)c * m + row];
-        o.ref = (o.best == -INFINITY) ? 0.0f : o.best;  // partial sums are relative to their max
-        o.idx = p_idx[(int64_t)c * m + row];
-        s = stat_merge(s, o);
-    }
-    // s.sum is relative to s.best, so the maximum itself contributes exp2(0) = 1 and the
-    // sum is at least 1 (rounding of the rescaling could leave it an ulp below).
-    const float S = (s.best == -INFINITY) ? 0.0f : fmaxf(s.sum, 1.0f);
-    const float inv = S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
+    float inv;
+    const RowStat s = merged_row(p_best, p_sum, p_idx, m, nsplit, row, &inv);
     if (idx) idx[row] = s.idx;
     if (maxprob) maxprob[row] = inv;
     if (row_max) row_max[row] = s.best;
@@ -227,6 +252,68 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
         cnt += __popcll(mask);
     }
     if (lane == 0) {
+        seq_len[line] = cnt;
+        score[line] = cnt ? sum / (float)cnt : 0.0f;
+    }
+}
+
+// The merge of the vocabulary chunks and the CTC collapse in one pass: one workgroup per
+// text line.  The line is taken 256 steps at a time: every thread merges one step's row
+// into LDS, then wave 0 collapses the 256 steps as ctc_greedy_kernel does (ballot, prefix
+// popcount, score summed in step order), carrying the previous index between rounds.
+// Offsets are clamped into [0, m] (a line with t1 < t0 is empty).
+__global__ __launch_bounds__(256) void merge_ctc_kernel(const float* __restrict__ p_best,
+                                                        const float* __restrict__ p_sum,
+                                                        const int* __restrict__ p_idx, int64_t m, int nsplit,
+                                                        const int64_t* __restrict__ line_off, int64_t lines,
+                                                        int32_t blank, int32_t* __restrict__ idx_out,
+                                                        float* __restrict__ val_out, int32_t* __restrict__ seq,
+                                                        int64_t* __restrict__ seq_len, float* __restrict__ score) {
+    __shared__ int32_t s_id[256];
+    __shared__ float s_v[256];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t line = blockIdx.x;
+    const int64_t t0 = min(max(line_off[line], (int64_t)0), m);
+    const int64_t t1 = min(max(line_off[line + 1], t0), m);
+    int64_t cnt = 0;
+    float sum = -0.0f;
+    int32_t carry = blank;  // index of the step before the current one
+    for (int64_t base = t0; base < t1; base += 256) {
+        const int64_t t = base + tid;
+        int32_t id = blank;
+        float v = 0.0f;
+        if (t < t1) {
+            id = merged_row(p_best, p_sum, p_idx, m, nsplit, t, &v).idx;
+            if (idx_out) idx_out[t] = id;
+            if (val_out) val_out[t] = v;
+        }
+        s_id[tid] = id;
+        s_v[tid] = v;
+        __syncthreads();
+        if (tid < 64) {
+            const int64_t rem = min(t1 - base, (int64_t)256);
+            for (int c0 = 0; c0 < rem; c0 += 64) {
+                const bool valid = c0 + lane < rem;
+                const int32_t cid = valid ? s_id[c0 + lane] : blank;
+                const float cv = valid ? s_v[c0 + lane] : 0.0f;
+                const int32_t prev = (c0 + lane == 0) ? carry : s_id[c0 + lane - 1];
+                const bool emit = valid && cid != blank && cid != prev;
+                const uint64_t mask = __ballot(emit);
+                const int pos = __popcll(mask & ((1ull << lane) - 1ull));
+                if (emit) seq[t0 + cnt + pos] = cid;
+                uint64_t mm = mask;
+                while (mm) {
+                    const int src = __ffsll((unsigned long long)mm) - 1;
+                    mm &= mm - 1;
+                    sum += __shfl(cv, src, 64);
+                }
+                cnt += __popcll(mask);
+            }
+            carry = s_id[rem - 1];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
         seq_len[line] = cnt;
         score[line] = cnt ? sum / (float)cnt : 0.0f;
     }
@@ -275,6 +362,17 @@ int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* l
     const int64_t blocks = (lines + 3) / 4;
     if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
     ctc_greedy_kernel<<<(unsigned)blocks, 256, 0, st>>>(idx, maxprob, line_off, lines, blank, seq, seq_len, score);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
+                     const CtcOut& ctc, int32_t* idx, float* maxprob, hipStream_t st) {
+    if (ctc.lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
+    if (ctc.lines == 0) return PPOCR_OK;
+    if (ctc.lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
+    merge_ctc_kernel<<<(unsigned)ctc.lines, 256, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
+                                                       ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

@@ -386,3 +386,86 @@ def test_logit_range_guard(orc, rh, head, bias_shift):
     errp = np.abs(probs - refp["probs"]).max()
     print(f"  max|probs diff| = {errp:.3e}")
     assert errp < TOL
+
+
+def _ctc_lines_host(idx, val, off, m, blank=0):
+    """CTC collapse per line (CtcDecoder::decode_batch rules, src/postprocess/ctc.rs:151-163)
+    with the device entry's offset clamping; f32 score summed in step order."""
+    seqs, lens, scores = [], [], []
+    for i in range(len(off) - 1):
+        t0 = min(max(int(off[i]), 0), m)
+        t1 = min(max(int(off[i + 1]), t0), m)
+        prev, out, s = blank, [], np.float32(-0.0)
+        for t in range(t0, t1):
+            if idx[t] != blank and idx[t] != prev:
+                out.append(int(idx[t]))
+                s = np.float32(s + val[t])
+            prev = idx[t]
+        seqs.append((t0, out))
+        lens.append(len(out))
+        scores.append(np.float32(s / np.float32(len(out))) if out else np.float32(0.0))
+    return seqs, np.array(lens, np.int64), np.array(scores, np.float32)
+
+
+def test_decode_dev_one_merge_ctc_kernel(orc, rh, head, rhead):
+    """ppocr_rh_decode_dev (chunk merge and CTC collapse in one kernel) equals
+    ppocr_rh_argmax_dev + ppocr_ctc_greedy_dev bit for bit on the dense batch, and the
+    restated collapse on ragged and malformed offsets (empty, reversed, past m, 300 rows)."""
+    from ppocr_rechead import workloads as wl
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    L = rh._lib.lib()
+    a = wl.activations("dense_256")
+    m = a.shape[0]
+    off = wl.line_offsets([120] * 256)
+    lines = len(off) - 1
+    da, doff = DeviceArray.from_numpy(a), DeviceArray.from_numpy(off)
+    di1, dp1 = DeviceArray((m,), np.int32), DeviceArray((m,), np.float32)
+    ds1, dl1, dc1 = DeviceArray((m,), np.int32), DeviceArray((lines,), np.int64), DeviceArray((lines,), np.float32)
+    di2, dp2 = DeviceArray((m,), np.int32), DeviceArray((m,), np.float32)
+    ds2, dl2, dc2 = DeviceArray((m,), np.int32), DeviceArray((lines,), np.int64), DeviceArray((lines,), np.float32)
+    print("decode_dev vs argmax_dev + ctc_greedy_dev, dense_256", flush=True)
+    rh._check(L.ppocr_rh_argmax_dev(rhead.handle, da.p, m, 2, di1.p, dp1.p, None, 0, None))
+    rh._check(L.ppocr_ctc_greedy_dev(di1.p, dp1.p, doff.p, lines, 0, ds1.p, dl1.p, dc1.p, None))
+    rh._check(L.ppocr_rh_decode_dev(rhead.handle, da.p, m, doff.p, lines, 2, di2.p, dp2.p, ds2.p, dl2.p, dc2.p,
+                                    None, 0, None))
+    synchronize()
+    assert np.array_equal(di1.numpy(), di2.numpy())
+    assert np.array_equal(dp1.numpy().view(np.uint32), dp2.numpy().view(np.uint32))
+    l1, l2 = dl1.numpy(), dl2.numpy()
+    assert np.array_equal(l1, l2)
+    assert np.array_equal(dc1.numpy().view(np.uint32), dc2.numpy().view(np.uint32))
+    s1, s2 = ds1.numpy(), ds2.numpy()
+    for b in range(lines):
+        assert np.array_equal(s1[off[b]:off[b] + l1[b]], s2[off[b]:off[b] + l2[b]]), b
+
+    # ragged and malformed offsets on a small batch; idx/maxprob not requested
+    rng = np.random.default_rng(31)
+    mm = 700
+    a2 = rng.standard_normal((mm, 120), dtype=np.float32)
+    # empty lines, a 300-row line, offsets past m, a reversed and negative pair at the end
+    off2 = np.array([0, 0, 5, 305, 420, 690, 700, 900, 950, -3], np.int64)
+    n2 = len(off2) - 1
+    da2, doff2 = DeviceArray.from_numpy(a2), DeviceArray.from_numpy(off2)
+    ds3, dl3, dc3 = DeviceArray((mm,), np.int32), DeviceArray((n2,), np.int64), DeviceArray((n2,), np.float32)
+    di4, dp4 = DeviceArray((mm,), np.int32), DeviceArray((mm,), np.float32)
+    print("decode_dev ragged / malformed offsets", flush=True)
+    rh._check(L.ppocr_rh_decode_dev(rhead.handle, da2.p, mm, doff2.p, n2, 2, None, None, ds3.p, dl3.p, dc3.p,
+                                    None, 0, None))
+    rh._check(L.ppocr_rh_argmax_dev(rhead.handle, da2.p, mm, 2, di4.p, dp4.p, None, 0, None))
+    synchronize()
+    seqs, lens, scores = _ctc_lines_host(di4.numpy(), dp4.numpy(), off2, mm)
+    assert np.array_equal(dl3.numpy(), lens)
+    assert np.array_equal(dc3.numpy().view(np.uint32), scores.view(np.uint32))
+    s3 = ds3.numpy()
+    for b, (t0, out) in enumerate(seqs):
+        assert np.array_equal(s3[t0:t0 + len(out)], np.array(out, np.int32)), b
+
+    # no rows at all: every line empty
+    offz = np.zeros(4, np.int64)
+    doffz = DeviceArray.from_numpy(offz)
+    dlz, dcz = DeviceArray.from_numpy(np.full(3, 7, np.int64)), DeviceArray.from_numpy(np.full(3, 9.0, np.float32))
+    rh._check(L.ppocr_rh_decode_dev(rhead.handle, None, 0, doffz.p, 3, 2, None, None, None, dlz.p, dcz.p,
+                                    None, 0, None))
+    synchronize()
+    assert np.array_equal(dlz.numpy(), np.zeros(3, np.int64))
+    assert np.array_equal(dcz.numpy(), np.zeros(3, np.float32))
