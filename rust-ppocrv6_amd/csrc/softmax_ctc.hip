@@ -168,33 +168,31 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
     }
 }
 
-// A row's statistics merged over its vocabulary chunks: first-index argmax and
-// 1 / sum exp2(t - max) (the maximum probability).
+// A row's statistics merged over its vocabulary chunks by a group of kMergeLanes
+// consecutive lanes of one wave: lane g of the group takes chunks g, g + kMergeLanes, ...,
+// then the group combines with xor shuffles, so every lane of the group ends with the
+// merged statistic (first-index argmax) and 1 / sum exp2(t - max) (the maximum
+// probability).  Every kernel that merges partials uses this one order, so their results
+// agree bit for bit.
+constexpr int kMergeLanes = 8;
 __device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, const float* __restrict__ p_sum,
                                               const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
-                                              float* inv_out) {
+                                              bool valid, int g, float* inv_out) {
     RowStat s{-INFINITY, 0.0f, 0.0f, 0};
-    int c = 0;
-    // eight chunks' loads in flight at a time (nsplit is a power of two)
-    for (; c + 8 <= nsplit; c += 8) {
-        float b[8], sm[8];
-        int ix[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            b[u] = p_best[(int64_t)(c + u) * m + row];
-            sm[u] = p_sum[(int64_t)(c + u) * m + row];
-            ix[u] = p_idx[(int64_t)(c + u) * m + row];
+    if (valid) {
+        for (int c = g; c < nsplit; c += kMergeLanes) {
+            RowStat o;
+            o.best = p_best[(int64_t)c * m + row];
+            o.sum = p_sum[(int64_t)c * m + row];
+            o.ref = (o.best == -INFINITY) ? 0.0f : o.best;  // partial sums are relative to their max
+            o.idx = p_idx[(int64_t)c * m + row];
+            s = stat_merge(s, o);
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)  // partial sums are relative to their max
-            s = stat_merge(s, RowStat{b[u], sm[u], (b[u] == -INFINITY) ? 0.0f : b[u], ix[u]});
     }
-    for (; c < nsplit; ++c) {
-        RowStat o;
-        o.best = p_best[(int64_t)c * m + row];
-        o.sum = p_sum[(int64_t)c * m + row];
-        o.ref = (o.best == -INFINITY) ? 0.0f : o.best;
-        o.idx = p_idx[(int64_t)c * m + row];
+#pragma unroll
+    for (int off = 1; off < kMergeLanes; off <<= 1) {
+        const RowStat o{__shfl_xor(s.best, off, 64), __shfl_xor(s.sum, off, 64), __shfl_xor(s.ref, off, 64),
+                        __shfl_xor(s.idx, off, 64)};
         s = stat_merge(s, o);
     }
     // s.sum is relative to s.best, so the maximum itself contributes exp2(0) = 1 and the
@@ -209,10 +207,12 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
                                                           const int* __restrict__ p_idx, int64_t m, int nsplit,
                                                           int32_t* __restrict__ idx, float* __restrict__ maxprob,
                                                           float* __restrict__ row_max, float* __restrict__ row_inv) {
-    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (row >= m) return;
+    // 256 / kMergeLanes rows per workgroup
+    const int64_t row = (int64_t)blockIdx.x * (256 / kMergeLanes) + threadIdx.x / kMergeLanes;
+    const int g = threadIdx.x % kMergeLanes;
     float inv;
-    const RowStat s = merged_row(p_best, p_sum, p_idx, m, nsplit, row, &inv);
+    const RowStat s = merged_row(p_best, p_sum, p_idx, m, nsplit, row, row < m, g, &inv);
+    if (row >= m || g != 0) return;
     if (idx) idx[row] = s.idx;
     if (maxprob) maxprob[row] = inv;
     if (row_max) row_max[row] = s.best;
@@ -257,41 +257,45 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
     }
 }
 
-// The merge of the vocabulary chunks and the CTC collapse in one pass: one workgroup per
-// text line.  The line is taken 256 steps at a time: every thread merges one step's row
-// into LDS, then wave 0 collapses the 256 steps as ctc_greedy_kernel does (ballot, prefix
-// popcount, score summed in step order), carrying the previous index between rounds.
-// Offsets are clamped into [0, m] (a line with t1 < t0 is empty).
-__global__ __launch_bounds__(256) void merge_ctc_kernel(const float* __restrict__ p_best,
-                                                        const float* __restrict__ p_sum,
-                                                        const int* __restrict__ p_idx, int64_t m, int nsplit,
-                                                        const int64_t* __restrict__ line_off, int64_t lines,
-                                                        int32_t blank, int32_t* __restrict__ idx_out,
-                                                        float* __restrict__ val_out, int32_t* __restrict__ seq,
-                                                        int64_t* __restrict__ seq_len, float* __restrict__ score) {
-    __shared__ int32_t s_id[256];
-    __shared__ float s_v[256];
-    const int tid = threadIdx.x, lane = tid & 63;
+// The merge of the vocabulary chunks and the CTC collapse in one pass: one workgroup of
+// 1024 threads per text line.  The line is taken kCtcRound steps at a time: each step's row
+// is merged by a group of kMergeLanes lanes into LDS, then wave 0 collapses the round as
+// ctc_greedy_kernel does (ballot, prefix popcount, score summed in step order), carrying
+// the previous index between rounds.  Offsets are clamped into [0, m] (a line with t1 < t0
+// is empty).
+constexpr int kCtcRound = 1024 / kMergeLanes;
+__global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict__ p_best,
+                                                         const float* __restrict__ p_sum,
+                                                         const int* __restrict__ p_idx, int64_t m, int nsplit,
+                                                         const int64_t* __restrict__ line_off, int64_t lines,
+                                                         int32_t blank, int32_t* __restrict__ idx_out,
+                                                         float* __restrict__ val_out, int32_t* __restrict__ seq,
+                                                         int64_t* __restrict__ seq_len, float* __restrict__ score) {
+    __shared__ int32_t s_id[kCtcRound];
+    __shared__ float s_v[kCtcRound];
+    const int tid = threadIdx.x, lane = tid & 63, g = tid % kMergeLanes, step = tid / kMergeLanes;
     const int64_t line = blockIdx.x;
     const int64_t t0 = min(max(line_off[line], (int64_t)0), m);
     const int64_t t1 = min(max(line_off[line + 1], t0), m);
     int64_t cnt = 0;
     float sum = -0.0f;
     int32_t carry = blank;  // index of the step before the current one
-    for (int64_t base = t0; base < t1; base += 256) {
-        const int64_t t = base + tid;
-        int32_t id = blank;
+    for (int64_t base = t0; base < t1; base += kCtcRound) {
+        const int64_t t = base + step;
         float v = 0.0f;
-        if (t < t1) {
-            id = merged_row(p_best, p_sum, p_idx, m, nsplit, t, &v).idx;
-            if (idx_out) idx_out[t] = id;
-            if (val_out) val_out[t] = v;
+        const RowStat st = merged_row(p_best, p_sum, p_idx, m, nsplit, t, t < t1, g, &v);
+        if (g == 0) {
+            const int32_t id = t < t1 ? st.idx : blank;
+            if (t < t1) {
+                if (idx_out) idx_out[t] = id;
+                if (val_out) val_out[t] = v;
+            }
+            s_id[step] = id;
+            s_v[step] = t < t1 ? v : 0.0f;
         }
-        s_id[tid] = id;
-        s_v[tid] = v;
         __syncthreads();
         if (tid < 64) {
-            const int64_t rem = min(t1 - base, (int64_t)256);
+            const int64_t rem = min(t1 - base, (int64_t)kCtcRound);
             for (int c0 = 0; c0 < rem; c0 += 64) {
                 const bool valid = c0 + lane < rem;
                 const int32_t cid = valid ? s_id[c0 + lane] : blank;
@@ -347,7 +351,7 @@ int launch_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx,
 int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
                        int32_t* idx, float* maxprob, float* row_max, float* row_inv, hipStream_t st) {
     if (m <= 0) return PPOCR_OK;
-    const int64_t blocks = (m + 255) / 256;
+    const int64_t blocks = (m + 256 / kMergeLanes - 1) / (256 / kMergeLanes);
     if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
     merge_stats_kernel<<<(unsigned)blocks, 256, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max,
                                                          row_inv);
@@ -371,7 +375,7 @@ int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, 
     if (ctc.lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
     if (ctc.lines == 0) return PPOCR_OK;
     if (ctc.lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
-    merge_ctc_kernel<<<(unsigned)ctc.lines, 256, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
+    merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
                                                        ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
