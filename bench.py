@@ -119,6 +119,21 @@ def copy_probe(mib):
             "GBps_read_plus_write": round(2 * nbytes / (ms / 1e3) / 1e9, 1)}
 
 
+def measured_peaks():
+    """Peaks measured on this GPU in the same run, beside the datasheet ones: dense bf16
+    MFMA with every operand in registers (the benchmark's probe library), and a 256 MiB
+    device-to-device copy."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "rust-ppocrv6_amd", "lib", "libppocr_probe.so"))
+    tf, ms = ctypes.c_double(), ctypes.c_double()
+    rc = lib.ppocr_probe_mfma_bf16(ctypes.c_int(20000), ctypes.byref(tf), ctypes.byref(ms))
+    if rc:
+        raise RuntimeError(f"MFMA peak probe failed ({rc})")
+    cp = copy_probe(256)
+    return {"bf16_mfma_TFLOPs": round(tf.value, 1), "mfma_probe_ms": round(ms.value, 3),
+            "copy_GBps_read_plus_write": cp["GBps_read_plus_write"]}
+
+
 def make_workload(name):
     """A workload by name; the stress batch packs its weights with the GPU packer first
     (its near-tie rows are placed on the dequantised weights)."""
@@ -278,6 +293,7 @@ def main():
         dprobs.free()
 
     copy = copy_probe(args.copy_probe) if args.copy_probe > 0 else None
+    peaks = measured_peaks() if args.only == "" else None
 
     others = None
     if args.only == "" and not args.no_others:
@@ -316,6 +332,7 @@ def main():
                          "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles("stats_main_kernel_dense_256"),
                          "algorithmic_flops_per_launch": flops, "kernel_ms": round(ms_head, 5)},
+            "measured_peaks": peaks,
             "wall_ms_per_step": round(wall_ms, 5),
             "unfused": unf,
             "probs_fused": probs,

@@ -1,0 +1,66 @@
+// Peak probe of the benchmark (not part of the head library's interface): dense bf16
+// MFMA throughput with every operand in registers, i.e. the matrix cores' ceiling at the
+// clock the GPU holds under this load, to set beside the datasheet peak.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Four independent accumulation chains per wave, so the matrix core never waits on a
+// chain's previous result; the sums are stored so nothing is optimised away.
+__global__ __launch_bounds__(256) void mfma_peak_kernel(float* __restrict__ out, int iters) {
+    const int lane = threadIdx.x & 63;
+    bf16x8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        a[e] = (__bf16)(0.001f * (float)((lane + e) % 7));
+        b[e] = (__bf16)(0.002f * (float)((3 * lane + e) % 5));
+    }
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int it = 0; it < iters; ++it) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, a, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, b, c3, 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += (c0[r] + c1[r]) + (c2[r] + c3[r]);
+    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+}  // namespace
+
+// Runs the probe on the current device with 4 workgroups of 4 waves per CU (4 waves per
+// SIMD) and `iters` steps of 4 MFMAs per wave; returns 0 and the rate in TFLOP/s (2 flops
+// per multiply-add) and the kernel time, or the HIP error code.
+extern "C" int ppocr_probe_mfma_bf16(int iters, double* tflops, double* ms) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1;
+    const int blocks = 4 * cus;
+    float* out = nullptr;
+    if (hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)) != hipSuccess) return 2;
+    hipEvent_t e0, e1;
+    (void)hipEventCreate(&e0);
+    (void)hipEventCreate(&e1);
+    mfma_peak_kernel<<<blocks, 256>>>(out, iters / 4 + 1);  // warm-up, clocks up
+    (void)hipEventRecord(e0, nullptr);
+    mfma_peak_kernel<<<blocks, 256>>>(out, iters);
+    (void)hipEventRecord(e1, nullptr);
+    hipError_t rc = hipEventSynchronize(e1);
+    float t = 0.0f;
+    if (rc == hipSuccess) rc = hipEventElapsedTime(&t, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipFree(out);
+    if (rc != hipSuccess) return (int)rc;
+    const double flops = (double)blocks * 4.0 * (double)iters * 4.0 * (32.0 * 32.0 * 16.0 * 2.0);
+    *ms = t;
+    *tflops = flops / ((double)t * 1e-3) / 1e12;
+    return 0;
+}
