@@ -110,3 +110,13 @@ def test_workloads_are_deterministic():
     zero_rows = np.nonzero(~ws.any(axis=1))[0]
     assert zero_rows.size == 18710 // 200
     assert (np.abs(ws) == 5.0).sum() == 18710 // 200
+
+
+def test_decode_dev_argument_errors_do_not_need_a_device(rh):
+    """ppocr_rh_decode_dev rejects a null head, negative counts and missing outputs before
+    any HIP call; zero lines is a no-op."""
+    L = rh._lib.lib()
+    args = (None, 0, None, 1, 2, None, None, None, None, None, None, 0, None)
+    assert L.ppocr_rh_decode_dev(None, *args) == rh.PPOCR_ERR_INVALID_ARG
+    assert rh._lib.last_error() == "RecHeadHip: null head handle"
+    assert L.ppocr_rh_decode(None, None, None, 1, 2, None, None, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
