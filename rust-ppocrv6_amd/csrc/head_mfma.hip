@@ -338,16 +338,18 @@ __device__ __forceinline__ void epi_pieces_of_half(f32x16 (&t)[MB], const float*
 // into LDS), one barrier per tile.
 constexpr int kPrefetch = 2;
 constexpr int kRing = 4;  // LDS tile slots of the main statistics pass (a power of two)
+constexpr int kStatsWaves = 4;  // waves per workgroup of the statistics pass: two workgroups per CU
 
 template <int C, int G, int MB, bool GATHER, bool NOREF>
-__global__ __launch_bounds__(256, 2) void stats_main_kernel(
+__global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
     int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows,
     const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
-    constexpr int RPB = 128 * MB;
+    constexpr int RPB = 32 * kStatsWaves * MB;
+    constexpr int NT = 64 * kStatsWaves;
     extern __shared__ __align__(16) uint8_t lds[];
 
     int mbi, chunk;
@@ -391,11 +393,11 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
         }
 
         if (t0 < t1) {
-            constexpr int kOps = stage_direct_min_ops<GE::REC>();
+            constexpr int kOps = stage_direct_min_ops<GE::REC, NT>();
             if constexpr (GATHER) ring_barrier<0>();  // a previous row block's tiles are no longer read
 #pragma unroll
             for (int x = 0; x < kRing - 1; ++x)
-                stage_direct<GE::REC>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
+                stage_direct<GE::REC, NT>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
             ring_barrier<kOps>();  // tiles t0 and t0+1 are in LDS
             f32x16 acc_a[MB], acc_b[MB];
 #pragma unroll
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(256, 2) void stats_main_kernel(
             // keeps the body branch-free.
             auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
                 const unsigned rel = (unsigned)(j - t0);
-                stage_direct<GE::REC>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
+                stage_direct<GE::REC, NT>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
                                       lds + ((rel + kRing - 1) & (kRing - 1)) * GE::BUF, tid);
                 const uint8_t* bufn = lds + ((rel + 1) & (kRing - 1)) * GE::BUF;
                 const float* ep = reinterpret_cast<const float*>(lds + (rel & (kRing - 1)) * GE::BUF + GE::FRAG);
@@ -719,17 +721,17 @@ static constexpr int mb_of() {
 // LDS of the main statistics pass: the tile ring and each wave's saved best tile.
 template <int C, int G>
 static constexpr int main_lds_bytes() {
-    return kRing * Geo<C, G>::BUF + 4 * mb_of<C>() * 16 * 64 * 4;
+    return kRing * Geo<C, G>::BUF + kStatsWaves * mb_of<C>() * 16 * 64 * 4;
 }
 
 // Rows per workgroup of the main statistics pass and of the rescue pass (4 waves).
 int stats_rows_per_block_mfma(int cfg) {
     switch (cfg) {
-        case CFG_Q1: return 128 * mb_of<CFG_Q1>();
-        case CFG_Q2: return 128 * mb_of<CFG_Q2>();
-        case CFG_Q3: return 128 * mb_of<CFG_Q3>();
-        case CFG_F1: return 128 * mb_of<CFG_F1>();
-        default: return 128 * mb_of<CFG_F3>();
+        case CFG_Q1: return 32 * kStatsWaves * mb_of<CFG_Q1>();
+        case CFG_Q2: return 32 * kStatsWaves * mb_of<CFG_Q2>();
+        case CFG_Q3: return 32 * kStatsWaves * mb_of<CFG_Q3>();
+        case CFG_F1: return 32 * kStatsWaves * mb_of<CFG_F1>();
+        default: return 32 * kStatsWaves * mb_of<CFG_F3>();
     }
 }
 
@@ -740,7 +742,7 @@ int stats_rows_per_block_mfma(int cfg) {
 // 147 tiles, one round, than in 8 chunks of 74, two rounds).  The chunk count from 4 to
 // 64 minimising rounds x (fixed + tiles per chunk) is taken.  At least 4 chunks keep each
 // XCD's slice of the weight records (the chunks of workgroup id mod 8) within its L2.
-constexpr int64_t kStatsSlots = 512;
+constexpr int64_t kStatsSlots = 256 * 8 / kStatsWaves;
 constexpr int64_t kChunkFixedTiles = 8;
 int stats_nsplit(int64_t m, int rows_per_block, int tiles) {
     const int64_t mblocks = (m + rows_per_block - 1) / rows_per_block;
@@ -885,7 +887,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         if constexpr (C == CFG_Q2) {
             if (noref) kern = stats_main_kernel<C, G, mb_of<C>(), false, true>;
         }
-        kern<<<grid, 256, main_lds_bytes<C, G>(), st>>>(
+        kern<<<grid, 64 * kStatsWaves, main_lds_bytes<C, G>(), st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
             guarded ? (noref ? guard->stats_amax_limit : guard->amax_limit) : 0.0f,
             guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr, nullptr, nullptr);
@@ -901,7 +903,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         const int rgrid = grid_blocks(slots, nsplit);
         e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
             constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-            stats_main_kernel<C, G, mb_of<C>(), true, false><<<rgrid, 256, main_lds_bytes<C, G>(), st>>>(
+            stats_main_kernel<C, G, mb_of<C>(), true, false><<<rgrid, 64 * kStatsWaves, main_lds_bytes<C, G>(), st>>>(
                 a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, slots, p_best, p_sum, p_idx, 0.0f, nullptr, nullptr,
                 guard->rows, guard->count);
             PPOCR_HIP(hipGetLastError());
