@@ -327,7 +327,7 @@ def main():
             "config": {"workload": f"{args.workload}: {lines} lines x T=120, m={m}, k={k}, n={n}, fused "
                                    "projection+softmax-max+argmax+CTC", "mode": mode},
             "roofline": {"bound": "mfma" if mode else "valu",
-                         "kernel": "ppocr_rh_argmax_dev: stats_main_kernel (>= 95% of the time) + guard reset, "
+                         "kernel": "ppocr_rh_argmax_dev: stats_main_kernel (>= 95% of the time) + "
                                    "guarded-row rescue and merge kernels",
                          "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles("stats_main_kernel_dense_256"),

@@ -1,6 +1,7 @@
 // The extern "C" boundary (include/ppocr_rechead.h): head handles, argument checks with
 // the reference's error messages, and the host/device entry points.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -287,7 +288,7 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t p_best, p_sum, p_idx, row_max, row_inv, guard_count, guard_rows, total;
+    size_t p_best, p_sum, p_idx, row_max, row_inv, guard_header, guard_rows, total;
 };
 WsLayout ws_layout(int64_t m, int nsplit) {
     WsLayout L;
@@ -298,15 +299,24 @@ WsLayout ws_layout(int64_t m, int nsplit) {
     L.p_idx = 2 * pm;
     L.row_max = 3 * pm;
     L.row_inv = L.row_max + rm;
-    L.guard_count = L.row_inv + rm;
-    L.guard_rows = L.guard_count + kAlign;
+    L.guard_header = L.row_inv + rm;
+    L.guard_rows = L.guard_header + kAlign;
     L.total = L.guard_rows + rm;
     return L;
 }
 
-Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws) {
-    return Guard{h->amax_limit, reinterpret_cast<int*>(ws + L.guard_count), reinterpret_cast<int*>(ws + L.guard_rows),
-                 h->stats_amax_limit, h->stats_noref};
+// A new epoch for every guarded pass (never 0, so zeroed memory is not taken for a list).
+unsigned next_epoch() {
+    static std::atomic<unsigned> counter{0};
+    unsigned e = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+    while (e == 0) e = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+    return e;
+}
+
+Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws, int64_t m) {
+    return Guard{h->amax_limit, reinterpret_cast<unsigned long long*>(ws + L.guard_header),
+                 reinterpret_cast<int*>(ws + L.guard_rows), (int)std::min<int64_t>(m, INT32_MAX), next_epoch(), h->stats_amax_limit,
+                 h->stats_noref};
 }
 
 // Projection + softmax statistics + merge (+ the CTC collapse with `ctc`), on device pointers.
@@ -318,15 +328,15 @@ int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* 
     float* p_sum = reinterpret_cast<float*>(ws + L.p_sum);
     int* p_idx = reinterpret_cast<int*>(ws + L.p_idx);
     if (cfg >= 0) {
-        const Guard g = make_guard(h, L, ws);
+        const Guard g = make_guard(h, L, ws, m);
         return launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, d_idx,
                                  d_maxprob, d_row_max, d_row_inv, ctc, st);
     }
     if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
                                  p_idx, st))
         return e;
-    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, d_idx, d_maxprob, st);
-    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, st);
+    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, d_idx, d_maxprob, nullptr, st);
+    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, nullptr, st);
 }
 
 // Workspace: caller's, or stream-ordered scratch freed on the same stream.
@@ -448,7 +458,7 @@ int ppocr_rh_logits_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mo
     const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
     Workspace ws;
     if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, op)) return e;
-    const Guard g = make_guard(h, L, ws.p);
+    const Guard g = make_guard(h, L, ws.p, m);
     return launch_logits_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, d_out, &g, st);
 }
 
@@ -567,7 +577,7 @@ int ppocr_rh_probs_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mod
     if (int e = run_stats(h, cfg, d_a, m, nullptr, nullptr, rmax, rinv, ws.p, st)) return e;
     if (cfg < 0)
         return launch_probs_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, rmax, rinv, d_probs, st);
-    const Guard g = make_guard(h, L, ws.p);
+    const Guard g = make_guard(h, L, ws.p, m);
     return launch_probs_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, rmax, rinv, d_probs, &g, st);
 }
 
@@ -650,7 +660,7 @@ int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const 
     DeviceGuard dg(h->device);
     hipStream_t st = (hipStream_t)stream;
     const CtcOut ctc{d_line_off, lines, 0, d_seq, d_seq_len, d_score};
-    if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, st);
+    if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
     const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
     Workspace ws;
     if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;

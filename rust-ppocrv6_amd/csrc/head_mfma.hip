@@ -159,8 +159,9 @@ struct RowSource {
     int count;        // list length
     __device__ __forceinline__ int64_t row(int64_t j, int64_t m, bool& valid) const {
         if (list) {
-            valid = j < count;
-            return valid ? (int64_t)list[j] : 0;
+            const int64_t r = j < count ? (int64_t)list[j] : -1;
+            valid = r >= 0 && r < m;  // list entries are checked, not trusted
+            return valid ? r : 0;
         }
         valid = j < m;
         return j;
@@ -170,13 +171,31 @@ struct RowSource {
 // Precision guard of the split-activation modes: a row whose largest |a| times the
 // head's largest |w| exceeds the limit is appended to a device list, to be recomputed
 // with one more activation term.  lanes i and i+32 see complementary k groups.
+// The list's header is (epoch << 32) | count: the first append of a call installs the
+// call's epoch with count 0 (a header of another call, or uninitialised memory, counts as
+// empty), then each append takes the next slot.  Slots past the capacity are dropped.
 __device__ __forceinline__ void guard_append(float amax, float amax_limit, bool valid, int64_t row, int h,
-                                             int* guard_count, int* guard_rows) {
+                                             unsigned long long* guard_header, int* guard_rows, unsigned epoch,
+                                             int capacity) {
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
     if (h == 0 && valid && amax > amax_limit) {
-        const int pos = atomicAdd(guard_count, 1);
-        guard_rows[pos] = (int)row;
+        unsigned long long cur = __hip_atomic_load(guard_header, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while ((unsigned)(cur >> 32) != epoch) {
+            const unsigned long long prev = atomicCAS(guard_header, cur, (unsigned long long)epoch << 32);
+            if (prev == cur) break;
+            cur = prev;  // another lane or workgroup changed it first; look again
+        }
+        const int pos = (int)(unsigned)atomicAdd(guard_header, 1ull);
+        if (pos >= 0 && pos < capacity) guard_rows[pos] = (int)row;
     }
+}
+
+// Entries of the guard list for this call's epoch (0 for a header of another epoch).
+__device__ __forceinline__ int guard_count_of(const unsigned long long* guard_header, unsigned epoch, int capacity) {
+    const unsigned long long v = *guard_header;
+    if ((unsigned)(v >> 32) != epoch) return 0;
+    const unsigned c = (unsigned)v;
+    return c < (unsigned)capacity ? (int)c : capacity;
 }
 
 // Global -> LDS staging of one tile record by all NT threads of a workgroup, without
@@ -344,8 +363,8 @@ template <int C, int G, int MB, bool GATHER, bool NOREF>
 __global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, float amax_limit, int* __restrict__ guard_count, int* __restrict__ guard_rows,
-    const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
+    int* __restrict__ p_idx, float amax_limit, unsigned long long* __restrict__ guard_header,
+    int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
     constexpr int RPB = 32 * kStatsWaves * MB;
@@ -358,7 +377,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_
     const int t0 = chunk * tiles_per_chunk;
     const int t1 = min(t0 + tiles_per_chunk, tiles);
     // one row block, or (GATHER) the row blocks of a device-side row list, mblocks apart
-    const RowSource src{GATHER ? gather_rows : nullptr, GATHER ? *gather_count : 0};
+    const RowSource src{GATHER ? guard_rows : nullptr, GATHER ? guard_count_of(guard_header, guard_epoch, guard_cap) : 0};
     const int64_t blk_end = GATHER ? ((int64_t)src.count + RPB - 1) / RPB : (int64_t)mbi + 1;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
@@ -379,7 +398,8 @@ __global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_
             float amax = 0.0f;
 #pragma unroll
             for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
-            if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid[b], arow[b], h, guard_count, guard_rows);
+            if (!GATHER && guard_header && chunk == 0)
+                guard_append(amax, amax_limit, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch, guard_cap);
         }
 
         float best[MB], sum[MB], ref[MB];
@@ -564,14 +584,14 @@ constexpr int writer_ring() {
 // take the same tile and write its 32 classes of their rows, rows front to back.
 // Orientation: rows of the MFMA = activation rows, columns = classes; a lane holds one
 // class of 16 rows, so each store instruction writes 32 consecutive classes of two rows.
-// `gather_rows`: the rows are entries of a device list (the rescue of guarded rows); a
+// GATHER: the rows are the entries of the guard list (the rescue of guarded rows); a
 // workgroup then takes several row blocks and the producer streams the tiles once per block.
 template <int C, int G, int EPI, bool GATHER>
 __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles, int n,
     int nsplit, int tiles_per_chunk, int mblocks, const float* __restrict__ row_max,
-    const float* __restrict__ row_inv, float* __restrict__ out, float amax_limit, int* __restrict__ guard_count,
-    int* __restrict__ guard_rows, const int* __restrict__ gather_rows, const int* __restrict__ gather_count) {
+    const float* __restrict__ row_inv, float* __restrict__ out, float amax_limit,
+    unsigned long long* __restrict__ guard_header, int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
     constexpr int NC = kWriterWaves;
@@ -585,7 +605,7 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
     const int t0 = chunk * tiles_per_chunk;
     const int t1 = min(t0 + tiles_per_chunk, tiles);
     if (t0 >= t1) return;
-    const RowSource src{GATHER ? gather_rows : nullptr, GATHER ? *gather_count : 0};
+    const RowSource src{GATHER ? guard_rows : nullptr, GATHER ? guard_count_of(guard_header, guard_epoch, guard_cap) : 0};
     const int64_t blk_end = GATHER ? ((int64_t)src.count + ROWS - 1) / ROWS : (int64_t)mbi + 1;
     const int64_t nblk = (blk_end - mbi + mblocks - 1) / mblocks;  // row blocks of this workgroup
     if (nblk <= 0) return;
@@ -633,7 +653,8 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
         bf16x8 bf[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec != 0, s, h, amax);
-        if (guard_count && chunk == 0) guard_append(amax, amax_limit, valid, arow, h, guard_count, guard_rows);
+        if (!GATHER && guard_header && chunk == 0)
+            guard_append(amax, amax_limit, valid, arow, h, guard_header, guard_rows, guard_epoch, guard_cap);
         // rows of this lane's 16 accumulators (r -> row slot 8*(r/4) + 4*h + (r%4))
         int64_t orow[16];
         bool ovalid[16];
@@ -711,7 +732,10 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
     }
 }
 
-__global__ void guard_reset_kernel(int* guard_count) { *guard_count = 0; }
+// Sets the guard list's header to (epoch, 0) before a pass that is not followed by a merge.
+__global__ void guard_reset_kernel(unsigned long long* guard_header, unsigned epoch) {
+    *guard_header = (unsigned long long)epoch << 32;
+}
 
 // ============================================================ launchers
 template <int C>
@@ -816,9 +840,10 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     if (grid > 0x7fffffff) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
     const int vec = vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
-    const bool guarded = guard && guard->count && rcfg >= 0;
+    const bool guarded = guard && guard->header && rcfg >= 0;
     if (guarded) {
-        guard_reset_kernel<<<1, 1, 0, st>>>(guard->count);
+        // a replay of this call (same epoch) must start from an empty list too
+        guard_reset_kernel<<<1, 1, 0, st>>>(guard->header, guard->epoch);
         PPOCR_HIP(hipGetLastError());
     }
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
@@ -827,8 +852,8 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
         auto kern = epi == 0 ? rows_w_kernel<C, G, 0, false> : rows_w_kernel<C, G, 1, false>;
         kern<<<(unsigned)grid, 64 * (kWriterWaves + 1), LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, (int)mblocks,
                                               row_max, row_inv, out, guarded ? guard->amax_limit : 0.0f,
-                                              guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr,
-                                              nullptr, nullptr);
+                                              guarded ? guard->header : nullptr, guarded ? guard->rows : nullptr,
+                                              guarded ? guard->epoch : 0u, guarded ? guard->capacity : 0);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
@@ -841,7 +866,8 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
         constexpr int LDS = writer_ring<Geo<C, G>::REC>() * Geo<C, G>::BUF;
         auto kern = epi == 0 ? rows_w_kernel<C, G, 0, true> : rows_w_kernel<C, G, 1, true>;
         kern<<<(unsigned)rgrid, 64 * (kWriterWaves + 1), LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, slots, row_max,
-                                               row_inv, out, 0.0f, nullptr, nullptr, guard->rows, guard->count);
+                                               row_inv, out, 0.0f, guard->header, guard->rows, guard->epoch,
+                                               guard->capacity);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
@@ -873,11 +899,8 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     const int grid = grid_blocks((int)mblocks, nsplit);
     const int vec = vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
-    const bool guarded = guard && guard->count && rcfg >= 0;
-    if (guarded) {
-        guard_reset_kernel<<<1, 1, 0, st>>>(guard->count);
-        PPOCR_HIP(hipGetLastError());
-    }
+    // No reset launch: the list is emptied by its epoch (first use) and by the merge below.
+    const bool guarded = guard && guard->header && rcfg >= 0;
     // With the guard, rows whose logits could leave [-kLogitBound, kLogitBound] go to the
     // rescue pass, so the main pass may skip the reference shift (NOREF).
     const bool noref = guarded && guard->stats_noref;
@@ -890,7 +913,8 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         kern<<<grid, 64 * kStatsWaves, main_lds_bytes<C, G>(), st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
             guarded ? (noref ? guard->stats_amax_limit : guard->amax_limit) : 0.0f,
-            guarded ? guard->count : nullptr, guarded ? guard->rows : nullptr, nullptr, nullptr);
+            guarded ? guard->header : nullptr, guarded ? guard->rows : nullptr, guarded ? guard->epoch : 0u,
+            guarded ? guard->capacity : 0);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
@@ -904,15 +928,16 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
             constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
             stats_main_kernel<C, G, mb_of<C>(), true, false><<<rgrid, 64 * kStatsWaves, main_lds_bytes<C, G>(), st>>>(
-                a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, slots, p_best, p_sum, p_idx, 0.0f, nullptr, nullptr,
-                guard->rows, guard->count);
+                a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, slots, p_best, p_sum, p_idx, 0.0f, guard->header,
+                guard->rows, guard->epoch, guard->capacity);
             PPOCR_HIP(hipGetLastError());
             return PPOCR_OK;
         });
         if (e) return e;
     }
-    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, idx, maxprob, st);
-    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max, row_inv, st);
+    const Guard* reset = guarded ? guard : nullptr;
+    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, idx, maxprob, reset, st);
+    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max, row_inv, reset, st);
 }
 
 }  // namespace ppocr

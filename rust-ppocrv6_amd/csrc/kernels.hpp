@@ -24,7 +24,11 @@ struct TileGeom {
 enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4 };
 
 // Precision guard of the split-activation modes: rows whose max |a| exceeds amax_limit
-// are collected in rows[0 .. *count) and recomputed with one more activation term.
+// are collected in rows[0 .. count) and recomputed with one more activation term.  The
+// 64-bit header holds (epoch << 32) | count.  Every call draws a new epoch; the first
+// append of a call installs it (count 0), and a header with another epoch counts as empty,
+// so a fresh or stale workspace needs no reset.  Paths that end with a merge kernel reset
+// the header to (epoch, 0) there, so a replay of the same call (same epoch) starts empty.
 // The statistics pass may use a lower limit, stats_amax_limit, under which every logit of
 // the row lies in [-kLogitBound, kLogitBound]; its main pass then skips the reference
 // shift of the softmax sum (stats_noref), and the rescue pass, which keeps it, takes the
@@ -32,8 +36,10 @@ enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4 };
 constexpr float kLogitBound = 60.0f;
 struct Guard {
     float amax_limit;
-    int* count;
+    unsigned long long* header;
     int* rows;
+    int capacity;  // entries of rows (the batch's row count)
+    unsigned epoch;
     float stats_amax_limit;
     bool stats_noref;
 };
@@ -85,9 +91,10 @@ int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const 
 
 // Merge the per-chunk partials of each row: argmax index, max probability, and (when
 // row_max/row_inv are non-null) the row's log2-domain maximum and 1/sum for a probs pass.
+// With `guard`, the merge also resets the guard header to (epoch, 0) (see Guard).
 int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m,
                        int nsplit, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
-                       hipStream_t st);
+                       const Guard* guard, hipStream_t st);
 
 int launch_softmax_rows(float* x, int64_t rows, int64_t cols, int32_t* idx, float* maxprob,
                         hipStream_t st);
@@ -99,6 +106,6 @@ int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* l
 // Merge of the vocabulary-chunk partials and the CTC collapse in one kernel; idx and
 // maxprob (per row) may be null.
 int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
-                     const CtcOut& ctc, int32_t* idx, float* maxprob, hipStream_t st);
+                     const CtcOut& ctc, int32_t* idx, float* maxprob, const Guard* guard, hipStream_t st);
 
 }  // namespace ppocr

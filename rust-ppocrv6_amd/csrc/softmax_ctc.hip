@@ -206,7 +206,10 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
                                                           const float* __restrict__ p_sum,
                                                           const int* __restrict__ p_idx, int64_t m, int nsplit,
                                                           int32_t* __restrict__ idx, float* __restrict__ maxprob,
-                                                          float* __restrict__ row_max, float* __restrict__ row_inv) {
+                                                          float* __restrict__ row_max, float* __restrict__ row_inv,
+                                                          unsigned long long* __restrict__ guard_header,
+                                                          unsigned guard_epoch) {
+    if (guard_header && blockIdx.x == 0 && threadIdx.x == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     // 256 / kMergeLanes rows per workgroup
     const int64_t row = (int64_t)blockIdx.x * (256 / kMergeLanes) + threadIdx.x / kMergeLanes;
     const int g = threadIdx.x % kMergeLanes;
@@ -270,8 +273,11 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
                                                          const int64_t* __restrict__ line_off, int64_t lines,
                                                          int32_t blank, int32_t* __restrict__ idx_out,
                                                          float* __restrict__ val_out, int32_t* __restrict__ seq,
-                                                         int64_t* __restrict__ seq_len, float* __restrict__ score) {
+                                                         int64_t* __restrict__ seq_len, float* __restrict__ score,
+                                                         unsigned long long* __restrict__ guard_header,
+                                                         unsigned guard_epoch) {
     __shared__ int32_t s_id[kCtcRound];
+    if (guard_header && blockIdx.x == 0 && threadIdx.x == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     __shared__ float s_v[kCtcRound];
     const int tid = threadIdx.x, lane = tid & 63, g = tid % kMergeLanes, step = tid / kMergeLanes;
     const int64_t line = blockIdx.x;
@@ -349,12 +355,14 @@ int launch_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx,
 }
 
 int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
-                       int32_t* idx, float* maxprob, float* row_max, float* row_inv, hipStream_t st) {
+                       int32_t* idx, float* maxprob, float* row_max, float* row_inv, const Guard* guard,
+                       hipStream_t st) {
     if (m <= 0) return PPOCR_OK;
     const int64_t blocks = (m + 256 / kMergeLanes - 1) / (256 / kMergeLanes);
     if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
     merge_stats_kernel<<<(unsigned)blocks, 256, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max,
-                                                         row_inv);
+                                                         row_inv, guard ? guard->header : nullptr,
+                                                         guard ? guard->epoch : 0u);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
@@ -371,12 +379,13 @@ int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* l
 }
 
 int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
-                     const CtcOut& ctc, int32_t* idx, float* maxprob, hipStream_t st) {
+                     const CtcOut& ctc, int32_t* idx, float* maxprob, const Guard* guard, hipStream_t st) {
     if (ctc.lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
     if (ctc.lines == 0) return PPOCR_OK;
     if (ctc.lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
     merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
-                                                       ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score);
+                                                       ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score,
+                                                       guard ? guard->header : nullptr, guard ? guard->epoch : 0u);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

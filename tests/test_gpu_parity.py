@@ -469,3 +469,61 @@ def test_decode_dev_one_merge_ctc_kernel(orc, rh, head, rhead):
     synchronize()
     assert np.array_equal(dlz.numpy(), np.zeros(3, np.int64))
     assert np.array_equal(dcz.numpy(), np.zeros(3, np.float32))
+
+
+def test_guard_list_in_a_reused_workspace(orc, rh):
+    """The guarded-row list lives in the caller's workspace with an epoch-tagged header,
+    so a workspace filled with 0xff bytes, or left by a larger guarded call, must not leak
+    rows into the next call: argmax, decode and probabilities through one reused workspace
+    equal those of calls with their own fresh workspace, bit for bit.  The stress weights
+    (+-5 outliers) put many rows over the precision guard."""
+    from ppocr_rechead import workloads as wl
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    L = rh._lib.lib()
+    w_t, bias = wl.weights(stress=True)
+    q, s = orc.pack_int8(w_t)
+    h = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    rng = np.random.default_rng(41)
+    big = rng.standard_normal((1500, 120), dtype=np.float32)
+    big[rng.choice(1500, 200, replace=False)] *= np.float32(50.0)
+    small = rng.standard_normal((130, 120), dtype=np.float32)
+    ws_bytes = max(h.workspace_bytes(1500, mode) for mode in (2, 3))
+    ws = DeviceArray((ws_bytes,), np.uint8)
+    ws.fill_bytes(0xFF)
+
+    def argmax(a, mode, use_ws):
+        m = a.shape[0]
+        da, di, dp = DeviceArray.from_numpy(a), DeviceArray((m,), np.int32), DeviceArray((m,), np.float32)
+        rh._check(L.ppocr_rh_argmax_dev(h.handle, da.p, m, mode, di.p, dp.p, ws.p if use_ws else None,
+                                        ws_bytes if use_ws else 0, None))
+        synchronize()
+        return di.numpy(), dp.numpy().view(np.uint32)
+
+    def decode(a, mode, use_ws):
+        m = a.shape[0]
+        off = np.array([0, m // 3, m // 3, m], np.int64)
+        da, doff = DeviceArray.from_numpy(a), DeviceArray.from_numpy(off)
+        dsq, dln, dsc = DeviceArray((m,), np.int32), DeviceArray((3,), np.int64), DeviceArray((3,), np.float32)
+        rh._check(L.ppocr_rh_decode_dev(h.handle, da.p, m, doff.p, 3, mode, None, None, dsq.p, dln.p, dsc.p,
+                                        ws.p if use_ws else None, ws_bytes if use_ws else 0, None))
+        synchronize()
+        return dsq.numpy(), dln.numpy(), dsc.numpy().view(np.uint32)
+
+    def probs(a, mode, use_ws):
+        m = a.shape[0]
+        da, dpr = DeviceArray.from_numpy(a), DeviceArray((m, 18710), np.float32)
+        rh._check(L.ppocr_rh_probs_dev(h.handle, da.p, m, mode, dpr.p, ws.p if use_ws else None,
+                                       ws_bytes if use_ws else 0, None))
+        synchronize()
+        return (dpr.numpy().view(np.uint32),)
+
+    for fn in (argmax, decode, probs):
+        for a in (big, small, big[:700], small):
+            print(f"reused workspace: {fn.__name__} m={a.shape[0]}", flush=True)
+            for got, want in zip(fn(a, 2, True), fn(a, 2, False)):
+                assert np.array_equal(got, want), (fn.__name__, a.shape[0])
+    idx, _ = argmax(big, 2, True)
+    ref = orc.rechead_lines(big[:64], np.array([0, 64], np.int64), q, s, bias)
+    gap = top2_gap(f64_logits_q(big[:64], q, s, bias))
+    check_argmax(idx[:64], ref["idx"], gap, label="reused workspace, stress head")
+    h.close()
