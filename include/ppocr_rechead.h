@@ -35,6 +35,7 @@ extern "C" {
 #define PPOCR_ERR_INVALID_ARG 1 /* shape / argument error (OperatorError) */
 #define PPOCR_ERR_DEVICE 2      /* HIP runtime error */
 #define PPOCR_ERR_NO_MEMORY 3   /* device allocation failed */
+#define PPOCR_ERR_MODEL 4       /* model file unreadable or malformed (ModelError / SafeTensorsError) */
 
 /* How the projection's inner products are computed.  All modes accumulate in fp32 and
  * apply the per-class scale and bias in fp32 in the epilogue. */
@@ -70,6 +71,19 @@ int ppocr_rh_create(const int8_t* q, const float* scales, const float* bias, int
                     int64_t k, int device, ppocr_rh_t** out);
 int ppocr_rh_create_f32(const float* w_t, const float* bias, int64_t n, int64_t k, int device,
                         ppocr_rh_t** out);
+/* Head straight from a model file: replaces load_safetensors_model
+ * (src/engine/loader.rs:34-92) for the head's tensors, the prepack transpose
+ * (src/engine/model.rs:565-605) and, with quantize != 0, Model::quantize_matmul_weights
+ * (src/engine/model.rs:628-638).  The F32 weight `weight_name` is read as the model stores
+ * it, [k][n] (the B operand of MatMul.12, e.g. linear_8.w_0 [120, 18710]); `bias_name`
+ * (may be NULL) is the F32 bias [n] folded from the following Add.  The file is
+ * memory-mapped and the weight copied to the device as stored; the transpose, the INT8
+ * packing (bit-exact with ppocr_rh_pack_int8), the guard limits and the MFMA tile records
+ * are computed on the device.  The handle equals the one ppocr_rh_create (quantize != 0)
+ * or ppocr_rh_create_f32 (quantize == 0) makes from the transposed weight.  A missing or
+ * malformed file or tensor returns PPOCR_ERR_MODEL. */
+int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, const char* bias_name,
+                                     int quantize, int device, ppocr_rh_t** out);
 void ppocr_rh_destroy(ppocr_rh_t* h);
 
 /* Bytes this weight contributes to Model::weight_footprint_bytes

@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "kernels.hpp"
+#include "safetensors.hpp"
 
 namespace ppocr {
 
@@ -167,54 +168,73 @@ int upload(T** dst, const T* src, size_t count, size_t* total) {
     return PPOCR_OK;
 }
 
-int create_common(const int8_t* q, const float* w_t, const float* scales, const float* bias, int64_t n, int64_t k,
-                  int device, ppocr_rh_t** out) {
-    const char* op = q ? "MatMulQuantizedB" : "MatMulTransposedB";
+// Checks shared by every way of creating a head; makes `device` current.
+int check_create(const char* op, int64_t n, int64_t k, int device, ppocr_rh_t** out) {
     if (!out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": out handle pointer is null");
     *out = nullptr;
     if (n <= 0 || k <= 0) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": weight must have positive shape");
     if (n > (1LL << 30) || k > (1LL << 20)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": weight too large");
-    if ((q && !scales) || (!q && !w_t)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null weight pointer");
     int ndev = 0;
     PPOCR_HIP(hipGetDeviceCount(&ndev));
     if (device < 0 || device >= ndev)
         return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: device " + std::to_string(device) + " out of range");
-    DeviceGuard dg(device);
-    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: hipSetDevice failed");
+    return PPOCR_OK;
+}
 
-    std::unique_ptr<ppocr_rh, void (*)(ppocr_rh*)> h(new (std::nothrow) ppocr_rh, free_handle);
-    if (!h) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
+ppocr_rh* new_handle(int64_t n, int64_t k, bool quantized, int device) {
+    ppocr_rh* h = new (std::nothrow) ppocr_rh;
+    if (!h) return nullptr;
     h->device = device;
     h->n = n;
     h->k = k;
-    h->quantized = q != nullptr;
+    h->quantized = quantized;
     h->geom.G = (int)((k + 7) / 8);
-    h->geom.wplanes = q ? 1 : 2;
+    h->geom.wplanes = quantized ? 1 : 2;
     h->geom.tiles = (int)((n + 31) / 32);
     h->mfma_ok = mfma_supports_groups(h->geom.G);
+    return h;
+}
+
+// Guard limits of an INT8 head from wmax = max_c (float)max|q_c| * scale_c, w1 = max_c
+// sum_k |q_ck| * scale_c and bmax = max_c |b_c| (both in double).
+void set_limits(ppocr_rh* h, float wmax, double w1, double bmax) {
+    h->amax_limit = wmax > 0.0f ? 16.0f / wmax : INFINITY;
+    // logit range bound: the largest L1 norm of a dequantised weight row and the largest
+    // |bias|, rounded up by a small margin
+    const double room = (double)kLogitBound - bmax * 1.001;
+    if (room > 0.0 && std::isfinite(w1) && std::isfinite(bmax)) {
+        const double lim = w1 > 0.0 ? room / (w1 * 1.001) : INFINITY;
+        h->stats_amax_limit = (float)std::min((double)h->amax_limit, lim);
+        h->stats_noref = true;
+    }
+}
+
+int create_common(const int8_t* q, const float* w_t, const float* scales, const float* bias, int64_t n, int64_t k,
+                  int device, ppocr_rh_t** out) {
+    const char* op = q ? "MatMulQuantizedB" : "MatMulTransposedB";
+    if (int e = check_create(op, n, k, device, out)) return e;
+    if ((q && !scales) || (!q && !w_t)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null weight pointer");
+    DeviceGuard dg(device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: hipSetDevice failed");
+
+    std::unique_ptr<ppocr_rh, void (*)(ppocr_rh*)> h(new_handle(n, k, q != nullptr, device), free_handle);
+    if (!h) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
     if (q) {
         float wmax = 0.0f;
-        for (int64_t j = 0; j < n; ++j) {
-            int qm = 0;
-            for (int64_t kk = 0; kk < k; ++kk) qm = std::max(qm, std::abs((int)q[j * k + kk]));
-            wmax = std::max(wmax, (float)qm * scales[j]);
-        }
-        h->amax_limit = wmax > 0.0f ? 16.0f / wmax : INFINITY;
-        // logit range bound: the largest L1 norm of a dequantised weight row and the
-        // largest |bias| (in double, rounded up by a small margin)
         double w1 = 0.0, bmax = 0.0;
         for (int64_t j = 0; j < n; ++j) {
+            int qm = 0;
             int64_t l1 = 0;
-            for (int64_t kk = 0; kk < k; ++kk) l1 += std::abs((int)q[j * k + kk]);
+            for (int64_t kk = 0; kk < k; ++kk) {
+                const int v = std::abs((int)q[j * k + kk]);
+                qm = std::max(qm, v);
+                l1 += v;
+            }
+            wmax = std::max(wmax, (float)qm * scales[j]);
             w1 = std::max(w1, (double)l1 * (double)scales[j]);
             if (bias) bmax = std::max(bmax, std::fabs((double)bias[j]));
         }
-        const double room = (double)kLogitBound - bmax * 1.001;
-        if (room > 0.0 && std::isfinite(w1) && std::isfinite(bmax)) {
-            const double lim = w1 > 0.0 ? room / (w1 * 1.001) : INFINITY;
-            h->stats_amax_limit = (float)std::min((double)h->amax_limit, lim);
-            h->stats_noref = true;
-        }
+        set_limits(h.get(), wmax, w1, bmax);
     }
 
     std::vector<float> sc_host;
@@ -416,6 +436,101 @@ int ppocr_rh_create_f32(const float* w_t, const float* bias, int64_t n, int64_t 
         return fail(PPOCR_ERR_INVALID_ARG, "MatMulTransposedB: null weight pointer");
     }
     return create_common(nullptr, w_t, nullptr, bias, n, k, device, out);
+}
+
+int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, const char* bias_name, int quantize,
+                                     int device, ppocr_rh_t** out) {
+    const char* op = quantize ? "MatMulQuantizedB" : "MatMulTransposedB";
+    if (out) *out = nullptr;
+    if (!weight_name) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null weight name");
+    StFile f;
+    if (int e = f.open(path)) return e;
+    const StTensor* w = f.find(weight_name);
+    if (!w) return fail(PPOCR_ERR_MODEL, std::string("Model: tensor '") + weight_name + "' not found in the model file");
+    if (w->dtype != "F32" || w->shape.size() != 2)
+        return fail(PPOCR_ERR_MODEL, std::string("Model: tensor '") + weight_name + "' must be a 2-D F32 matrix [k][n]");
+    const int64_t k = w->shape[0], n = w->shape[1];
+    const StTensor* b = nullptr;
+    if (bias_name) {
+        b = f.find(bias_name);
+        if (!b) return fail(PPOCR_ERR_MODEL, std::string("Model: tensor '") + bias_name + "' not found in the model file");
+        if (b->dtype != "F32" || (int64_t)(b->bytes / 4) != n)
+            return fail(PPOCR_ERR_MODEL, std::string("Model: tensor '") + bias_name + "' must be F32 with " +
+                                             std::to_string(n) + " values");
+    }
+    if (int e = check_create(op, n, k, device, out)) return e;
+    DeviceGuard dg(device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: hipSetDevice failed");
+    std::unique_ptr<ppocr_rh, void (*)(ppocr_rh*)> h(new_handle(n, k, quantize != 0, device), free_handle);
+    if (!h) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
+
+    // the weight as stored ([k][n], straight from the mapped file), then W^T [n][k] on the
+    // device (the prepack), then the packed INT8 weight and its scales
+    const size_t nk = (size_t)(n * k);
+    DevBuf raw, wt;
+    if (int e = raw.alloc(nk * 4)) return e;
+    if (int e = wt.alloc(nk * 4)) return e;
+    PPOCR_HIP(hipMemcpy(raw.p, w->data, nk * 4, hipMemcpyHostToDevice));
+    if (int e = launch_transpose(raw.as<float>(), k, n, wt.as<float>(), nullptr)) return e;
+    size_t total = 0;
+    auto dev_alloc = [&](void** p, size_t bytes) -> int {
+        bytes = std::max<size_t>(bytes, 1);
+        if (hipMalloc(p, bytes) != hipSuccess) {
+            *p = nullptr;
+            (void)hipGetLastError();
+            return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation failed");
+        }
+        total += bytes;
+        return PPOCR_OK;
+    };
+    if (quantize) {
+        if (int e = dev_alloc((void**)&h->d_q, nk)) return e;
+    } else {
+        h->d_w = wt.as<float>();  // the handle keeps W^T
+        wt.p = nullptr;
+        total += std::max<size_t>(nk * 4, 1);
+    }
+    if (int e = dev_alloc((void**)&h->d_scale, (size_t)n * 4)) return e;
+    if (int e = dev_alloc((void**)&h->d_bias, (size_t)n * 4)) return e;
+    if (quantize) {
+        if (int e = launch_pack_int8(wt.as<float>(), n, k, h->d_q, h->d_scale, nullptr)) return e;
+    } else {
+        std::vector<float> ones((size_t)n, 1.0f);
+        PPOCR_HIP(hipMemcpy(h->d_scale, ones.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+    }
+    if (b) PPOCR_HIP(hipMemcpy(h->d_bias, b->data, (size_t)n * 4, hipMemcpyHostToDevice));
+    else PPOCR_HIP(hipMemset(h->d_bias, 0, (size_t)n * 4));
+    if (quantize) {
+        // guard limits from the packed weight, reduced on the device
+        DevBuf lim;
+        if (int e = lim.alloc(24)) return e;
+        PPOCR_HIP(hipMemset(lim.p, 0, 24));
+        unsigned long long* l64 = lim.as<unsigned long long>();
+        if (int e = launch_head_limits(h->d_q, h->d_scale, b ? h->d_bias : nullptr, n, k,
+                                       reinterpret_cast<unsigned*>(l64 + 2), l64, l64 + 1, nullptr))
+            return e;
+        unsigned long long hl[3];
+        PPOCR_HIP(hipMemcpy(hl, lim.p, 24, hipMemcpyDeviceToHost));
+        float wmax;
+        double w1, bmax;
+        const unsigned wbits = (unsigned)(hl[2] & 0xffffffffu);
+        std::memcpy(&wmax, &wbits, 4);
+        std::memcpy(&w1, &hl[0], 8);
+        std::memcpy(&bmax, &hl[1], 8);
+        set_limits(h.get(), wmax, w1, bmax);
+    }
+    if (h->mfma_ok) {
+        const size_t rec_bytes = (size_t)h->geom.tiles * h->geom.rec_bytes();
+        if (int e = dev_alloc((void**)&h->d_rec, rec_bytes)) return e;
+        PPOCR_HIP(hipMemset(h->d_rec, 0, rec_bytes));
+        if (int e = launch_build_records(h->geom, n, k, h->d_q, h->d_w, h->d_scale, b ? h->d_bias : nullptr, h->d_rec,
+                                         nullptr))
+            return e;
+    }
+    PPOCR_HIP(hipDeviceSynchronize());
+    h->device_bytes = total;
+    *out = h.release();
+    return PPOCR_OK;
 }
 
 void ppocr_rh_destroy(ppocr_rh_t* h) { free_handle(h); }

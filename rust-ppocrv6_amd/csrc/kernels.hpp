@@ -50,6 +50,18 @@ bool mfma_supports_groups(int G);
 int launch_pack_int8(const float* w_t, int64_t n, int64_t k, int8_t* q, float* scales,
                      hipStream_t st);
 
+// Head preparation on the device (a head created from a model file): dst [cols][rows] =
+// src [rows][cols]; the guard limits of an INT8 head as bit patterns of non-negative
+// values (wmax float, w1 and bmax double; maxima taken with atomicMax, so the outputs must
+// start at 0); the MFMA tile records (rec zeroed beforehand; q for an INT8 head, w for an
+// FP32 head).
+int launch_transpose(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t st);
+int launch_head_limits(const int8_t* q, const float* scales, const float* bias, int64_t n, int64_t k,
+                       unsigned* wmax_bits, unsigned long long* w1_bits, unsigned long long* bmax_bits,
+                       hipStream_t st);
+int launch_build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
+                         const float* scale, const float* bias, uint8_t* rec, hipStream_t st);
+
 int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                        int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.

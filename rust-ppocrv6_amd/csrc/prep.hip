@@ -1,0 +1,155 @@
+// Head preparation on the device, for a head created from a model file: the prepack
+// transpose (src/engine/model.rs:565-605), the precision and range limits of the split
+// activation modes, and the MFMA tile records.  Each produces exactly what the host path
+// of ppocr_rh_create / ppocr_rh_create_f32 computes from host arrays.
+#include "kernels.hpp"
+
+namespace ppocr {
+
+// dst[c][r] = src[r][c] for src [rows][cols], through a 32x33 LDS tile (coalesced reads
+// and writes).  Block 32x8 threads, one 32x32 tile per block.
+__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ src, int64_t rows, int64_t cols,
+                                                        float* __restrict__ dst) {
+    __shared__ float tile[32][33];
+    const int64_t c0 = (int64_t)blockIdx.x * 32, r0 = (int64_t)blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+    for (int y = ty; y < 32; y += 8) {
+        const int64_t r = r0 + y, c = c0 + tx;
+        if (r < rows && c < cols) tile[y][tx] = src[r * cols + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int y = ty; y < 32; y += 8) {
+        const int64_t c = c0 + y, r = r0 + tx;
+        if (c < cols && r < rows) dst[c * rows + r] = tile[tx][y];
+    }
+}
+
+int launch_transpose(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t st) {
+    if (rows <= 0 || cols <= 0) return PPOCR_OK;
+    const int64_t gx = (cols + 31) / 32, gy = (rows + 31) / 32;
+    if (gx > 0x7fffffffLL || gy > 65535) return fail(PPOCR_ERR_INVALID_ARG, "Transpose: matrix too large");
+    transpose_kernel<<<dim3((unsigned)gx, (unsigned)gy), 256, 0, st>>>(src, rows, cols, dst);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+// Per class row j of an INT8 head (one wave per row): the largest |dequantised weight|
+// (float, (float)max|q| * scale, as the host computes it), the L1 norm of the dequantised
+// row in double, and |bias| in double (NaN ignored, as std::max ignores it on the host).
+// Maxima of non-negative values are taken on their bit patterns, which order the same way.
+__global__ __launch_bounds__(256) void head_limits_kernel(const int8_t* __restrict__ q, const float* __restrict__ scales,
+                                                          const float* __restrict__ bias, int64_t n, int64_t k,
+                                                          unsigned* wmax_bits, unsigned long long* w1_bits,
+                                                          unsigned long long* bmax_bits) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    int qm = 0, l1 = 0;
+    for (int64_t i = lane; i < k; i += 64) {
+        const int v = abs((int)q[row * k + i]);
+        qm = max(qm, v);
+        l1 += v;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        qm = max(qm, __shfl_xor(qm, o, 64));
+        l1 += __shfl_xor(l1, o, 64);
+    }
+    if (lane == 0) {
+        const float wm = __fmul_rn((float)qm, scales[row]);
+        if (wm == wm) atomicMax(wmax_bits, __float_as_uint(wm));
+        const double w1 = (double)l1 * (double)scales[row];
+        if (w1 == w1) atomicMax(w1_bits, (unsigned long long)__double_as_longlong(w1));
+        if (bias) {
+            const double b = fabs((double)bias[row]);
+            if (b == b) atomicMax(bmax_bits, (unsigned long long)__double_as_longlong(b));
+        }
+    }
+}
+
+int launch_head_limits(const int8_t* q, const float* scales, const float* bias, int64_t n, int64_t k,
+                       unsigned* wmax_bits, unsigned long long* w1_bits, unsigned long long* bmax_bits,
+                       hipStream_t st) {
+    if (n <= 0) return PPOCR_OK;
+    if ((n + 3) / 4 > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: too many classes");
+    head_limits_kernel<<<(unsigned)((n + 3) / 4), 256, 0, st>>>(q, scales, bias, n, k, wmax_bits, w1_bits, bmax_bits);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+// bf16 bits of x, rounded to nearest even; NaN stays NaN (quiet).  The same integer steps
+// as the host's record builder.
+__device__ __forceinline__ unsigned short bf16_bits_rne_dev(float x) {
+    unsigned u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (unsigned short)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (unsigned short)(u >> 16);
+}
+
+// One thread per (tile, class i, group g): the 8 bf16 weights of that group (and the low
+// plane of an FP32 head); the threads of group 0 also write the class's epilogue
+// constants.  Entries past k stay zero, classes past n get zero weights, scale 0 and
+// bias*log2e = -inf.
+__global__ __launch_bounds__(256) void build_records_kernel(int tiles, int G, int wplanes, int64_t n, int64_t k,
+                                                            const int8_t* __restrict__ q, const float* __restrict__ w,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ bias, uint8_t* __restrict__ rec) {
+    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_tile = 32LL * G;
+    if (x >= (int64_t)tiles * per_tile) return;
+    const int t = (int)(x / per_tile);
+    const int rem = (int)(x % per_tile);
+    const int g = rem / 32, i = rem % 32;
+    const size_t frag_bytes = (size_t)wplanes * G * 512;
+    uint8_t* r = rec + (size_t)t * (frag_bytes + 512);
+    unsigned short* frag = reinterpret_cast<unsigned short*>(r);
+    const int64_t row = (int64_t)t * 32 + i;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t kk = (int64_t)g * 8 + e;
+        unsigned short hi = 0, lo = 0;
+        if (row < n && kk < k) {
+            if (q) {
+                hi = bf16_bits_rne_dev((float)q[row * k + kk]);  // exact
+            } else {
+                const float v = w[row * k + kk];
+                hi = bf16_bits_rne_dev(v);
+                lo = bf16_bits_rne_dev(__fsub_rn(v, __uint_as_float((unsigned)hi << 16)));
+            }
+        }
+        frag[((size_t)(0 * G + g) * 32 + i) * 8 + e] = hi;
+        if (wplanes == 2) frag[((size_t)(1 * G + g) * 32 + i) * 8 + e] = lo;
+    }
+    if (g == 0) {
+        float* ep = reinterpret_cast<float*>(r + frag_bytes);
+        if (row < n) {
+            const float sc = scale[row], bi = bias ? bias[row] : 0.0f;
+            ep[i] = __fmul_rn(sc, kLog2e);
+            ep[32 + i] = __fmul_rn(bi, kLog2e);
+            ep[64 + i] = sc;
+            ep[96 + i] = bi;
+        } else {
+            ep[i] = 0.0f;
+            ep[32 + i] = -INFINITY;
+            ep[64 + i] = 0.0f;
+            ep[96 + i] = 0.0f;
+        }
+    }
+}
+
+int launch_build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
+                         const float* scale, const float* bias, uint8_t* rec, hipStream_t st) {
+    if (k > 8LL * g.G || g.tiles != (int)((n + 31) / 32) || (q == nullptr) != (g.wplanes == 2))
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
+    const int64_t threads = (int64_t)g.tiles * 32 * g.G;
+    if (threads <= 0) return PPOCR_OK;
+    if ((threads + 255) / 256 > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: too many classes");
+    build_records_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(g.tiles, g.G, g.wplanes, n, k, q, w, scale,
+                                                                             bias, rec);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+}  // namespace ppocr

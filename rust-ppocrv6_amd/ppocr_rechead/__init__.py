@@ -14,12 +14,13 @@ Every computation runs in libppocr_rechead.so (hand-written gfx950 kernels).  Er
 come back as OcrError(op, msg), the shape of OcrError::OperatorError (src/error.rs).
 """
 import ctypes
+import os
 
 import numpy as np
 
 from . import _lib
 from ._lib import (MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
-                   PPOCR_ERR_INVALID_ARG, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
+                   PPOCR_ERR_INVALID_ARG, PPOCR_ERR_MODEL, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
 
 __all__ = [
     "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "matmul_quantized_b", "matmul_transposed_b",
@@ -105,6 +106,23 @@ class RecHead:
             _check(_lib.lib().ppocr_rh_create_f32(_ptr(w_t), _ptr(bias_c), self.n, self.k, device,
                                                   ctypes.byref(self._h)))
         self.default_mode = MODE_BF16X2 if self.quantized else MODE_BF16X3
+
+    @classmethod
+    def from_safetensors(cls, path, weight_name, bias_name=None, quantize=True, device=0):
+        """The head straight from a model file (load_safetensors_model, src/engine/loader.rs:34-92,
+        then the prepack and, with `quantize`, Model::quantize_matmul_weights): `weight_name`
+        is the F32 [k][n] MatMul weight as stored, `bias_name` its F32 [n] bias.  Transpose,
+        INT8 packing and the tile records run on the GPU."""
+        self = cls.__new__(cls)
+        self._h = ctypes.c_void_p()
+        enc = (lambda x: None if x is None else os.fsencode(x))
+        _check(_lib.lib().ppocr_rh_create_from_safetensors(enc(path), enc(weight_name), enc(bias_name),
+                                                           1 if quantize else 0, device, ctypes.byref(self._h)))
+        n, k, q = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+        _check(_lib.lib().ppocr_rh_shape(self._h, ctypes.byref(n), ctypes.byref(k), ctypes.byref(q)))
+        self.n, self.k, self.quantized = n.value, k.value, bool(q.value)
+        self.default_mode = MODE_BF16X2 if self.quantized else MODE_BF16X3
+        return self
 
     def close(self):
         if self._h:

@@ -14,6 +14,7 @@ PPOCR_OK = 0
 PPOCR_ERR_INVALID_ARG = 1
 PPOCR_ERR_DEVICE = 2
 PPOCR_ERR_NO_MEMORY = 3
+PPOCR_ERR_MODEL = 4
 
 MODE_FP32_FMA = 0
 MODE_BF16X1 = 1
@@ -33,6 +34,8 @@ SIGNATURES = {
     "ppocr_rh_pack_int8_dev": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "ppocr_rh_create": (_int, [_vp, _vp, _vp, _i64, _i64, _int, ctypes.POINTER(_vp)]),
     "ppocr_rh_create_f32": (_int, [_vp, _vp, _i64, _i64, _int, ctypes.POINTER(_vp)]),
+    "ppocr_rh_create_from_safetensors": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _int, _int,
+                                                ctypes.POINTER(_vp)]),
     "ppocr_rh_destroy": (None, [_vp]),
     "ppocr_rh_footprint_bytes": (_sz, [_vp]),
     "ppocr_rh_device_bytes": (_sz, [_vp]),

@@ -1,0 +1,85 @@
+"""A head created from a model file (ppocr_rh_create_from_safetensors: transpose, INT8
+packing, guard limits and tile records on the device) equals the head created from the
+host-transposed weight (ppocr_rh_create / ppocr_rh_create_f32), bit for bit in every
+output, for the PP-OCRv6 small head (120 x 18710), the tiny head's k = 80 and shapes
+without an MFMA path."""
+import numpy as np
+import pytest
+
+from gpu_common import check_argmax, f64_logits_q, top2_gap
+
+pytestmark = pytest.mark.gpu
+
+
+def _save(tmp_path, w_kn, bias, name="rec.safetensors"):
+    from safetensors.numpy import save_file
+    path = str(tmp_path / name)
+    t = {"linear_8.w_0": np.ascontiguousarray(w_kn, np.float32)}
+    if bias is not None:
+        t["linear_8.b_0"] = np.ascontiguousarray(bias, np.float32)
+    save_file(t, path, metadata={"graph": "{}"})
+    return path
+
+
+def _same(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape
+    if a.dtype == np.float32:
+        a, b = a.view(np.uint32), b.view(np.uint32)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("k,n,with_bias", [(120, 18710, True), (80, 6906, True), (120, 70, False), (50, 33, True)])
+def test_int8_head_from_file_equals_host_packed(orc, rh, tmp_path, k, n, with_bias):
+    rng = np.random.default_rng(k * 7 + n)
+    w_t = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    w_t[3] = 0.0                       # an all-zero class: scale 1.0
+    w_t[5, 7] = 5.0                    # an outlier class
+    bias = (rng.standard_normal(n) * 0.01).astype(np.float32) if with_bias else None
+    path = _save(tmp_path, w_t.T, bias)
+    print(f"model file head k={k} n={n} bias={with_bias}", flush=True)
+    hf = rh.RecHead.from_safetensors(path, "linear_8.w_0", "linear_8.b_0" if with_bias else None)
+    q, s = orc.pack_int8(w_t)
+    hh = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    assert (hf.n, hf.k, hf.quantized) == (n, k, True)
+    assert hf.weight_footprint_bytes() == hh.weight_footprint_bytes() == n * k + 4 * n
+    assert hf.device_bytes() == hh.device_bytes()
+    a = rng.standard_normal((300, k)).astype(np.float32)
+    a[::37] *= np.float32(40.0)        # rows over the precision guard
+    modes = (0, 2, 3) if k in (120, 80) else (0,)
+    for mode in modes:
+        _same(hf.logits(a, mode), hh.logits(a, mode))
+        i1, p1 = hf.argmax(a, mode)
+        i2, p2 = hh.argmax(a, mode)
+        _same(i1, i2)
+        _same(p1, p2)
+    if k in (120, 80):
+        _same(hf.probs(a[:40], 2), hh.probs(a[:40], 2))
+        idx, _ = hf.argmax(a, 2)
+        ref = orc.rechead_lines(a, np.array([0, 300], np.int64), q, s, bias)
+        check_argmax(idx, ref["idx"], top2_gap(f64_logits_q(a, q, s, bias)), label=f"file head k={k}")
+    hf.close()
+    hh.close()
+
+
+@pytest.mark.parametrize("k,n", [(120, 18710), (80, 6906), (50, 33)])
+def test_fp32_head_from_file_equals_host_transposed(rh, tmp_path, k, n):
+    rng = np.random.default_rng(k + n)
+    w_t = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.01).astype(np.float32)
+    path = _save(tmp_path, w_t.T, bias)
+    print(f"model file fp32 head k={k} n={n}", flush=True)
+    hf = rh.RecHead.from_safetensors(path, "linear_8.w_0", "linear_8.b_0", quantize=False)
+    hh = rh.RecHead(w_t=w_t, bias=bias)
+    assert (hf.n, hf.k, hf.quantized) == (n, k, False)
+    assert hf.weight_footprint_bytes() == hh.weight_footprint_bytes() == 4 * n * k
+    assert hf.device_bytes() == hh.device_bytes()
+    a = rng.standard_normal((200, k)).astype(np.float32)
+    for mode in ((0, 1, 3) if k in (120, 80) else (0,)):
+        _same(hf.logits(a, mode), hh.logits(a, mode))
+        i1, p1 = hf.argmax(a, mode)
+        i2, p2 = hh.argmax(a, mode)
+        _same(i1, i2)
+        _same(p1, p2)
+    hf.close()
+    hh.close()
