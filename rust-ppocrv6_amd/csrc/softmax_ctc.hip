@@ -175,18 +175,34 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
 // probability).  Every kernel that merges partials uses this one order, so their results
 // agree bit for bit.
 constexpr int kMergeLanes = 8;
+constexpr int kMergeBatch = 8;  // partials per lane loaded together (all of them for nsplit <= 64)
 __device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, const float* __restrict__ p_sum,
                                               const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
                                               bool valid, int g, float* inv_out) {
     RowStat s{-INFINITY, 0.0f, 0.0f, 0};
     if (valid) {
-        for (int c = g; c < nsplit; c += kMergeLanes) {
-            RowStat o;
-            o.best = p_best[(int64_t)c * m + row];
-            o.sum = p_sum[(int64_t)c * m + row];
-            o.ref = (o.best == -INFINITY) ? 0.0f : o.best;  // partial sums are relative to their max
-            o.idx = p_idx[(int64_t)c * m + row];
-            s = stat_merge(s, o);
+        // chunks g, g + 8, g + 16, ... in order; up to kMergeBatch of them are loaded before
+        // any is merged, so their loads are in flight together
+        for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
+            float bv[kMergeBatch], sv[kMergeBatch];
+            int iv[kMergeBatch];
+#pragma unroll
+            for (int x = 0; x < kMergeBatch; ++x) {
+                const int c = c0 + x * kMergeLanes;
+                if (c < nsplit) {
+                    bv[x] = p_best[(int64_t)c * m + row];
+                    sv[x] = p_sum[(int64_t)c * m + row];
+                    iv[x] = p_idx[(int64_t)c * m + row];
+                }
+            }
+#pragma unroll
+            for (int x = 0; x < kMergeBatch; ++x) {
+                if (c0 + x * kMergeLanes < nsplit) {
+                    // partial sums are relative to their own maximum
+                    const RowStat o{bv[x], sv[x], (bv[x] == -INFINITY) ? 0.0f : bv[x], iv[x]};
+                    s = stat_merge(s, o);
+                }
+            }
         }
     }
 #pragma unroll
@@ -224,7 +240,8 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
 
 // One wavefront per text line.  Steps are taken 64 at a time; the emit mask is a ballot,
 // emitted indices are compacted by prefix popcount, and the score is summed in step order
-// (every lane runs the same sequential sum over shuffled values).
+// (every lane runs the same sequential sum over the emitting lanes' values, read lane by
+// lane).
 __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restrict__ idx,
                                                          const float* __restrict__ val,
                                                          const int64_t* __restrict__ line_off, int64_t lines,
@@ -248,9 +265,9 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
         if (emit) seq[t0 + cnt + pos] = id;
         uint64_t mm = mask;
         while (mm) {
-            const int src = __ffsll((unsigned long long)mm) - 1;
+            const int src = __builtin_ctzll(mm);  // wave-uniform
             mm &= mm - 1;
-            sum += __shfl(v, src, 64);
+            sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
         }
         cnt += __popcll(mask);
     }
@@ -313,9 +330,9 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
                 if (emit) seq[t0 + cnt + pos] = cid;
                 uint64_t mm = mask;
                 while (mm) {
-                    const int src = __ffsll((unsigned long long)mm) - 1;
+                    const int src = __builtin_ctzll(mm);  // wave-uniform
                     mm &= mm - 1;
-                    sum += __shfl(cv, src, 64);
+                    sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), src));
                 }
                 cnt += __popcll(mask);
             }

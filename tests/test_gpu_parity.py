@@ -507,7 +507,10 @@ def test_guard_list_in_a_reused_workspace(orc, rh):
         rh._check(L.ppocr_rh_decode_dev(h.handle, da.p, m, doff.p, 3, mode, None, None, dsq.p, dln.p, dsc.p,
                                         ws.p if use_ws else None, ws_bytes if use_ws else 0, None))
         synchronize()
-        return dsq.numpy(), dln.numpy(), dsc.numpy().view(np.uint32)
+        ln = dln.numpy()
+        # only seq[off[b] .. off[b] + len[b]) is defined; the rest of the array is not written
+        emitted = np.concatenate([dsq.numpy()[off[b]:off[b] + ln[b]] for b in range(3)])
+        return emitted, ln, dsc.numpy().view(np.uint32)
 
     def probs(a, mode, use_ws):
         m = a.shape[0]
