@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -63,6 +64,165 @@ struct DeviceGuard {
         int cur = -1;
         if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
     }
+};
+
+// Device memory of the host-pointer entry points.  Each call takes an arena (one device
+// allocation, a pinned host staging buffer and a stream of its own) from a pool, lays its
+// inputs, outputs and workspace out in it, and gives it back, so a call costs its copies
+// and kernels rather than allocations.  Inputs and outputs of up to kStageBytes move as
+// one copy each way through the pinned buffer; larger ones are copied directly.  Calls
+// running at the same time take different arenas.  Arenas above kArenaKeepBytes are freed
+// after the call instead of kept (the logits of a large batch need gigabytes once).  The
+// pool lives until the process ends.
+constexpr size_t kArenaKeepBytes = 256u << 20;
+constexpr size_t kStageBytes = 4u << 20;
+
+struct HostArena {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    uint8_t* base = nullptr;
+    size_t cap = 0;
+    uint8_t* pinned = nullptr;  // kStageBytes, allocated on first use
+};
+
+class ArenaPool {
+public:
+    HostArena* take(int device) {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (size_t i = 0; i < idle_.size(); ++i) {
+            if (idle_[i]->device == device) {
+                HostArena* a = idle_[i];
+                idle_.erase(idle_.begin() + (std::ptrdiff_t)i);
+                return a;
+            }
+        }
+        HostArena* a = new (std::nothrow) HostArena;
+        if (a) a->device = device;
+        return a;
+    }
+    void give(HostArena* a) {
+        std::lock_guard<std::mutex> lk(mu_);
+        idle_.push_back(a);
+    }
+
+private:
+    std::mutex mu_;
+    std::vector<HostArena*> idle_;
+};
+
+ArenaPool& arena_pool() {
+    static ArenaPool* pool = new ArenaPool;  // never destroyed: arenas may be in use until exit
+    return *pool;
+}
+
+size_t align256(size_t x) { return (std::max<size_t>(x, 1) + 255) / 256 * 256; }
+
+// One host-pointer call on the current device: inputs, then outputs, then the workspace,
+// each 256-byte aligned in the arena.  The destructor waits for the call's stream before
+// the arena goes back.
+class HostCall {
+public:
+    ~HostCall() {
+        if (!a_) return;
+        (void)hipStreamSynchronize(a_->stream);
+        if (a_->cap > kArenaKeepBytes) {
+            (void)hipFree(a_->base);
+            a_->base = nullptr;
+            a_->cap = 0;
+        }
+        arena_pool().give(a_);
+    }
+    int begin(std::initializer_list<size_t> in, std::initializer_list<size_t> out, size_t ws) {
+        int dev = 0;
+        PPOCR_HIP(hipGetDevice(&dev));
+        a_ = arena_pool().take(dev);
+        if (!a_) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
+        if (!a_->stream) PPOCR_HIP(hipStreamCreateWithFlags(&a_->stream, hipStreamNonBlocking));
+        size_t total = 0;
+        for (size_t r : in) place(r, &total, &in_);
+        in_end_ = total;
+        for (size_t r : out) place(r, &total, &out_);
+        out_end_ = total;
+        ws_off_ = total;
+        ws_bytes_ = align256(ws);
+        total += ws_bytes_;
+        if (a_->cap < total) {
+            if (a_->base) (void)hipFree(a_->base);
+            a_->base = nullptr;
+            a_->cap = 0;
+            void* p = nullptr;
+            if (hipMalloc(&p, total) != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation of " + std::to_string(total) +
+                                                     " bytes failed");
+            }
+            a_->base = static_cast<uint8_t*>(p);
+            a_->cap = total;
+        }
+        if (!a_->pinned && (in_end_ <= kStageBytes || out_end_ - in_end_ <= kStageBytes)) {
+            void* p = nullptr;
+            if (hipHostMalloc(&p, kStageBytes, hipHostMallocDefault) == hipSuccess) a_->pinned = static_cast<uint8_t*>(p);
+            else (void)hipGetLastError();  // no staging: copies go directly
+        }
+        return PPOCR_OK;
+    }
+    template <typename T>
+    T* in(size_t i) const {
+        return reinterpret_cast<T*>(a_->base + in_[i].first);
+    }
+    template <typename T>
+    T* out(size_t i) const {
+        return reinterpret_cast<T*>(a_->base + out_[i].first);
+    }
+    uint8_t* ws() const { return a_->base + ws_off_; }
+    size_t ws_bytes() const { return ws_bytes_; }
+    hipStream_t stream() const { return a_->stream; }
+    // Copies the inputs (srcs in the order given to begin) to the device.
+    int copy_in(std::initializer_list<const void*> srcs) const {
+        size_t i = 0;
+        const bool staged = a_->pinned && in_end_ <= kStageBytes;
+        for (const void* src : srcs) {
+            const auto [off, n] = in_[i++];
+            if (!n || !src) continue;
+            if (staged) std::memcpy(a_->pinned + off, src, n);
+            else PPOCR_HIP(hipMemcpyAsync(a_->base + off, src, n, hipMemcpyHostToDevice, a_->stream));
+        }
+        if (staged && in_end_) PPOCR_HIP(hipMemcpyAsync(a_->base, a_->pinned, in_end_, hipMemcpyHostToDevice, a_->stream));
+        return PPOCR_OK;
+    }
+    // Copies the outputs back (dsts in the order given to begin; null ones are skipped) and
+    // waits for the call to finish.
+    int copy_out(std::initializer_list<void*> dsts) const {
+        const size_t span = out_end_ - in_end_;
+        const bool staged = a_->pinned && span <= kStageBytes;
+        if (staged) {
+            if (span) PPOCR_HIP(hipMemcpyAsync(a_->pinned, a_->base + in_end_, span, hipMemcpyDeviceToHost, a_->stream));
+        } else {
+            size_t i = 0;
+            for (void* dst : dsts) {
+                const auto [off, n] = out_[i++];
+                if (n && dst) PPOCR_HIP(hipMemcpyAsync(dst, a_->base + off, n, hipMemcpyDeviceToHost, a_->stream));
+            }
+        }
+        PPOCR_HIP(hipStreamSynchronize(a_->stream));
+        if (staged) {
+            size_t i = 0;
+            for (void* dst : dsts) {
+                const auto [off, n] = out_[i++];
+                if (n && dst) std::memcpy(dst, a_->pinned + (off - in_end_), n);
+            }
+        }
+        return PPOCR_OK;
+    }
+
+private:
+    static void place(size_t bytes, size_t* total, std::vector<std::pair<size_t, size_t>>* v) {
+        v->push_back({*total, bytes});
+        *total += align256(bytes);
+    }
+    HostArena* a_ = nullptr;
+    std::vector<std::pair<size_t, size_t>> in_, out_;  // (offset, bytes)
+    size_t in_end_ = 0, out_end_ = 0, ws_off_ = 0, ws_bytes_ = 0;
 };
 
 // Device buffer owned for the duration of a host-pointer call.
@@ -586,13 +746,14 @@ int ppocr_rh_logits(const ppocr_rh_t* h, const float* a, int64_t m, int mode, fl
     if (m == 0) return PPOCR_OK;
     if (!a || !out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null pointer");
     DeviceGuard dg(h->device);
-    DevBuf da, dout;
-    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
-    if (int e = dout.alloc((size_t)(m * h->n) * 4)) return e;
-    PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
-    if (int e = ppocr_rh_logits_dev(h, da.as<float>(), m, mode, dout.as<float>(), nullptr, 0, nullptr)) return e;
-    PPOCR_HIP(hipMemcpy(out, dout.p, (size_t)(m * h->n) * 4, hipMemcpyDeviceToHost));
-    return PPOCR_OK;
+    const size_t ab = (size_t)(m * h->k) * 4, ob = (size_t)(m * h->n) * 4;
+    const size_t wsb = cfg >= 0 ? ws_layout(m, nsplit_for(h, m, cfg)).total : 0;
+    HostCall hc;
+    if (int e = hc.begin({ab}, {ob}, wsb)) return e;
+    if (int e = hc.copy_in({a})) return e;
+    if (int e = ppocr_rh_logits_dev(h, hc.in<float>(0), m, mode, hc.out<float>(0), hc.ws(), hc.ws_bytes(), hc.stream()))
+        return e;
+    return hc.copy_out({out});
 }
 
 int ppocr_softmax_rows_dev(float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, float* d_maxprob, void* stream) {
@@ -606,12 +767,14 @@ int ppocr_softmax_rows(float* x, int64_t rows, int64_t cols) {
     if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: negative shape");
     if (rows == 0 || cols == 0) return PPOCR_OK;  // empty input: nothing to do (src/ops/softmax.rs:226-229)
     if (!x) return fail(PPOCR_ERR_INVALID_ARG, "Softmax: null pointer");
-    DevBuf dx;
-    if (int e = dx.alloc((size_t)(rows * cols) * 4)) return e;
-    PPOCR_HIP(hipMemcpy(dx.p, x, (size_t)(rows * cols) * 4, hipMemcpyHostToDevice));
-    if (int e = launch_softmax_rows(dx.as<float>(), rows, cols, nullptr, nullptr, nullptr)) return e;
-    PPOCR_HIP(hipMemcpy(x, dx.p, (size_t)(rows * cols) * 4, hipMemcpyDeviceToHost));
-    return PPOCR_OK;
+    const size_t xb = (size_t)(rows * cols) * 4;
+    HostCall hc;
+    if (int e = hc.begin({xb}, {}, 0)) return e;
+    if (int e = hc.copy_in({x})) return e;
+    if (int e = launch_softmax_rows(hc.in<float>(0), rows, cols, nullptr, nullptr, hc.stream())) return e;
+    // in place: the result goes back over the input
+    PPOCR_HIP(hipMemcpyAsync(x, hc.in<float>(0), xb, hipMemcpyDeviceToHost, hc.stream()));
+    return hc.copy_out({});
 }
 
 int ppocr_argmax_rows_dev(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, float* d_val, void* stream) {
@@ -625,15 +788,13 @@ int ppocr_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx, 
     if (rows < 0 || cols < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative shape");
     if (rows == 0) return PPOCR_OK;
     if ((!x && cols) || !idx || !val) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
-    DevBuf dx, di, dv;
-    if (int e = dx.alloc((size_t)(rows * cols) * 4)) return e;
-    if (int e = di.alloc((size_t)rows * 4)) return e;
-    if (int e = dv.alloc((size_t)rows * 4)) return e;
-    if (rows * cols) PPOCR_HIP(hipMemcpy(dx.p, x, (size_t)(rows * cols) * 4, hipMemcpyHostToDevice));
-    if (int e = launch_argmax_rows(dx.as<float>(), rows, cols, di.as<int32_t>(), dv.as<float>(), nullptr)) return e;
-    PPOCR_HIP(hipMemcpy(idx, di.p, (size_t)rows * 4, hipMemcpyDeviceToHost));
-    PPOCR_HIP(hipMemcpy(val, dv.p, (size_t)rows * 4, hipMemcpyDeviceToHost));
-    return PPOCR_OK;
+    const size_t xb = (size_t)(rows * cols) * 4, rb = (size_t)rows * 4;
+    HostCall hc;
+    if (int e = hc.begin({xb}, {rb, rb}, 0)) return e;
+    if (int e = hc.copy_in({x})) return e;
+    if (int e = launch_argmax_rows(hc.in<float>(0), rows, cols, hc.out<int32_t>(0), hc.out<float>(1), hc.stream()))
+        return e;
+    return hc.copy_out({idx, val});
 }
 
 int ppocr_rh_argmax_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, int32_t* d_idx, float* d_maxprob,
@@ -660,18 +821,14 @@ int ppocr_rh_argmax(const ppocr_rh_t* h, const float* a, int64_t m, int mode, in
     if (m == 0) return PPOCR_OK;
     if (!a || !idx || !maxprob) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
     DeviceGuard dg(h->device);
-    DevBuf da, di, dp, dws;
-    const size_t wsb = ws_layout(m, nsplit_for(h, m, cfg)).total;
-    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
-    if (int e = di.alloc((size_t)m * 4)) return e;
-    if (int e = dp.alloc((size_t)m * 4)) return e;
-    if (int e = dws.alloc(wsb)) return e;
-    PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
-    if (int e = ppocr_rh_argmax_dev(h, da.as<float>(), m, mode, di.as<int32_t>(), dp.as<float>(), dws.p, wsb, nullptr))
+    const size_t ab = (size_t)(m * h->k) * 4, rb = (size_t)m * 4;
+    HostCall hc;
+    if (int e = hc.begin({ab}, {rb, rb}, ws_layout(m, nsplit_for(h, m, cfg)).total)) return e;
+    if (int e = hc.copy_in({a})) return e;
+    if (int e = ppocr_rh_argmax_dev(h, hc.in<float>(0), m, mode, hc.out<int32_t>(0), hc.out<float>(1), hc.ws(),
+                                    hc.ws_bytes(), hc.stream()))
         return e;
-    PPOCR_HIP(hipMemcpy(idx, di.p, (size_t)m * 4, hipMemcpyDeviceToHost));
-    PPOCR_HIP(hipMemcpy(maxprob, dp.p, (size_t)m * 4, hipMemcpyDeviceToHost));
-    return PPOCR_OK;
+    return hc.copy_out({idx, maxprob});
 }
 
 int ppocr_rh_probs_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, float* d_probs, void* d_workspace,
@@ -704,15 +861,13 @@ int ppocr_rh_probs(const ppocr_rh_t* h, const float* a, int64_t m, int mode, flo
     if (m == 0) return PPOCR_OK;
     if (!a || !probs) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
     DeviceGuard dg(h->device);
-    DevBuf da, dp, dws;
-    const size_t wsb = ws_layout(m, nsplit_for(h, m, cfg)).total;
-    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
-    if (int e = dp.alloc((size_t)(m * h->n) * 4)) return e;
-    if (int e = dws.alloc(wsb)) return e;
-    PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
-    if (int e = ppocr_rh_probs_dev(h, da.as<float>(), m, mode, dp.as<float>(), dws.p, wsb, nullptr)) return e;
-    PPOCR_HIP(hipMemcpy(probs, dp.p, (size_t)(m * h->n) * 4, hipMemcpyDeviceToHost));
-    return PPOCR_OK;
+    const size_t ab = (size_t)(m * h->k) * 4, pb = (size_t)(m * h->n) * 4;
+    HostCall hc;
+    if (int e = hc.begin({ab}, {pb}, ws_layout(m, nsplit_for(h, m, cfg)).total)) return e;
+    if (int e = hc.copy_in({a})) return e;
+    if (int e = ppocr_rh_probs_dev(h, hc.in<float>(0), m, mode, hc.out<float>(0), hc.ws(), hc.ws_bytes(), hc.stream()))
+        return e;
+    return hc.copy_out({probs});
 }
 
 int ppocr_ctc_greedy_dev(const int32_t* d_idx, const float* d_maxprob, const int64_t* d_line_off, int64_t lines,
@@ -740,25 +895,14 @@ int ppocr_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* li
     if (int e = check_offsets(line_off, lines)) return e;
     const int64_t steps = line_off[lines];
     if (steps > 0 && (!idx || !maxprob || !seq)) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
-    DevBuf di, dv, doff, dseq, dlen, dsc;
-    if (int e = di.alloc((size_t)steps * 4)) return e;
-    if (int e = dv.alloc((size_t)steps * 4)) return e;
-    if (int e = doff.alloc((size_t)(lines + 1) * 8)) return e;
-    if (int e = dseq.alloc((size_t)steps * 4)) return e;
-    if (int e = dlen.alloc((size_t)lines * 8)) return e;
-    if (int e = dsc.alloc((size_t)lines * 4)) return e;
-    if (steps) {
-        PPOCR_HIP(hipMemcpy(di.p, idx, (size_t)steps * 4, hipMemcpyHostToDevice));
-        PPOCR_HIP(hipMemcpy(dv.p, maxprob, (size_t)steps * 4, hipMemcpyHostToDevice));
-    }
-    PPOCR_HIP(hipMemcpy(doff.p, line_off, (size_t)(lines + 1) * 8, hipMemcpyHostToDevice));
-    if (int e = launch_ctc_greedy(di.as<int32_t>(), dv.as<float>(), doff.as<int64_t>(), lines, blank,
-                                  dseq.as<int32_t>(), dlen.as<int64_t>(), dsc.as<float>(), nullptr))
+    const size_t sb = (size_t)steps * 4, ob = (size_t)(lines + 1) * 8;
+    HostCall hc;
+    if (int e = hc.begin({sb, sb, ob}, {sb, (size_t)lines * 8, (size_t)lines * 4}, 0)) return e;
+    if (int e = hc.copy_in({idx, maxprob, line_off})) return e;
+    if (int e = launch_ctc_greedy(hc.in<int32_t>(0), hc.in<float>(1), hc.in<int64_t>(2), lines, blank,
+                                  hc.out<int32_t>(0), hc.out<int64_t>(1), hc.out<float>(2), hc.stream()))
         return e;
-    PPOCR_HIP(hipMemcpy(seq_len, dlen.p, (size_t)lines * 8, hipMemcpyDeviceToHost));
-    PPOCR_HIP(hipMemcpy(score, dsc.p, (size_t)lines * 4, hipMemcpyDeviceToHost));
-    if (steps) PPOCR_HIP(hipMemcpy(seq, dseq.p, (size_t)steps * 4, hipMemcpyDeviceToHost));
-    return PPOCR_OK;
+    return hc.copy_out({seq, seq_len, score});
 }
 
 int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off, int64_t lines,
@@ -796,29 +940,17 @@ int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off
     if (m > 0 && (!a || !seq)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
     DeviceGuard dg(h->device);
     const size_t wsb = m > 0 ? ws_layout(m, nsplit_for(h, m, cfg)).total : 0;
-    DevBuf da, di, dp, dws, doff, dseq, dlen, dsc;
-    if (int e = da.alloc((size_t)(m * h->k) * 4)) return e;
-    if (int e = di.alloc((size_t)m * 4)) return e;
-    if (int e = dp.alloc((size_t)m * 4)) return e;
-    if (int e = dws.alloc(wsb)) return e;
-    if (int e = doff.alloc((size_t)(lines + 1) * 8)) return e;
-    if (int e = dseq.alloc((size_t)m * 4)) return e;
-    if (int e = dlen.alloc((size_t)lines * 8)) return e;
-    if (int e = dsc.alloc((size_t)lines * 4)) return e;
-    if (m > 0) PPOCR_HIP(hipMemcpy(da.p, a, (size_t)(m * h->k) * 4, hipMemcpyHostToDevice));
-    PPOCR_HIP(hipMemcpy(doff.p, line_off, (size_t)(lines + 1) * 8, hipMemcpyHostToDevice));
-    if (int e = ppocr_rh_decode_dev(h, da.as<float>(), m, doff.as<int64_t>(), lines, mode, di.as<int32_t>(),
-                                    dp.as<float>(), dseq.as<int32_t>(), dlen.as<int64_t>(), dsc.as<float>(), dws.p,
-                                    wsb, nullptr))
+    const size_t ab = (size_t)(m * h->k) * 4, rb = (size_t)m * 4, ob = (size_t)(lines + 1) * 8;
+    HostCall hc;
+    if (int e = hc.begin({ab, ob}, {rb, (size_t)lines * 8, (size_t)lines * 4, idx ? rb : 0, maxprob ? rb : 0}, wsb))
         return e;
-    PPOCR_HIP(hipMemcpy(seq_len, dlen.p, (size_t)lines * 8, hipMemcpyDeviceToHost));
-    PPOCR_HIP(hipMemcpy(score, dsc.p, (size_t)lines * 4, hipMemcpyDeviceToHost));
-    if (m > 0) {
-        PPOCR_HIP(hipMemcpy(seq, dseq.p, (size_t)m * 4, hipMemcpyDeviceToHost));
-        if (idx) PPOCR_HIP(hipMemcpy(idx, di.p, (size_t)m * 4, hipMemcpyDeviceToHost));
-        if (maxprob) PPOCR_HIP(hipMemcpy(maxprob, dp.p, (size_t)m * 4, hipMemcpyDeviceToHost));
-    }
-    return PPOCR_OK;
+    if (int e = hc.copy_in({a, line_off})) return e;
+    if (int e = ppocr_rh_decode_dev(h, hc.in<float>(0), m, hc.in<int64_t>(1), lines, mode,
+                                    idx ? hc.out<int32_t>(3) : nullptr, maxprob ? hc.out<float>(4) : nullptr,
+                                    hc.out<int32_t>(0), hc.out<int64_t>(1), hc.out<float>(2), hc.ws(), hc.ws_bytes(),
+                                    hc.stream()))
+        return e;
+    return hc.copy_out({seq, seq_len, score, idx, maxprob});
 }
 
 }  // extern "C"
