@@ -530,3 +530,41 @@ def test_guard_list_in_a_reused_workspace(orc, rh):
     gap = top2_gap(f64_logits_q(big[:64], q, s, bias))
     check_argmax(idx[:64], ref["idx"], gap, label="reused workspace, stress head")
     h.close()
+
+
+def test_host_calls_from_many_threads(rh, rhead):
+    """The handle is shared by threads (the reference's rec_pool workers): 8 threads
+    decoding different line batches at once through the host-pointer entry point (each
+    call takes its own device arena) get exactly the results of serial calls."""
+    import threading
+    from ppocr_rechead import workloads as wl
+    rng = np.random.default_rng(23)
+    jobs = []
+    for t in range(8):
+        lens = rng.integers(1, 130, size=int(rng.integers(1, 12)))
+        off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        jobs.append((rng.standard_normal((int(off[-1]), 120)).astype(np.float32), off))
+    print("host calls from 8 threads", flush=True)
+    serial = [rhead.decode(a, off) for a, off in jobs]
+    got = [None] * len(jobs)
+    errors = []
+
+    def work(t):
+        try:
+            for _ in range(5):
+                got[t] = rhead.decode(*jobs[t])
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(len(jobs))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for s, g in zip(serial, got):
+        assert np.array_equal(s["idx"], g["idx"])
+        assert np.array_equal(s["maxprob"].view(np.uint32), g["maxprob"].view(np.uint32))
+        assert np.array_equal(s["score"].view(np.uint32), g["score"].view(np.uint32))
+        for a, b in zip(s["seqs"], g["seqs"]):
+            assert np.array_equal(a, b)
