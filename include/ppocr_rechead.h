@@ -12,7 +12,8 @@
  *    "<op>: <msg>" in the form of OcrError::OperatorError { op, msg } (src/error.rs:4-27).
  *    Nothing aborts or panics across this boundary.
  *  - Host-pointer entry points copy inputs to the device, run, copy results back and
- *    synchronise.  `_dev` entry points take device pointers and a HIP stream
+ *    synchronise, on device memory and a stream of their own taken from a process-wide
+ *    pool (one per concurrent call, kept for the next call).  `_dev` entry points take device pointers and a HIP stream
  *    (hipStream_t passed as void*, NULL = the null stream), enqueue only, and never
  *    synchronise.
  *  - Matrices are row-major and contiguous.  m is the number of activation rows (B*T),
