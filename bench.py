@@ -292,6 +292,21 @@ def main():
                  "hbm_frac": round(pbytes / (ms_p / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
         dprobs.free()
 
+    host = None
+    if args.only == "":
+        # the same step from host arrays to host results (ppocr_rh_decode: PCIe both ways);
+        # reported beside the device rate, never as `value`
+        off = wk["line_off"]
+        for _ in range(2):
+            head.decode(a, off, mode)
+        reps = max(3, args.steps // 2)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            head.decode(a, off, mode)
+        host_ms = (time.perf_counter() - t0) / reps * 1e3
+        host = {"ms_per_step": round(host_ms, 4), "rows_per_s": round(m / (host_ms / 1e3), 1),
+                "entry": "ppocr_rh_decode (host activations in, host sequences out)"}
+
     copy = copy_probe(args.copy_probe) if args.copy_probe > 0 else None
     peaks = measured_peaks() if args.only == "" else None
 
@@ -334,6 +349,7 @@ def main():
                          "algorithmic_flops_per_launch": flops, "kernel_ms": round(ms_head, 5)},
             "measured_peaks": peaks,
             "wall_ms_per_step": round(wall_ms, 5),
+            "host_arrays": host,
             "unfused": unf,
             "probs_fused": probs,
             "cpu_baseline": cpu,
