@@ -31,8 +31,8 @@ FP32_PEAK_TFLOPS = 157.3
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="dense_256")
     p.add_argument("--mode", type=int, default=2, help="0 fp32 FMA, 1/2/3 bf16 terms")
     p.add_argument("--no-cpu", action="store_true")
