@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "kernels.hpp"
+#include "model_graph.hpp"
 #include "safetensors.hpp"
 
 namespace ppocr {
@@ -690,6 +691,21 @@ int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, 
     PPOCR_HIP(hipDeviceSynchronize());
     h->device_bytes = total;
     *out = h.release();
+    return PPOCR_OK;
+}
+
+int ppocr_model_find_rec_head(const char* path, char* weight_name, size_t weight_cap, char* bias_name,
+                              size_t bias_cap, int64_t* n, int64_t* k) {
+    StFile f;
+    if (int e = f.open(path)) return e;
+    RecHeadNames r;
+    if (int e = find_rec_head(f, &r)) return e;
+    if (!weight_name || r.weight.size() + 1 > weight_cap || !bias_name || r.bias.size() + 1 > bias_cap)
+        return fail(PPOCR_ERR_INVALID_ARG, "Model: a tensor name does not fit its buffer");
+    std::memcpy(weight_name, r.weight.c_str(), r.weight.size() + 1);
+    std::memcpy(bias_name, r.bias.c_str(), r.bias.size() + 1);
+    if (n) *n = r.n;
+    if (k) *k = r.k;
     return PPOCR_OK;
 }
 

@@ -14,6 +14,7 @@
 #include <cstring>
 
 #include "../../include/ppocr_rechead.h"
+#include "json.hpp"
 
 namespace ppocr {
 
@@ -23,182 +24,6 @@ namespace {
 
 // Errors of the model file are PPOCR_ERR_MODEL, in the form of OcrError::SafeTensorsError.
 int st_fail(const std::string& msg) { return fail(PPOCR_ERR_MODEL, "SafeTensors: " + msg); }
-
-// Minimal JSON reader for the header: objects, arrays, strings (with escapes), integers,
-// true/false/null.  Values the header does not need (the metadata) are skipped.
-struct Json {
-    const char* p;
-    const char* end;
-    std::string err;
-
-    void ws() {
-        while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
-    }
-    bool expect(char c) {
-        ws();
-        if (p >= end || *p != c) {
-            err = std::string("expected '") + c + "'";
-            return false;
-        }
-        ++p;
-        return true;
-    }
-    bool peek(char c) {
-        ws();
-        return p < end && *p == c;
-    }
-    bool string(std::string* out) {
-        if (!expect('"')) return false;
-        std::string s;
-        while (p < end && *p != '"') {
-            char c = *p++;
-            if ((unsigned char)c < 0x20) {
-                err = "control character in string";
-                return false;
-            }
-            if (c == '\\') {
-                if (p >= end) break;
-                const char e = *p++;
-                switch (e) {
-                    case '"': s += '"'; break;
-                    case '\\': s += '\\'; break;
-                    case '/': s += '/'; break;
-                    case 'b': s += '\b'; break;
-                    case 'f': s += '\f'; break;
-                    case 'n': s += '\n'; break;
-                    case 'r': s += '\r'; break;
-                    case 't': s += '\t'; break;
-                    case 'u': {
-                        if (end - p < 4) {
-                            err = "truncated \\u escape";
-                            return false;
-                        }
-                        unsigned v = 0;
-                        for (int x = 0; x < 4; ++x) {
-                            const char h = *p++;
-                            v <<= 4;
-                            if (h >= '0' && h <= '9') v |= (unsigned)(h - '0');
-                            else if (h >= 'a' && h <= 'f') v |= (unsigned)(h - 'a' + 10);
-                            else if (h >= 'A' && h <= 'F') v |= (unsigned)(h - 'A' + 10);
-                            else {
-                                err = "bad \\u escape";
-                                return false;
-                            }
-                        }
-                        // names are compared byte for byte: keep BMP code points as UTF-8
-                        if (v < 0x80) {
-                            s += (char)v;
-                        } else if (v < 0x800) {
-                            s += (char)(0xC0 | (v >> 6));
-                            s += (char)(0x80 | (v & 0x3F));
-                        } else {
-                            s += (char)(0xE0 | (v >> 12));
-                            s += (char)(0x80 | ((v >> 6) & 0x3F));
-                            s += (char)(0x80 | (v & 0x3F));
-                        }
-                        break;
-                    }
-                    default: err = "bad escape"; return false;
-                }
-            } else {
-                s += c;
-            }
-        }
-        if (p >= end) {
-            err = "unterminated string";
-            return false;
-        }
-        ++p;  // closing quote
-        if (out) *out = std::move(s);
-        return true;
-    }
-    bool integer(int64_t* out) {
-        ws();
-        const char* q = p;
-        if (q < end && *q == '-') ++q;
-        if (q >= end || *q < '0' || *q > '9') {
-            err = "expected an integer";
-            return false;
-        }
-        bool neg = *p == '-';
-        if (neg) ++p;
-        uint64_t v = 0;
-        while (p < end && *p >= '0' && *p <= '9') {
-            const uint64_t d = (uint64_t)(*p - '0');
-            if (v > (UINT64_MAX - d) / 10) {
-                err = "integer overflow";
-                return false;
-            }
-            v = v * 10 + d;
-            ++p;
-        }
-        if (p < end && (*p == '.' || *p == 'e' || *p == 'E')) {
-            err = "expected an integer";
-            return false;
-        }
-        if (v > (uint64_t)INT64_MAX) {
-            err = "integer overflow";
-            return false;
-        }
-        *out = neg ? -(int64_t)v : (int64_t)v;
-        return true;
-    }
-    // Skips any value (depth-limited).
-    bool skip(int depth = 0) {
-        if (depth > 64) {
-            err = "nesting too deep";
-            return false;
-        }
-        ws();
-        if (p >= end) {
-            err = "unexpected end";
-            return false;
-        }
-        if (*p == '"') return string(nullptr);
-        if (*p == '{') {
-            ++p;
-            if (peek('}')) return ++p, true;
-            do {
-                if (!string(nullptr) || !expect(':') || !skip(depth + 1)) return false;
-            } while (peek(',') && ++p);
-            return expect('}');
-        }
-        if (*p == '[') {
-            ++p;
-            if (peek(']')) return ++p, true;
-            do {
-                if (!skip(depth + 1)) return false;
-            } while (peek(',') && ++p);
-            return expect(']');
-        }
-        for (const char* lit : {"true", "false", "null"}) {
-            const size_t l = std::strlen(lit);
-            if ((size_t)(end - p) >= l && std::memcmp(p, lit, l) == 0) {
-                p += l;
-                return true;
-            }
-        }
-        // a number (any form)
-        const char* q = p;
-        while (p < end && (std::strchr("+-.eE", *p) || (*p >= '0' && *p <= '9'))) ++p;
-        if (p == q) {
-            err = "unexpected character";
-            return false;
-        }
-        return true;
-    }
-    bool int_array(std::vector<int64_t>* out) {
-        if (!expect('[')) return false;
-        out->clear();
-        if (peek(']')) return ++p, true;
-        do {
-            int64_t v;
-            if (!integer(&v)) return false;
-            out->push_back(v);
-        } while (peek(',') && ++p);
-        return expect(']');
-    }
-};
 
 }  // namespace
 
@@ -250,7 +75,12 @@ int StFile::open(const char* path) {
             std::string key;
             if (!js.string(&key) || !js.expect(':')) return bad("");
             if (key == "__metadata__") {
-                if (!js.skip()) return bad("");
+                // a map of strings (the reference's bundles keep the model graph here)
+                JVal md;
+                if (!js.value(&md)) return bad("");
+                if (md.kind != JVal::kObj) return st_fail("invalid header: __metadata__ is not an object");
+                for (auto& kv : md.obj)
+                    if (kv.second.kind == JVal::kStr) metadata_.push_back({kv.first, std::move(kv.second.s)});
                 continue;
             }
             StTensor t;

@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace ppocr {
@@ -30,11 +31,18 @@ public:
     // Looks a tensor up by name; null when absent.
     const StTensor* find(const char* name) const;
     const std::vector<StTensor>& tensors() const { return tensors_; }
+    // A "__metadata__" entry by key; null when absent.
+    const std::string* metadata(const char* key) const {
+        for (const auto& kv : metadata_)
+            if (kv.first == key) return &kv.second;
+        return nullptr;
+    }
 
 private:
     void* map_ = nullptr;
     size_t size_ = 0;
     std::vector<StTensor> tensors_;
+    std::vector<std::pair<std::string, std::string>> metadata_;
 };
 
 // Bytes per element of a safetensors dtype (0 for an unknown one).

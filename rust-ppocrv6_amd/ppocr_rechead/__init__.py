@@ -23,7 +23,7 @@ from ._lib import (MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_FP32_FMA, PPOCR_E
                    PPOCR_ERR_INVALID_ARG, PPOCR_ERR_MODEL, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
 
 __all__ = [
-    "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "matmul_quantized_b", "matmul_transposed_b",
+    "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "find_rec_head", "matmul_quantized_b", "matmul_transposed_b",
     "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3",
 ]
 
@@ -124,6 +124,13 @@ class RecHead:
         self.default_mode = MODE_BF16X2 if self.quantized else MODE_BF16X3
         return self
 
+    @classmethod
+    def from_model(cls, path, quantize=True, device=0):
+        """The head of a model file, found in its graph (find_rec_head) and built on the
+        GPU from the file's tensors (from_safetensors)."""
+        names = find_rec_head(path)
+        return cls.from_safetensors(path, names["weight"], names["bias"], quantize=quantize, device=device)
+
     def close(self):
         if self._h:
             _lib.lib().ppocr_rh_destroy(self._h)
@@ -208,6 +215,18 @@ class RecHead:
                                               _ptr(seq), _ptr(seq_len), _ptr(score)))
         seqs = [seq[line_off[b]:line_off[b] + seq_len[b]].copy() for b in range(lines)]
         return {"idx": idx[:m], "maxprob": mp[:m], "seqs": seqs, "score": score[:lines]}
+
+
+def find_rec_head(path):
+    """The recognition head of a model file: the MatMul -> [Add bias] -> Softmax(axis=-1) ->
+    graph output segment of its graph, as {"weight", "bias" (None if absent), "n", "k"}
+    (the segment the engine-level fused hook replaces)."""
+    wb, bb = ctypes.create_string_buffer(1024), ctypes.create_string_buffer(1024)
+    n, k = ctypes.c_int64(), ctypes.c_int64()
+    _check(_lib.lib().ppocr_model_find_rec_head(os.fsencode(path), wb, 1024, bb, 1024, ctypes.byref(n),
+                                                ctypes.byref(k)))
+    bias = os.fsdecode(bb.value)
+    return {"weight": os.fsdecode(wb.value), "bias": bias or None, "n": n.value, "k": k.value}
 
 
 def matmul_quantized_b(a, qw, bias=None, mode=MODE_BF16X2):

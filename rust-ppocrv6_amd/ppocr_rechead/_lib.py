@@ -36,6 +36,8 @@ SIGNATURES = {
     "ppocr_rh_create_f32": (_int, [_vp, _vp, _i64, _i64, _int, ctypes.POINTER(_vp)]),
     "ppocr_rh_create_from_safetensors": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _int, _int,
                                                 ctypes.POINTER(_vp)]),
+    "ppocr_model_find_rec_head": (_int, [ctypes.c_char_p, ctypes.c_char_p, _sz, ctypes.c_char_p, _sz,
+                                         ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "ppocr_rh_destroy": (None, [_vp]),
     "ppocr_rh_footprint_bytes": (_sz, [_vp]),
     "ppocr_rh_device_bytes": (_sz, [_vp]),

@@ -83,3 +83,35 @@ def test_fp32_head_from_file_equals_host_transposed(rh, tmp_path, k, n):
         _same(p1, p2)
     hf.close()
     hh.close()
+
+
+def test_head_found_in_the_model_graph(orc, rh, tmp_path):
+    """RecHead.from_model finds MatMul.12 -> Add -> Softmax.2 in the file's graph and builds
+    the same head as naming its tensors; the whole-head decode agrees with the oracle."""
+    import json
+    from safetensors.numpy import save_file
+    from gpu_common import check_argmax, f64_logits_q, top2_gap
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    graph = {"inputs": ["x"], "outputs": ["probs"], "nodes": [
+        {"name": "MatMul.12", "op": "MatMul", "inputs": ["x", "linear_8.w_0"], "outputs": ["mm"]},
+        {"name": "Add.9", "op": "Add", "inputs": ["mm", "linear_8.b_0"], "outputs": ["logits"]},
+        {"name": "Softmax.2", "op": "Softmax", "inputs": ["logits"], "outputs": ["probs"], "attrs": {"axis": -1}}]}
+    path = str(tmp_path / "rec.safetensors")
+    save_file({"linear_8.w_0": np.ascontiguousarray(w_t.T), "linear_8.b_0": bias}, path,
+              metadata={"graph": json.dumps(graph)})
+    print("head from the model graph", flush=True)
+    hm = rh.RecHead.from_model(path)
+    hs = rh.RecHead.from_safetensors(path, "linear_8.w_0", "linear_8.b_0")
+    a = wl.activations("a4_page")
+    off = wl.line_offsets(wl.lines_for("a4_page"))
+    gm, gs = hm.decode(a, off), hs.decode(a, off)
+    _same(gm["idx"], gs["idx"])
+    _same(gm["maxprob"], gs["maxprob"])
+    _same(gm["score"], gs["score"])
+    q, s = orc.pack_int8(w_t)
+    ref = orc.rechead_lines(a, off, q, s, bias)
+    check_argmax(gm["idx"], ref["idx"], top2_gap(f64_logits_q(a, q, s, bias)), label="model graph head")
+    assert np.abs(gm["maxprob"] - ref["maxprob"]).max() < 1e-4
+    hm.close()
+    hs.close()

@@ -112,3 +112,98 @@ def test_header_padding_and_metadata_are_accepted(rh, tmp_path):
     _raw_file(path, json.dumps(hdr).encode() + b"     ", np.zeros(6, np.float32).tobytes())
     rc, msg = _create(rh, path, w="wé", b=None)
     assert not msg.startswith(("SafeTensors", "Model")), msg
+
+
+# ---------------------------------------------------------------- the head in the graph
+def _graph_file(tmp_path, nodes, outputs=("probs",), inputs=("x",), name="g.safetensors", graph=None, n=70, k=120,
+                with_bias=True):
+    from safetensors.numpy import save_file
+    t = {"linear_8.w_0": np.zeros((k, n), np.float32), "other.w": np.zeros((4, 4), np.float32)}
+    if with_bias:
+        t["linear_8.b_0"] = np.zeros(n, np.float32)
+    g = graph if graph is not None else json.dumps({"inputs": list(inputs), "outputs": list(outputs), "nodes": nodes})
+    path = str(tmp_path / name)
+    save_file(t, path, metadata={"graph": g})
+    return path
+
+
+def _node(name, op, inputs, outputs, attrs=None):
+    d = {"name": name, "op": op, "inputs": inputs, "outputs": outputs}
+    if attrs is not None:
+        d["attrs"] = attrs
+    return d
+
+
+NECK = [_node("MatMul.11", "MatMul", ["h", "other.w"], ["x2"])]
+HEAD = [_node("MatMul.12", "MatMul", ["x2", "linear_8.w_0"], ["mm"]),
+        _node("Add.9", "Add", ["mm", "linear_8.b_0"], ["logits"]),
+        _node("Softmax.2", "Softmax", ["logits"], ["probs"], {"axis": -1})]
+
+
+def test_find_head_in_the_graph(rh, tmp_path):
+    """The MatMul.12 -> Add -> Softmax.2 -> output tail of the recognition model."""
+    r = rh.find_rec_head(_graph_file(tmp_path, NECK + HEAD))
+    assert r == {"weight": "linear_8.w_0", "bias": "linear_8.b_0", "n": 70, "k": 120}
+
+
+@pytest.mark.parametrize("variant", ["bias_first", "no_bias", "identities", "no_axis", "tiny"])
+def test_find_head_variants(rh, tmp_path, variant):
+    nodes = [dict(n) for n in NECK + HEAD]
+    n, k, with_bias = 70, 120, True
+    outputs = ("probs",)
+    if variant == "bias_first":
+        nodes[2]["inputs"] = ["linear_8.b_0", "mm"]
+    elif variant == "no_bias":
+        nodes = NECK + [_node("MatMul.12", "MatMul", ["x2", "linear_8.w_0"], ["logits"]),
+                        _node("Softmax.2", "Softmax", ["logits"], ["probs"])]
+        with_bias = False
+    elif variant == "identities":
+        nodes = NECK + [HEAD[0], HEAD[1], _node("Identity.1", "Identity", ["logits"], ["logits2"]),
+                        _node("Softmax.2", "Softmax", ["logits2"], ["p"], {"axis": -1}),
+                        _node("Identity.2", "Identity", ["p"], ["probs"])]
+    elif variant == "no_axis":
+        del nodes[3]["attrs"]
+    elif variant == "tiny":
+        n, k = 6906, 80
+    r = rh.find_rec_head(_graph_file(tmp_path, nodes, outputs, n=n, k=k, with_bias=with_bias))
+    assert r == {"weight": "linear_8.w_0", "bias": None if variant == "no_bias" else "linear_8.b_0", "n": n, "k": k}
+
+
+@pytest.mark.parametrize("variant,msg", [
+    ("axis_1", "no MatMul"), ("not_output", "no MatMul"), ("logits_used_twice", "no MatMul"),
+    ("weight_missing", "no MatMul"), ("no_graph", "missing 'graph'"), ("bad_json", "failed to parse graph JSON"),
+    ("empty_outputs", "both must be non-empty"), ("no_outputs", "declares no outputs")])
+def test_find_head_rejects(rh, tmp_path, variant, msg):
+    nodes = [dict(n) for n in NECK + HEAD]
+    outputs, graph = ("probs",), None
+    if variant == "axis_1":
+        nodes[3]["attrs"] = {"axis": 1}
+    elif variant == "not_output":
+        nodes.append(_node("Mul.1", "Mul", ["probs", "probs"], ["y"]))
+        outputs = ("y",)
+    elif variant == "logits_used_twice":
+        outputs = ("probs", "mm")
+    elif variant == "weight_missing":
+        nodes[1]["inputs"] = ["x2", "linear_9.w_0"]
+    elif variant == "bad_json":
+        graph = '{"inputs": ["x"], "outputs": ["probs"], "nodes": [}'
+    elif variant == "empty_outputs":
+        nodes[0]["outputs"] = []
+    elif variant == "no_outputs":
+        outputs = ()
+    if variant == "no_graph":
+        from safetensors.numpy import save_file
+        path = str(tmp_path / "nograph.safetensors")
+        save_file({"linear_8.w_0": np.zeros((120, 70), np.float32)}, path)
+    else:
+        path = _graph_file(tmp_path, nodes, outputs, graph=graph)
+    with pytest.raises(rh.OcrError) as ei:
+        rh.find_rec_head(path)
+    assert ei.value.code == rh.PPOCR_ERR_MODEL and msg in str(ei.value), str(ei.value)
+
+
+def test_find_head_name_buffer_too_small(rh, tmp_path):
+    path = _graph_file(tmp_path, NECK + HEAD)
+    w, b = ctypes.create_string_buffer(5), ctypes.create_string_buffer(64)
+    rc = rh._lib.lib().ppocr_model_find_rec_head(os.fsencode(path), w, 5, b, 64, None, None)
+    assert rc == rh.PPOCR_ERR_INVALID_ARG and "does not fit" in rh._lib.last_error()
