@@ -738,26 +738,30 @@ __global__ void guard_reset_kernel(unsigned long long* guard_header, unsigned ep
 }
 
 // ============================================================ launchers
+// 32-row blocks per wave of the main statistics pass: two for the one- and two-term
+// modes (each weight fragment read from LDS serves both), one for three terms (registers).
 template <int C>
 static constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1) ? 2 : 1;
 }
+// Small batches of the two-term mode run one block per wave instead: the workgroup's rows
+// (128) are then mostly real rows, and its per-tile work halves (measured on the MI355X:
+// one 120-row line 0.033 -> 0.027 ms, a 2245-row page 0.051 -> 0.050 ms; 30720 rows
+// 0.259 -> 0.295 ms, so large batches keep two blocks).
+constexpr int64_t kSmallBatchRows = 8192;
+static int main_blocks(int cfg, int64_t m) {
+    if (cfg == CFG_Q2) return m <= kSmallBatchRows ? 1 : 2;
+    return (cfg == CFG_Q1 || cfg == CFG_F1) ? 2 : 1;
+}
 // LDS of the main statistics pass: the tile ring and each wave's saved best tile.
-template <int C, int G>
+template <int C, int G, int MB>
 static constexpr int main_lds_bytes() {
-    return kRing * Geo<C, G>::BUF + kStatsWaves * mb_of<C>() * 16 * 64 * 4;
+    return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
 }
 
-// Rows per workgroup of the main statistics pass and of the rescue pass (4 waves).
-int stats_rows_per_block_mfma(int cfg) {
-    switch (cfg) {
-        case CFG_Q1: return 32 * kStatsWaves * mb_of<CFG_Q1>();
-        case CFG_Q2: return 32 * kStatsWaves * mb_of<CFG_Q2>();
-        case CFG_Q3: return 32 * kStatsWaves * mb_of<CFG_Q3>();
-        case CFG_F1: return 32 * kStatsWaves * mb_of<CFG_F1>();
-        default: return 32 * kStatsWaves * mb_of<CFG_F3>();
-    }
-}
+// Rows per workgroup of the main statistics pass for a batch of m rows, and of the rescue
+// pass (4 waves).
+int stats_rows_per_block_mfma(int cfg, int64_t m) { return 32 * kStatsWaves * main_blocks(cfg, m); }
 
 // Vocabulary chunks per row block.  The grid runs in rounds of kStatsSlots workgroups
 // (2 per CU on the 256 CUs of an MI355X), and a workgroup costs a fixed start and finish
@@ -892,7 +896,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     if (nsplit != 1 && nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16 && nsplit != 32 && nsplit != 64)
         return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be a power of two <= 64");
     if (m <= 0) return PPOCR_OK;
-    const int rpb = stats_rows_per_block_mfma(cfg);
+    const int rpb = stats_rows_per_block_mfma(cfg, m);
     const int64_t mblocks = (m + rpb - 1) / rpb;
     if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
     const int tpc = (tg.tiles + nsplit - 1) / nsplit;
@@ -906,11 +910,18 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     const bool noref = guarded && guard->stats_noref;
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-        auto kern = stats_main_kernel<C, G, mb_of<C>(), false, false>;
+        constexpr int MB = mb_of<C>();
+        auto kern = stats_main_kernel<C, G, MB, false, false>;
+        int lds = main_lds_bytes<C, G, MB>();
         if constexpr (C == CFG_Q2) {
-            if (noref) kern = stats_main_kernel<C, G, mb_of<C>(), false, true>;
+            if (rpb == 32 * kStatsWaves) {  // small batch: one block per wave
+                kern = noref ? stats_main_kernel<C, G, 1, false, true> : stats_main_kernel<C, G, 1, false, false>;
+                lds = main_lds_bytes<C, G, 1>();
+            } else if (noref) {
+                kern = stats_main_kernel<C, G, MB, false, true>;
+            }
         }
-        kern<<<grid, 64 * kStatsWaves, main_lds_bytes<C, G>(), st>>>(
+        kern<<<grid, 64 * kStatsWaves, lds, st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
             guarded ? (noref ? guard->stats_amax_limit : guard->amax_limit) : 0.0f,
             guarded ? guard->header : nullptr, guarded ? guard->rows : nullptr, guarded ? guard->epoch : 0u,
@@ -922,12 +933,12 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     if (guarded) {
         // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
         // (with exact class indices)
-        const int rrpb = stats_rows_per_block_mfma(rcfg);
+        const int rrpb = stats_rows_per_block_mfma(rcfg, m);
         const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, kRescueSlots);
         const int rgrid = grid_blocks(slots, nsplit);
         e = dispatch_cfg_g(rcfg, tg.G, [&](auto CC, auto GG) -> int {
             constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
-            stats_main_kernel<C, G, mb_of<C>(), true, false><<<rgrid, 64 * kStatsWaves, main_lds_bytes<C, G>(), st>>>(
+            stats_main_kernel<C, G, mb_of<C>(), true, false><<<rgrid, 64 * kStatsWaves, main_lds_bytes<C, G, mb_of<C>()>(), st>>>(
                 a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, slots, p_best, p_sum, p_idx, 0.0f, guard->header,
                 guard->rows, guard->epoch, guard->capacity);
             PPOCR_HIP(hipGetLastError());

@@ -66,7 +66,7 @@ int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const fl
                        int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.
 int stats_nsplit(int64_t m, int rows_per_block, int tiles);
-int stats_rows_per_block_mfma(int cfg);
+int stats_rows_per_block_mfma(int cfg, int64_t m);
 // Main pass, rescue of the guarded rows, then one wave per row merges the partials and
 // resolves the argmax: idx, maxprob (1/sum) and, when non-null, row_max (log2-domain
 // maximum) and row_inv (1/sum) for a probs pass.
