@@ -238,10 +238,21 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
     if (row_inv) row_inv[row] = inv;
 }
 
+// sum + x(lane 0) + x(lane 1) + ... + x(lane 63), added in lane order in f32 (the same
+// value in every lane).  A lane that contributes nothing passes -0.0, which is the exact
+// identity of IEEE addition (x + -0.0 = x for every x, -0.0 included), so the result is
+// bit for bit the sequential sum over the contributing lanes alone.
+__device__ __forceinline__ float ordered_lane_sum(float sum, float x) {
+    const int xi = __float_as_int(x);
+#pragma unroll
+    for (int l = 0; l < 64; ++l) sum += __int_as_float(__builtin_amdgcn_readlane(xi, l));
+    return sum;
+}
+
 // One wavefront per text line.  Steps are taken 64 at a time; the emit mask is a ballot,
 // emitted indices are compacted by prefix popcount, and the score is summed in step order
 // (every lane runs the same sequential sum over the emitting lanes' values, read lane by
-// lane).
+// lane, ordered_lane_sum).
 __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restrict__ idx,
                                                          const float* __restrict__ val,
                                                          const int64_t* __restrict__ line_off, int64_t lines,
@@ -263,12 +274,7 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
         const uint64_t mask = __ballot(emit);
         const int pos = __popcll(mask & ((1ull << lane) - 1ull));
         if (emit) seq[t0 + cnt + pos] = id;
-        uint64_t mm = mask;
-        while (mm) {
-            const int src = __builtin_ctzll(mm);  // wave-uniform
-            mm &= mm - 1;
-            sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
-        }
+        sum = ordered_lane_sum(sum, emit ? v : -0.0f);
         cnt += __popcll(mask);
     }
     if (lane == 0) {
@@ -328,12 +334,7 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
                 const uint64_t mask = __ballot(emit);
                 const int pos = __popcll(mask & ((1ull << lane) - 1ull));
                 if (emit) seq[t0 + cnt + pos] = cid;
-                uint64_t mm = mask;
-                while (mm) {
-                    const int src = __builtin_ctzll(mm);  // wave-uniform
-                    mm &= mm - 1;
-                    sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), src));
-                }
+                sum = ordered_lane_sum(sum, emit ? cv : -0.0f);
                 cnt += __popcll(mask);
             }
             carry = s_id[rem - 1];
