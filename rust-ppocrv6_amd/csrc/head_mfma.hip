@@ -845,6 +845,12 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     const int vec = vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
     const bool guarded = guard && guard->header && rcfg >= 0;
+    // Probabilities are exp2(t - row_max) * row_inv with row_max and row_inv from the
+    // statistics pass, so this pass must compute every t exactly as that pass did: the
+    // same rows take three activation terms (that pass's limit, the lower one when it skips
+    // the reference shift).  Logits need only the precision limit.
+    const float limit = !guarded ? 0.0f
+                        : (epi == 1 && guard->stats_noref) ? guard->stats_amax_limit : guard->amax_limit;
     if (guarded) {
         // a replay of this call (same epoch) must start from an empty list too
         guard_reset_kernel<<<1, 1, 0, st>>>(guard->header, guard->epoch);
@@ -855,7 +861,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
         constexpr int LDS = writer_ring<Geo<C, G>::REC>() * Geo<C, G>::BUF;
         auto kern = epi == 0 ? rows_w_kernel<C, G, 0, false> : rows_w_kernel<C, G, 1, false>;
         kern<<<(unsigned)grid, 64 * (kWriterWaves + 1), LDS, st>>>(a, m, (int)k, vec, rec, tg.tiles, (int)n, nsplit, tpc, (int)mblocks,
-                                              row_max, row_inv, out, guarded ? guard->amax_limit : 0.0f,
+                                              row_max, row_inv, out, guarded ? limit : 0.0f,
                                               guarded ? guard->header : nullptr, guarded ? guard->rows : nullptr,
                                               guarded ? guard->epoch : 0u, guarded ? guard->capacity : 0);
         PPOCR_HIP(hipGetLastError());

@@ -568,3 +568,24 @@ def test_host_calls_from_many_threads(rh, rhead):
         assert np.array_equal(s["score"].view(np.uint32), g["score"].view(np.uint32))
         for a, b in zip(s["seqs"], g["seqs"]):
             assert np.array_equal(a, b)
+
+
+def test_probs_consistent_with_the_statistics_pass(orc, rh):
+    """The probabilities pass recomputes every logit; it must take the same activation
+    terms as the statistics pass for each row (rows between the range limit and the
+    precision limit get three terms in both), or a row's own maximum stops mapping to
+    exp2(0).  With a single class every probability is 1 (within f32 rounding of 1/sum)."""
+    rng = np.random.default_rng(29)
+    w = (rng.standard_normal((1, 120)) * 0.05).astype(np.float32)
+    q, s = orc.pack_int8(w)
+    bias = np.array([0.003], np.float32)
+    factors = np.repeat(np.array([1, 4, 12, 24, 30, 48, 90], np.float32), 8)
+    a = rng.standard_normal((factors.size, 120)).astype(np.float32) * factors[:, None]
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    print("probs of a one-class head", flush=True)
+    for mode in (2, 3):
+        p = head.probs(a, mode)
+        err = np.abs(p - 1.0).max()
+        print(f"  mode {mode}: max|p - 1| = {err:.2e}")
+        assert err < 1e-6, (mode, err)
+    head.close()

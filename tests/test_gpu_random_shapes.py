@@ -92,3 +92,49 @@ def test_unaligned_activation_pointer(orc, rh):
     for x, y in zip(*outs):
         assert np.array_equal(x, y)
     head.close()
+
+
+@pytest.mark.parametrize("seed,k,n,lens,mode", [c for c in CASES if c[2] <= 6906])
+def test_logits_and_probs_random_shapes(orc, rh, seed, k, n, lens, mode):
+    """The same sweep through the unfused projection (logits) and the fused probabilities,
+    against the oracle's matmul_quantized_b and softmax, max-abs 1e-4."""
+    rng = np.random.default_rng(seed + 100)
+    q, s, bias = _head(orc, rng, n, k)
+    m = max(1, min(int(sum(lens)), 300))
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[rng.choice(m, max(1, m // 20), replace=False)] *= np.float32(30.0)
+    print(f"logits/probs seed={seed} k={k} n={n} m={m} mode={mode}", flush=True)
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    logits = head.logits(a, mode)
+    probs = head.probs(a, mode)
+    head.close()
+    ref = orc.matmul_quantized_b(a, q, s, bias)
+    tol = 1e-4 + 1e-5 * np.abs(ref)  # f32 rounding of the x30 rows' large logits
+    assert np.all(np.abs(logits - ref) <= tol)
+    assert np.abs(probs - orc.softmax_rows(ref)).max() < TOL
+
+
+@pytest.mark.parametrize("k,n,mode", [(120, 500, 0), (120, 500, 3), (80, 6906, 3), (77, 33, 0), (119, 2049, 3)])
+def test_fp32_head_random_shapes(orc, rh, k, n, mode):
+    """FP32 heads (W^T in fp32, matmul_transposed_b): logits, probabilities and the whole
+    head against the oracle, for the fp32 FMA and the three-term MFMA modes."""
+    rng = np.random.default_rng(k * 31 + n)
+    w_t = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.01).astype(np.float32)
+    lens = [37, 120, 5]
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    a = rng.standard_normal((int(off[-1]), k)).astype(np.float32)
+    print(f"fp32 head k={k} n={n} mode={mode}", flush=True)
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    logits = head.logits(a, mode)
+    probs = head.probs(a, mode)
+    got = head.decode(a, off, mode)
+    head.close()
+    ref = orc.matmul_transposed_b(a, w_t, bias)
+    assert np.abs(logits - ref).max() < TOL
+    refp = orc.softmax_rows(ref)
+    assert np.abs(probs - refp).max() < TOL
+    ref64 = a.astype(np.float64) @ w_t.astype(np.float64).T + bias
+    gap = top2_gap(ref64)
+    check_argmax(got["idx"], np.argmax(ref64, axis=1).astype(np.int32), gap, label=f"fp32 head k={k}")
+    assert np.abs(got["maxprob"] - refp.max(axis=1)).max() < TOL
