@@ -120,3 +120,34 @@ def test_decode_dev_argument_errors_do_not_need_a_device(rh):
     assert L.ppocr_rh_decode_dev(None, *args) == rh.PPOCR_ERR_INVALID_ARG
     assert rh._lib.last_error() == "RecHeadHip: null head handle"
     assert L.ppocr_rh_decode(None, None, None, 1, 2, None, None, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """With the HIP library absent, every compute entry of the mirror raises; nothing falls
+    back to a CPU path."""
+    import subprocess
+    import sys
+    code = r"""
+import numpy as np
+import ppocr_rechead as rh
+calls = {
+    "softmax_inplace": lambda: rh.softmax_inplace(np.zeros((1, 4), np.float32)),
+    "pack": lambda: rh.QuantizedWeight.from_f32_transposed(np.ones((3, 4), np.float32)),
+    "matmul_quantized_b": lambda: rh.matmul_quantized_b(
+        np.ones((1, 4), np.float32), rh.QuantizedWeight(np.ones((3, 4), np.int8), np.ones(3, np.float32))),
+    "collapse": lambda: rh.CtcDecoder.collapse(np.zeros(2, np.int32), np.zeros(2, np.float32),
+                                               np.array([0, 2], np.int64)),
+}
+for name, f in calls.items():
+    try:
+        f()
+        print(name, "RETURNED")
+    except RuntimeError as e:
+        print(name, "RAISED", "not found" in str(e))
+"""
+    env = dict(os.environ, PPOCR_RECHEAD_LIB=str(tmp_path / "absent" / "libppocr_rechead.so"),
+               PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "rust-ppocrv6_amd"), ROOT]))
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    lines = dict(l.split(" ", 1) for l in out.stdout.strip().splitlines())
+    assert lines == {k: "RAISED True" for k in ("softmax_inplace", "pack", "matmul_quantized_b", "collapse")}, out.stdout
