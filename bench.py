@@ -72,10 +72,33 @@ def traffic_from_profiles(kernel_key):
         return None
 
 
-def cpu_baseline(wk, q, s, seconds):
+def agreement(wk, q, s, ref, gpu):
+    """The GPU step's results against the oracle's on the same batch, in the survey's
+    terms: argmax mismatches (each with its top-2 logit gap, from f64 logits of the
+    dequantized weight), the largest maxprob difference, and per line whether the CTC
+    sequences are identical, plus the largest score difference."""
+    mis = np.nonzero(ref["idx"] != gpu["idx"])[0]
+    gaps = []
+    if mis.size:
+        w = q.astype(np.float64) * s.astype(np.float64)[:, None]
+        lg = wk["a"][mis].astype(np.float64) @ w.T + wk["bias"].astype(np.float64)
+        top2 = np.sort(lg, axis=1)[:, -2:]
+        gaps = (top2[:, 1] - top2[:, 0]).tolist()
+    off = wk["line_off"]
+    same = sum(1 for b, r in enumerate(ref["seqs"])
+               if np.array_equal(r, gpu["seq"][off[b]:off[b] + gpu["seq_len"][b]]))
+    return {"rows": int(ref["idx"].size), "argmax_mismatches": int(mis.size),
+            "max_top2_gap_of_mismatches": max(gaps) if gaps else None,
+            "maxprob_max_abs_diff": float(np.abs(ref["maxprob"] - gpu["maxprob"]).max()),
+            "lines": len(ref["seqs"]), "ctc_sequences_identical": same,
+            "score_max_abs_diff": float(np.abs(ref["score"] - gpu["score"]).max())}
+
+
+def cpu_baseline(wk, q, s, seconds, gpu=None):
     """The oracle's line-parallel head (one line per worker, inner serial, as
     src/pipeline.rs:417-433): whole passes over the same batch, repeated to about
-    `seconds` of CPU work (one calibration pass first)."""
+    `seconds` of CPU work (one calibration pass first, whose results are also compared
+    with the GPU step's when `gpu` holds them)."""
     from oracle import oracle as orc
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     off = wk["line_off"]
@@ -83,17 +106,20 @@ def cpu_baseline(wk, q, s, seconds):
     lines = len(off) - 1
     rows = int(off[-1])
     t0 = time.perf_counter()
-    orc.rechead_lines(a, off, q, s, wk["bias"], exec_threads=threads)
+    ref = orc.rechead_lines(a, off, q, s, wk["bias"], exec_threads=threads)
     t_pass = time.perf_counter() - t0
     passes = max(1, int(round(seconds / max(t_pass, 1e-6))))
     t0 = time.perf_counter()
     for _ in range(passes):
         orc.rechead_lines(a, off, q, s, wk["bias"], exec_threads=threads)
     dt = time.perf_counter() - t0
-    return {"value": round(passes * rows / dt, 1), "unit": "rows/s", "cores": threads, "kind": "port",
-            "sample": f"{passes} passes over the batch ({lines} lines x T=120 = {rows} rows each, "
-                      f"{passes * rows} rows), INT8 AVX2 path of the reference restated in C, one line per "
-                      f"OpenMP thread, {dt:.1f} s"}
+    out = {"value": round(passes * rows / dt, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+           "sample": f"{passes} passes over the batch ({lines} lines x T=120 = {rows} rows each, "
+                     f"{passes * rows} rows), INT8 AVX2 path of the reference restated in C, one line per "
+                     f"OpenMP thread, {dt:.1f} s"}
+    if gpu is not None:
+        out["agreement_with_gpu_step"] = agreement(wk, q, s, ref, gpu)
+    return out
 
 
 def copy_probe(mib):
@@ -251,6 +277,9 @@ def main():
     flops = 2.0 * m * n * k
     if args.only in ("", "fused"):
         ms_step, wall_ms = timed(fused_step, stream, args.steps, args.warmup)
+        synchronize()
+        gpu_res = {"idx": didx.numpy(), "maxprob": dmp.numpy(), "seq": dseq.numpy(), "seq_len": dlen.numpy(),
+                   "score": dscore.numpy()}
         ms_head, _ = timed(fused_argmax, stream, args.steps, args.warmup)
         out["fused"] = (ms_step, wall_ms, ms_head)
 
@@ -319,7 +348,7 @@ def main():
 
     cpu = None
     if not args.no_cpu and args.only == "":
-        cpu = cpu_baseline(wk, qw.data, qw.scales, args.cpu_seconds)
+        cpu = cpu_baseline(wk, qw.data, qw.scales, args.cpu_seconds, gpu_res if "fused" in out else None)
 
     if "fused" in out:
         ms_step, wall_ms, ms_head = out["fused"]
