@@ -210,6 +210,15 @@ def other_config(name, modes, steps, warmup):
         flops = 2.0 * m * n * k
         r = {"ms_per_step": round(ms, 4), "rows_per_s": round(m / (ms / 1e3), 1),
              "TFLOPs": round(flops / (ms / 1e3) / 1e12, 2)}
+        if wk["quantized"] and m <= 8192:
+            # the same step from host arrays (ppocr_rh_decode): what one call per page costs
+            off = wk["line_off"]
+            for _ in range(3):
+                head.decode(a, off, mode)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                head.decode(a, off, mode)
+            r["host_arrays_ms"] = round((time.perf_counter() - t0) / steps * 1e3, 4)
         if not wk["quantized"]:
             dlog = DeviceArray((m, n), np.float32)
 
