@@ -207,3 +207,52 @@ def test_find_head_name_buffer_too_small(rh, tmp_path):
     w, b = ctypes.create_string_buffer(5), ctypes.create_string_buffer(64)
     rc = rh._lib.lib().ppocr_model_find_rec_head(os.fsencode(path), w, 5, b, 64, None, None)
     assert rc == rh.PPOCR_ERR_INVALID_ARG and "does not fit" in rh._lib.last_error()
+
+
+def test_mutated_files_never_crash(rh, tmp_path):
+    """Seeded truncations and byte mutations of a valid model file (header length field,
+    header JSON, graph JSON, data): the parser returns PPOCR_OK or PPOCR_ERR_MODEL for
+    each, never crashes.  Runs in a child process so that a crash fails this test alone."""
+    import subprocess
+    import sys
+    src = _graph_file(tmp_path, NECK + HEAD)
+    blob = open(src, "rb").read()
+    hlen = struct.unpack("<Q", blob[:8])[0]
+    rng = np.random.default_rng(77)
+    cases = []
+    for x in range(300):
+        b = bytearray(blob)
+        kind = x % 4
+        if kind == 0:  # truncation anywhere
+            b = b[:int(rng.integers(0, len(blob)))]
+        elif kind == 1:  # bytes of the header JSON replaced
+            for _ in range(int(rng.integers(1, 6))):
+                b[8 + int(rng.integers(0, hlen))] = int(rng.choice(list(b'{}[]",:0-9e\\ ')))
+        elif kind == 2:  # the header length field
+            vals = [0, 1, hlen - 1, hlen + 1, len(blob), 2**63 - 1, 2**64 - 1]
+            b[:8] = struct.pack("<Q", vals[int(rng.integers(0, len(vals)))])
+        else:  # a digit of an offset or shape changed
+            digits = [i for i in range(8, 8 + hlen) if chr(b[i]).isdigit()]
+            b[digits[int(rng.integers(0, len(digits)))]] = ord(str(int(rng.integers(0, 10))))
+        p = tmp_path / f"m{x}.safetensors"
+        p.write_bytes(bytes(b))
+        cases.append(str(p))
+    code = r"""
+import ctypes, os, sys
+import ppocr_rechead as rh
+L = rh._lib.lib()
+seen = set()
+for path in sys.argv[1:]:
+    w, b = ctypes.create_string_buffer(256), ctypes.create_string_buffer(256)
+    n, k = ctypes.c_int64(), ctypes.c_int64()
+    rc = L.ppocr_model_find_rec_head(os.fsencode(path), w, 256, b, 256, ctypes.byref(n), ctypes.byref(k))
+    seen.add(rc)
+print(sorted(seen))
+"""
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([os.path.join(os.path.dirname(os.path.dirname(
+        os.path.abspath(__file__))), "rust-ppocrv6_amd")]))
+    out = subprocess.run([sys.executable, "-c", code] + cases, env=env, capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, (out.returncode, out.stderr[-2000:])
+    seen = set(json.loads(out.stdout.strip().splitlines()[-1]))
+    assert seen <= {rh.PPOCR_OK, rh.PPOCR_ERR_MODEL}, seen
+    assert rh.PPOCR_ERR_MODEL in seen
