@@ -194,6 +194,21 @@ int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const 
                         int64_t* d_seq_len, float* d_score, void* d_workspace,
                         size_t workspace_bytes, void* stream);
 
+/* The whole head entered one node earlier, at the neck's Transpose.8 (perm [0,2,1]:
+ * Model::forward's Transpose, src/engine/model.rs:1325-1342, x.into_permute then a
+ * contiguous copy, src/tensor.rs:621-633): x [lines][k][steps] is the neck's output,
+ * channels first, for `lines` text lines of `steps` time steps each.  The transpose is
+ * folded into the head's activation loads (no transposed copy is made): the results are
+ * those of ppocr_rh_decode for the lines x[b] transposed, line b being rows
+ * b*steps .. b*steps + steps - 1 (idx, maxprob and seq in that row order).  The workspace
+ * is ppocr_rh_workspace_bytes(h, lines * steps, mode). */
+int ppocr_rh_decode_nct(const ppocr_rh_t* h, const float* x, int64_t lines, int64_t steps, int mode,
+                        int32_t* idx, float* maxprob, int32_t* seq, int64_t* seq_len, float* score);
+int ppocr_rh_decode_nct_dev(const ppocr_rh_t* h, const float* d_x, int64_t lines, int64_t steps,
+                            int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq,
+                            int64_t* d_seq_len, float* d_score, void* d_workspace,
+                            size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -501,8 +501,10 @@ Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws, int64_t m) {
 }
 
 // Projection + softmax statistics + merge (+ the CTC collapse with `ctc`), on device pointers.
+// line_len > 0: d_a is channels-first, [m / line_len][k][line_len].
 int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* d_idx, float* d_maxprob,
-              float* d_row_max, float* d_row_inv, uint8_t* ws, hipStream_t st, const CtcOut* ctc = nullptr) {
+              float* d_row_max, float* d_row_inv, uint8_t* ws, hipStream_t st, const CtcOut* ctc = nullptr,
+              int64_t line_len = 0) {
     const int nsplit = nsplit_for(h, m, cfg);
     const WsLayout L = ws_layout(m, nsplit);
     float* p_best = reinterpret_cast<float*>(ws + L.p_best);
@@ -511,10 +513,10 @@ int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* 
     if (cfg >= 0) {
         const Guard g = make_guard(h, L, ws, m);
         return launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, d_idx,
-                                 d_maxprob, d_row_max, d_row_inv, ctc, st);
+                                 d_maxprob, d_row_max, d_row_inv, ctc, st, line_len);
     }
     if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
-                                 p_idx, st))
+                                 p_idx, st, line_len))
         return e;
     if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, d_idx, d_maxprob, nullptr, st);
     return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, nullptr, st);
@@ -965,6 +967,57 @@ int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off
                                     idx ? hc.out<int32_t>(3) : nullptr, maxprob ? hc.out<float>(4) : nullptr,
                                     hc.out<int32_t>(0), hc.out<int64_t>(1), hc.out<float>(2), hc.ws(), hc.ws_bytes(),
                                     hc.stream()))
+        return e;
+    return hc.copy_out({seq, seq_len, score, idx, maxprob});
+}
+
+int ppocr_rh_decode_nct_dev(const ppocr_rh_t* h, const float* d_x, int64_t lines, int64_t steps, int mode,
+                            int32_t* d_idx, float* d_maxprob, int32_t* d_seq, int64_t* d_seq_len, float* d_score,
+                            void* d_workspace, size_t workspace_bytes, void* stream) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (lines < 0 || steps < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count or length");
+    if (steps > INT32_MAX || (steps > 0 && lines > INT64_MAX / steps))
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: line length too large");
+    const int64_t m = lines * steps;
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (lines == 0) return PPOCR_OK;
+    if (!d_seq_len || !d_score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    if (m > 0 && (!d_x || !d_seq)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    hipStream_t st = (hipStream_t)stream;
+    const CtcOut ctc{nullptr, lines, 0, d_seq, d_seq_len, d_score, steps};
+    if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
+    const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;
+    return run_stats(h, cfg, d_x, m, d_idx, d_maxprob, nullptr, nullptr, ws.p, st, &ctc, steps);
+}
+
+int ppocr_rh_decode_nct(const ppocr_rh_t* h, const float* x, int64_t lines, int64_t steps, int mode, int32_t* idx,
+                        float* maxprob, int32_t* seq, int64_t* seq_len, float* score) {
+    if (int e = check_head(h, "RecHeadHip")) return e;
+    if (lines < 0 || steps < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count or length");
+    if (steps > INT32_MAX || (steps > 0 && lines > INT64_MAX / steps))
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: line length too large");
+    const int64_t m = lines * steps;
+    if (int e = check_m(m, "RecHeadHip")) return e;
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    if (lines == 0) return PPOCR_OK;
+    if (!seq_len || !score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
+    if (m > 0 && (!x || !seq)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    DeviceGuard dg(h->device);
+    const size_t wsb = m > 0 ? ws_layout(m, nsplit_for(h, m, cfg)).total : 0;
+    const size_t xb = (size_t)(m * h->k) * 4, rb = (size_t)m * 4;
+    HostCall hc;
+    if (int e = hc.begin({xb}, {rb, (size_t)lines * 8, (size_t)lines * 4, idx ? rb : 0, maxprob ? rb : 0}, wsb))
+        return e;
+    if (int e = hc.copy_in({x})) return e;
+    if (int e = ppocr_rh_decode_nct_dev(h, hc.in<float>(0), lines, steps, mode, idx ? hc.out<int32_t>(3) : nullptr,
+                                        maxprob ? hc.out<float>(4) : nullptr, hc.out<int32_t>(0), hc.out<int64_t>(1),
+                                        hc.out<float>(2), hc.ws(), hc.ws_bytes(), hc.stream()))
         return e;
     return hc.copy_out({seq, seq_len, score, idx, maxprob});
 }

@@ -21,7 +21,7 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
     const float* __restrict__ bias, const float* __restrict__ a, int64_t m, int n, int k,
     int tiles_per_chunk, float* __restrict__ out, const float* __restrict__ row_max,
     const float* __restrict__ row_inv, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx) {
+    int* __restrict__ p_idx, int64_t line_len) {
     __shared__ __align__(16) float As[KC * AST];
     __shared__ float Ws[KC * WST];
 
@@ -56,10 +56,21 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
 
         for (int k0 = 0; k0 < k; k0 += KC) {
             __syncthreads();
-            for (int idx = tid; idx < BM * KC; idx += 256) {
-                const int mm = idx / KC, kk = idx % KC;
-                const int64_t row = m0 + mm;
-                As[kk * AST + mm] = (row < m && k0 + kk < k) ? a[row * k + k0 + kk] : 0.0f;
+            if (line_len > 0) {
+                // channels-first [lines][k][line_len]: neighbouring threads take neighbouring steps
+                for (int idx = tid; idx < BM * KC; idx += 256) {
+                    const int mm = idx % BM, kk = idx / BM;
+                    const int64_t row = m0 + mm, line = row / line_len;
+                    As[kk * AST + mm] = (row < m && k0 + kk < k)
+                                            ? a[(line * k + k0 + kk) * line_len + (row - line * line_len)]
+                                            : 0.0f;
+                }
+            } else {
+                for (int idx = tid; idx < BM * KC; idx += 256) {
+                    const int mm = idx / KC, kk = idx % KC;
+                    const int64_t row = m0 + mm;
+                    As[kk * AST + mm] = (row < m && k0 + kk < k) ? a[row * k + k0 + kk] : 0.0f;
+                }
             }
             for (int idx = tid; idx < BN * KC; idx += 256) {
                 const int nn = idx / KC, kk = idx % KC;
@@ -180,7 +191,7 @@ int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const
     const int ntiles = (int)((n + BN - 1) / BN);
     dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
     head_fma_kernel<EPI_LOGITS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, 1, out, nullptr,
-                                                      nullptr, nullptr, nullptr, nullptr);
+                                                      nullptr, nullptr, nullptr, nullptr, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
@@ -193,22 +204,23 @@ int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const 
     const int ntiles = (int)((n + BN - 1) / BN);
     dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
     head_fma_kernel<EPI_PROBS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, 1, probs, row_max,
-                                                     row_inv, nullptr, nullptr, nullptr);
+                                                     row_inv, nullptr, nullptr, nullptr, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
 
 int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                      const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
-                     float* p_sum, int* p_idx, hipStream_t st) {
+                     float* p_sum, int* p_idx, hipStream_t st, int64_t line_len) {
     if (int e = check_fma_args(m, n, k)) return e;
+    if (line_len < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
     if (nsplit < 1 || nsplit > 1024) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad nsplit");
     if (m <= 0) return PPOCR_OK;
     const int ntiles = (int)((n + BN - 1) / BN);
     const int tpc = (ntiles + nsplit - 1) / nsplit;
     dim3 grid(nsplit, (unsigned)((m + BM - 1) / BM));
     head_fma_kernel<EPI_STATS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, tpc, nullptr, nullptr,
-                                                     nullptr, p_best, p_sum, p_idx);
+                                                     nullptr, p_best, p_sum, p_idx, line_len);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

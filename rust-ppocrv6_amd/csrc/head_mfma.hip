@@ -119,9 +119,11 @@ __device__ __forceinline__ __bf16 split_term(float x, int t) {
 // Activation fragment of one lane for MFMA step s: row `row` of a (zero when the row
 // is not valid), the 8 k values of the lane's pair-group, as the bf16 term that pair
 // uses; `amax` is raised to the largest |value| loaded.  `vec`: rows and groups are
-// 16-byte aligned, so each fragment is two float4 loads.
+// 16-byte aligned, so each fragment is two float4 loads.  vec < 0 selects the
+// channels-first layout [lines][k][T] of the tensor before the neck's transpose, T = -vec:
+// row r is step r % T of line r / T, and its k values are T floats apart.
 template <int C, int G>
-__device__ __forceinline__ bf16x8 act_frag(const float* __restrict__ a, int64_t row, bool valid, int k, bool vec,
+__device__ __forceinline__ bf16x8 act_frag(const float* __restrict__ a, int64_t row, bool valid, int k, int vec,
                                           int s, int h, float& amax) {
     bf16x8 f;
 #pragma unroll
@@ -131,8 +133,14 @@ __device__ __forceinline__ bf16x8 act_frag(const float* __restrict__ a, int64_t 
     const int p = pg / G, g = pg % G;
     const int term = CfgT<C>::act(p);
     const float* src = a + row * (int64_t)k + 8 * g;
+    int64_t kst = 1;  // floats between consecutive k
+    if (vec < 0) {
+        kst = -(int64_t)vec;
+        const int64_t line = row / kst;
+        src = a + line * kst * k + (row - line * kst) + 8 * g * kst;
+    }
     float x[8];
-    if (vec && 8 * g + 8 <= k) {
+    if (vec > 0 && 8 * g + 8 <= k) {
         const f32x4 v0 = reinterpret_cast<const f32x4*>(src)[0];
         const f32x4 v1 = reinterpret_cast<const f32x4*>(src)[1];
 #pragma unroll
@@ -142,7 +150,7 @@ __device__ __forceinline__ bf16x8 act_frag(const float* __restrict__ a, int64_t 
         }
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (8 * g + e < k) ? src[e] : 0.0f;
+        for (int e = 0; e < 8; ++e) x[e] = (8 * g + e < k) ? src[e * kst] : 0.0f;
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -397,7 +405,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_
             arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
             float amax = 0.0f;
 #pragma unroll
-            for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec != 0, s, h, amax);
+            for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec, s, h, amax);
             if (!GATHER && guard_header && chunk == 0)
                 guard_append(amax, amax_limit, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch, guard_cap);
         }
@@ -652,7 +660,7 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
         float amax = 0.0f;
         bf16x8 bf[S];
 #pragma unroll
-        for (int s = 0; s < S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec != 0, s, h, amax);
+        for (int s = 0; s < S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec, s, h, amax);
         if (!GATHER && guard_header && chunk == 0)
             guard_append(amax, amax_limit, valid, arow, h, guard_header, guard_rows, guard_epoch, guard_cap);
         // rows of this lane's 16 accumulators (r -> row slot 8*(r/4) + 4*h + (r%4))
@@ -897,7 +905,8 @@ int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
                       int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx, const Guard* guard,
                       int32_t* idx, float* maxprob, float* row_max, float* row_inv, const CtcOut* ctc,
-                      hipStream_t st) {
+                      hipStream_t st, int64_t line_len) {
+    if (line_len < 0 || line_len > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
     if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
     if (nsplit != 1 && nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16 && nsplit != 32 && nsplit != 64)
         return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be a power of two <= 64");
@@ -907,7 +916,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
     const int tpc = (tg.tiles + nsplit - 1) / nsplit;
     const int grid = grid_blocks((int)mblocks, nsplit);
-    const int vec = vec_ok(a, k);
+    const int vec = line_len > 0 ? -(int)line_len : vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
     // No reset launch: the list is emptied by its epoch (first use) and by the merge below.
     const bool guarded = guard && guard->header && rcfg >= 0;

@@ -73,19 +73,22 @@ int stats_rows_per_block_mfma(int cfg, int64_t m);
 // CTC collapse of text lines fused into the statistics merge (device pointers): line i is
 // rows line_off[i] .. line_off[i+1]; outputs as ppocr_ctc_greedy.
 struct CtcOut {
-    const int64_t* line_off;
+    const int64_t* line_off;  // null: every line has line_len steps
     int64_t lines;
     int32_t blank;
     int32_t* seq;
     int64_t* seq_len;
     float* score;
+    int64_t line_len = 0;
 };
 
 // With `ctc`, the final merge also runs the CTC collapse (row_max and row_inv unused).
+// line_len > 0: `a` is channels-first, [m / line_len][k][line_len] (the tensor before the
+// neck's transpose); row r is step r % line_len of line r / line_len.
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                       int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
                       const Guard* guard, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
-                      const CtcOut* ctc, hipStream_t st);
+                      const CtcOut* ctc, hipStream_t st, int64_t line_len = 0);
 int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                       int64_t n, int64_t k, const float* row_max, const float* row_inv, float* probs,
                       const Guard* guard, hipStream_t st);
@@ -96,7 +99,7 @@ int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const
 constexpr int kFmaRowsPerBlock = 128;
 int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                      const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
-                     float* p_sum, int* p_idx, hipStream_t st);
+                     float* p_sum, int* p_idx, hipStream_t st, int64_t line_len = 0);
 int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                      const float* a, int64_t m, int64_t n, int64_t k, const float* row_max,
                      const float* row_inv, float* probs, hipStream_t st);

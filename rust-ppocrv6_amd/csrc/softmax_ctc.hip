@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
 // is merged by a group of kMergeLanes lanes into LDS, then wave 0 collapses the round as
 // ctc_greedy_kernel does (ballot, prefix popcount, score summed in step order), carrying
 // the previous index between rounds.  Offsets are clamped into [0, m] (a line with t1 < t0
-// is empty).
+// is empty); with no offsets, line i is steps i * line_len .. (i + 1) * line_len - 1.
 constexpr int kCtcRound = 1024 / kMergeLanes;
 __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict__ p_best,
                                                          const float* __restrict__ p_sum,
@@ -298,14 +298,14 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
                                                          float* __restrict__ val_out, int32_t* __restrict__ seq,
                                                          int64_t* __restrict__ seq_len, float* __restrict__ score,
                                                          unsigned long long* __restrict__ guard_header,
-                                                         unsigned guard_epoch) {
+                                                         unsigned guard_epoch, int64_t line_len) {
     __shared__ int32_t s_id[kCtcRound];
     if (guard_header && blockIdx.x == 0 && threadIdx.x == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     __shared__ float s_v[kCtcRound];
     const int tid = threadIdx.x, lane = tid & 63, g = tid % kMergeLanes, step = tid / kMergeLanes;
     const int64_t line = blockIdx.x;
-    const int64_t t0 = min(max(line_off[line], (int64_t)0), m);
-    const int64_t t1 = min(max(line_off[line + 1], t0), m);
+    const int64_t t0 = line_off ? min(max(line_off[line], (int64_t)0), m) : min(line * line_len, m);
+    const int64_t t1 = line_off ? min(max(line_off[line + 1], t0), m) : min(t0 + line_len, m);
     int64_t cnt = 0;
     float sum = -0.0f;
     int32_t carry = blank;  // index of the step before the current one
@@ -403,7 +403,8 @@ int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, 
     if (ctc.lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
     merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
                                                        ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score,
-                                                       guard ? guard->header : nullptr, guard ? guard->epoch : 0u);
+                                                       guard ? guard->header : nullptr, guard ? guard->epoch : 0u,
+                                                       ctc.line_len);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

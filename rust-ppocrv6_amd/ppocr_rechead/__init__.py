@@ -216,6 +216,27 @@ class RecHead:
         seqs = [seq[line_off[b]:line_off[b] + seq_len[b]].copy() for b in range(lines)]
         return {"idx": idx[:m], "maxprob": mp[:m], "seqs": seqs, "score": score[:lines]}
 
+    def decode_nct(self, x, mode=None):
+        """Whole head from the neck's output before its transpose (Transpose.8, perm
+        [0,2,1]; src/engine/model.rs:1325-1342): x [lines, k, T], channels first.  The
+        same results as decode() on x.transpose(0, 2, 1) with T steps per line."""
+        x = _f32(x)
+        if x.ndim != 3 or x.shape[1] != self.k:
+            raise OcrError("RecHeadHip", f"expected [lines, {self.k}, T], got {list(x.shape)}")
+        lines, _, steps = x.shape
+        m = lines * steps
+        idx = np.empty(max(m, 1), np.int32)
+        mp = np.empty(max(m, 1), np.float32)
+        seq = np.zeros(max(m, 1), np.int32)
+        seq_len = np.zeros(max(lines, 1), np.int64)
+        score = np.zeros(max(lines, 1), np.float32)
+        if lines:
+            _check(_lib.lib().ppocr_rh_decode_nct(self._h, _ptr(x), lines, steps,
+                                                  self.default_mode if mode is None else mode, _ptr(idx), _ptr(mp),
+                                                  _ptr(seq), _ptr(seq_len), _ptr(score)))
+        seqs = [seq[b * steps:b * steps + seq_len[b]].copy() for b in range(lines)]
+        return {"idx": idx[:m], "maxprob": mp[:m], "seqs": seqs, "score": score[:lines]}
+
 
 def find_rec_head(path):
     """The recognition head of a model file: the MatMul -> [Add bias] -> Softmax(axis=-1) ->

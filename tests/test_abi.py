@@ -120,6 +120,10 @@ def test_decode_dev_argument_errors_do_not_need_a_device(rh):
     assert L.ppocr_rh_decode_dev(None, *args) == rh.PPOCR_ERR_INVALID_ARG
     assert rh._lib.last_error() == "RecHeadHip: null head handle"
     assert L.ppocr_rh_decode(None, None, None, 1, 2, None, None, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
+    assert L.ppocr_rh_decode_nct(None, None, 1, 120, 2, None, None, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
+    assert L.ppocr_rh_decode_nct_dev(None, None, 1, 120, 2, None, None, None, None, None, None, 0,
+                                     None) == rh.PPOCR_ERR_INVALID_ARG
+    assert rh._lib.last_error() == "RecHeadHip: null head handle"
 
 
 def test_missing_library_fails_loudly(tmp_path):
