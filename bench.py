@@ -73,8 +73,8 @@ def traffic_from_profiles(kernel_key):
 
 
 def agreement(wk, q, s, ref, gpu):
-    """The GPU step's results against the oracle's on the same batch, in the survey's
-    terms: argmax mismatches (each with its top-2 logit gap, from f64 logits of the
+    """The GPU step's results against the oracle's on the same batch, in the terms of the
+    parity bar: argmax mismatches (each with its top-2 logit gap, from f64 logits of the
     dequantized weight), the largest maxprob difference, and per line whether the CTC
     sequences are identical, plus the largest score difference."""
     mis = np.nonzero(ref["idx"] != gpu["idx"])[0]
