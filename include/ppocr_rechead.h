@@ -111,7 +111,10 @@ int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized);
 
 /* Device workspace needed by the `_dev` entry points below for m rows (0 if none).  A
  * NULL workspace makes the call allocate one on its stream (stream-ordered) and free it
- * after use.  Calls that share one workspace must not overlap. */
+ * after use.  Calls that share one workspace must not overlap.  One workspace may serve
+ * calls of any size in turn: its first 8 bytes hold the precision guard's list header,
+ * which every guarded call leaves empty when it ends; what a new workspace holds there is
+ * told apart by the call's epoch (zeroing a new workspace once makes that certain). */
 size_t ppocr_rh_workspace_bytes(const ppocr_rh_t* h, int64_t m, int mode);
 
 /* ---------------------------------------------------------------- MatMul.12

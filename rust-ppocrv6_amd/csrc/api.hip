@@ -118,9 +118,10 @@ ArenaPool& arena_pool() {
 
 size_t align256(size_t x) { return (std::max<size_t>(x, 1) + 255) / 256 * 256; }
 
-// One host-pointer call on the current device: inputs, then outputs, then the workspace,
-// each 256-byte aligned in the arena.  The destructor waits for the call's stream before
-// the arena goes back.
+// One host-pointer call on the current device: the workspace, then the inputs, then the
+// outputs, each 256-byte aligned in the arena.  The workspace starts the arena, so its
+// guard header (offset 0) is the same word in every call; it is cleared whenever the arena
+// is allocated.  The destructor waits for the call's stream before the arena goes back.
 class HostCall {
 public:
     ~HostCall() {
@@ -139,14 +140,14 @@ public:
         a_ = arena_pool().take(dev);
         if (!a_) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
         if (!a_->stream) PPOCR_HIP(hipStreamCreateWithFlags(&a_->stream, hipStreamNonBlocking));
-        size_t total = 0;
+        ws_off_ = 0;
+        ws_bytes_ = align256(ws);
+        size_t total = ws_bytes_;
+        in_begin_ = total;
         for (size_t r : in) place(r, &total, &in_);
         in_end_ = total;
         for (size_t r : out) place(r, &total, &out_);
         out_end_ = total;
-        ws_off_ = total;
-        ws_bytes_ = align256(ws);
-        total += ws_bytes_;
         if (a_->cap < total) {
             if (a_->base) (void)hipFree(a_->base);
             a_->base = nullptr;
@@ -159,8 +160,9 @@ public:
             }
             a_->base = static_cast<uint8_t*>(p);
             a_->cap = total;
+            if (int e = launch_guard_clear(reinterpret_cast<unsigned long long*>(a_->base), a_->stream)) return e;
         }
-        if (!a_->pinned && (in_end_ <= kStageBytes || out_end_ - in_end_ <= kStageBytes)) {
+        if (!a_->pinned && (in_end_ - in_begin_ <= kStageBytes || out_end_ - in_end_ <= kStageBytes)) {
             void* p = nullptr;
             if (hipHostMalloc(&p, kStageBytes, hipHostMallocDefault) == hipSuccess) a_->pinned = static_cast<uint8_t*>(p);
             else (void)hipGetLastError();  // no staging: copies go directly
@@ -181,14 +183,16 @@ public:
     // Copies the inputs (srcs in the order given to begin) to the device.
     int copy_in(std::initializer_list<const void*> srcs) const {
         size_t i = 0;
-        const bool staged = a_->pinned && in_end_ <= kStageBytes;
+        const size_t span = in_end_ - in_begin_;
+        const bool staged = a_->pinned && span <= kStageBytes;
         for (const void* src : srcs) {
             const auto [off, n] = in_[i++];
             if (!n || !src) continue;
-            if (staged) std::memcpy(a_->pinned + off, src, n);
+            if (staged) std::memcpy(a_->pinned + (off - in_begin_), src, n);
             else PPOCR_HIP(hipMemcpyAsync(a_->base + off, src, n, hipMemcpyHostToDevice, a_->stream));
         }
-        if (staged && in_end_) PPOCR_HIP(hipMemcpyAsync(a_->base, a_->pinned, in_end_, hipMemcpyHostToDevice, a_->stream));
+        if (staged && span)
+            PPOCR_HIP(hipMemcpyAsync(a_->base + in_begin_, a_->pinned, span, hipMemcpyHostToDevice, a_->stream));
         return PPOCR_OK;
     }
     // Copies the outputs back (dsts in the order given to begin; null ones are skipped) and
@@ -223,7 +227,7 @@ private:
     }
     HostArena* a_ = nullptr;
     std::vector<std::pair<size_t, size_t>> in_, out_;  // (offset, bytes)
-    size_t in_end_ = 0, out_end_ = 0, ws_off_ = 0, ws_bytes_ = 0;
+    size_t in_begin_ = 0, in_end_ = 0, out_end_ = 0, ws_off_ = 0, ws_bytes_ = 0;
 };
 
 // Device buffer owned for the duration of a host-pointer call.
@@ -471,27 +475,35 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 struct WsLayout {
     size_t p_best, p_sum, p_idx, row_max, row_inv, guard_header, guard_rows, total;
 };
+// The guard header sits at offset 0 whatever m and nsplit are, so a workspace reused for
+// batches of other sizes finds there the header its previous call left (emptied by that
+// call's merge), never a partial or a list entry of another layout.
 WsLayout ws_layout(int64_t m, int nsplit) {
     WsLayout L;
     const size_t pm = align_up((size_t)nsplit * (size_t)m * 4);
     const size_t rm = align_up((size_t)m * 4);
-    L.p_best = 0;
-    L.p_sum = pm;
-    L.p_idx = 2 * pm;
-    L.row_max = 3 * pm;
+    L.guard_header = 0;
+    L.p_best = kAlign;
+    L.p_sum = L.p_best + pm;
+    L.p_idx = L.p_sum + pm;
+    L.row_max = L.p_idx + pm;
     L.row_inv = L.row_max + rm;
-    L.guard_header = L.row_inv + rm;
-    L.guard_rows = L.guard_header + kAlign;
+    L.guard_rows = L.row_inv + rm;
     L.total = L.guard_rows + rm;
     return L;
 }
 
-// A new epoch for every guarded pass (never 0, so zeroed memory is not taken for a list).
+// A new epoch for every guarded pass: a mixed counter with the top bit set.  A header whose
+// epoch differs from the call's counts as an empty list, so the epoch must not match what a
+// workspace may hold before its first use: with the top bit set it never equals a row or
+// class index, a count or a non-negative float, and it is never 0 (the cleared header).
 unsigned next_epoch() {
     static std::atomic<unsigned> counter{0};
-    unsigned e = counter.fetch_add(1, std::memory_order_relaxed) + 1;
-    while (e == 0) e = counter.fetch_add(1, std::memory_order_relaxed) + 1;
-    return e;
+    unsigned x = counter.fetch_add(1, std::memory_order_relaxed) * 0x9E3779B9u + 0x7F4A7C15u;
+    x ^= x >> 16;
+    x *= 0x85EBCA6Bu;
+    x ^= x >> 13;
+    return x | 0x80000000u;
 }
 
 Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws, int64_t m) {
@@ -540,13 +552,13 @@ struct Workspace {
             return PPOCR_OK;
         }
         void* q = nullptr;
-        if (hipMallocAsync(&q, std::max<size_t>(need, 1), s) != hipSuccess) {
+        if (hipMallocAsync(&q, std::max<size_t>(need, kAlign), s) != hipSuccess) {
             (void)hipGetLastError();
             return fail(PPOCR_ERR_NO_MEMORY, std::string(op) + ": workspace allocation failed");
         }
         p = static_cast<uint8_t*>(q);
         owned = true;
-        return PPOCR_OK;
+        return launch_guard_clear(reinterpret_cast<unsigned long long*>(p), s);  // the header, at offset 0
     }
 };
 

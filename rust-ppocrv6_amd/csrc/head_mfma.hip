@@ -891,6 +891,12 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     });
 }
 
+int launch_guard_clear(unsigned long long* guard_header, hipStream_t st) {
+    guard_reset_kernel<<<1, 1, 0, st>>>(guard_header, 0u);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
 int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m, int64_t n,
                        int64_t k, float* out, const Guard* guard, hipStream_t st) {
     return launch_rows(cfg, 0, tg, rec, a, m, n, k, nullptr, nullptr, out, guard, st);

@@ -62,6 +62,10 @@ int launch_head_limits(const int8_t* q, const float* scales, const float* bias, 
 int launch_build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
                          const float* scale, const float* bias, uint8_t* rec, hipStream_t st);
 
+// Writes an empty guard header (epoch 0, which no call uses): run once on every workspace
+// the library allocates, before its first use.
+int launch_guard_clear(unsigned long long* guard_header, hipStream_t st);
+
 int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                        int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.

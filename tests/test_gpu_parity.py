@@ -532,6 +532,42 @@ def test_guard_list_in_a_reused_workspace(orc, rh):
     h.close()
 
 
+def test_workspace_holding_small_integers(orc, rh):
+    """A caller workspace may hold anything before a call, in particular what calls of other
+    sizes leave there: row and class indices, counts.  The guard header is the workspace's
+    first 8 bytes and every epoch has its top bit set, so no such word reads as a list of
+    the current call: with the workspace filled with small integers before each call, the
+    fused head gives the results of a zeroed workspace, bit for bit."""
+    from ppocr_rechead import workloads as wl
+    from ppocr_rechead.hip import DeviceArray, hip, check, synchronize
+    import ctypes
+    L = rh._lib.lib()
+    w_t, bias = wl.weights(stress=True)
+    q, s = orc.pack_int8(w_t)
+    h = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    rng = np.random.default_rng(43)
+    a = rng.standard_normal((900, 120), dtype=np.float32)
+    a[rng.choice(900, 120, replace=False)] *= np.float32(50.0)  # many guarded rows
+    ws_bytes = h.workspace_bytes(900, 2)
+    ws = DeviceArray((ws_bytes // 4 + 1,), np.int32)
+
+    def run(m, fill):
+        check(hip().hipMemcpy(ws.p, np.full(ws_bytes // 4 + 1, fill, np.int32).ctypes.data_as(ctypes.c_void_p),
+                              ctypes.c_size_t(ws_bytes), 1), "hipMemcpy H2D")
+        da, di, dp = DeviceArray.from_numpy(a[:m]), DeviceArray((m,), np.int32), DeviceArray((m,), np.float32)
+        rh._check(L.ppocr_rh_argmax_dev(h.handle, da.p, m, 2, di.p, dp.p, ws.p, ws_bytes, None))
+        synchronize()
+        return di.numpy(), dp.numpy().view(np.uint32)
+
+    for m in (900, 333, 64):
+        want = run(m, 0)
+        for fill in (1, 2, 3, 37, 1000, 0x7FFFFFFF):
+            print(f"workspace of small integers: m={m} fill={fill}", flush=True)
+            got = run(m, fill)
+            assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), (m, fill)
+    h.close()
+
+
 def test_host_calls_from_many_threads(rh, rhead):
     """The handle is shared by threads (the reference's rec_pool workers): 8 threads
     decoding different line batches at once through the host-pointer entry point (each
