@@ -180,8 +180,9 @@ struct RowSource {
 // head's largest |w| exceeds the limit is appended to a device list, to be recomputed
 // with one more activation term.  lanes i and i+32 see complementary k groups.
 // The list's header is (epoch << 32) | count: the first append of a call installs the
-// call's epoch with count 0 (a header of another call, or uninitialised memory, counts as
-// empty), then each append takes the next slot.  Slots past the capacity are dropped.
+// call's epoch with count 0 (a header with another epoch counts as empty; epochs have the
+// top bit set, so no index, count or non-negative float left in the workspace matches
+// one), then each append takes the next slot.  Slots past the capacity are dropped.
 __device__ __forceinline__ void guard_append(float amax, float amax_limit, bool valid, int64_t row, int h,
                                              unsigned long long* guard_header, int* guard_rows, unsigned epoch,
                                              int capacity) {
