@@ -138,3 +138,22 @@ def test_fp32_head_random_shapes(orc, rh, k, n, mode):
     gap = top2_gap(ref64)
     check_argmax(got["idx"], np.argmax(ref64, axis=1).astype(np.int32), gap, label=f"fp32 head k={k}")
     assert np.abs(got["maxprob"] - refp.max(axis=1)).max() < TOL
+
+
+@pytest.mark.parametrize("n,mode", [(120, 3), (240, 3), (360, 3), (360, 0)])
+def test_neck_matmuls_with_k_120(orc, rh, n, mode):
+    """The rec neck's MatMul nodes with K = 120 (weights [120, 120 | 240 | 360], bias
+    folded) run as FP32 heads through the same entry points (ppocr_rh_create_f32 +
+    ppocr_rh_logits): against the oracle's matmul_transposed_b, max-abs 1e-4, for a
+    neck-like activation batch (3 lines x T=120, N(0,1)) and weights N(0, 0.1^2)."""
+    rng = np.random.default_rng(n + mode)
+    w_t = (rng.standard_normal((n, 120)) * 0.1).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    a = rng.standard_normal((360, 120)).astype(np.float32)
+    print(f"neck matmul n={n} mode={mode}", flush=True)
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    got = head.logits(a, mode)
+    head.close()
+    ref = orc.matmul_transposed_b(a, w_t, bias)
+    assert got.shape == (360, n)
+    assert np.abs(got - ref).max() < TOL
