@@ -87,11 +87,13 @@ int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, 
                                      int quantize, int device, ppocr_rh_t** out);
 /* Finds the recognition head in a model file's graph (the "graph" entry of the
  * safetensors metadata, src/engine/loader.rs:48-60): the segment MatMul(x, W) ->
- * Add(bias) (optional) -> Softmax(axis -1) -> graph output that the engine-level fused
- * hook replaces, with the reference's load-time rules: Identity nodes are aliases
+ * Add(bias) (optional) -> Softmax over the last axis -> graph output that the engine-level
+ * fused hook replaces, with the reference's load-time rules: Identity nodes are aliases
  * (src/engine/model.rs:67-95), the bias is folded when the MatMul's output is used only by
  * an Add whose other input is a weight (src/engine/model.rs:96-166), Softmax's axis
- * defaults to -1 (src/engine/model.rs:1286-1302).  Writes the weight's name (an F32
+ * defaults to -1 and is normalised by the input's rank (src/engine/model.rs:1286-1302); a
+ * non-negative axis is accepted when it is the last one, the rank being traced back to a
+ * Transpose (the PP-OCRv6 models' Softmax has axis 2 on [1, T, classes]).  Writes the weight's name (an F32
  * [k][n] tensor) and the bias's ("" when there is none) as NUL-terminated strings, and n
  * and k (may be NULL).  PPOCR_ERR_MODEL when the file has no graph or no such segment;
  * PPOCR_ERR_INVALID_ARG when a name does not fit its buffer. */

@@ -3,9 +3,15 @@
 // -1) -> graph output.  The rules follow the reference's load-time passes: Identity nodes
 // are aliases (src/engine/model.rs:67-95); a MatMul whose output is used once folds the
 // bias of the Add that uses it when the Add's other input is a weight
-// (src/engine/model.rs:96-166); Softmax takes attribute "axis", default -1
-// (src/engine/model.rs:1286-1302).  Graph validity checks are those of Model::load
-// (src/engine/model.rs:40-66).
+// (src/engine/model.rs:96-166); Softmax takes attribute "axis", default -1, normalised
+// against the input's rank at run time (src/engine/model.rs:1286-1302,
+// src/ops/softmax.rs:199-212).  The hook needs the softmax over the classes, the last axis:
+// axis -1, or a non-negative axis equal to the rank minus one, where the rank is traced
+// back from the MatMul's activation through MatMul with a weight, Add with a weight and
+// Identity (each keeps the rank) to a Transpose (its perm's length).  The PP-OCRv6 graphs
+// carry Transpose.8 perm [0,2,1] -> MatMul.12 -> Add -> Identity -> Softmax.2 axis 2 (the
+// small model) and Transpose -> MatMul.0 -> Add -> MatMul.1 -> Add -> Softmax.0 axis 2 (the
+// tiny one).  Graph validity checks are those of Model::load (src/engine/model.rs:40-66).
 #include "model_graph.hpp"
 
 #include <map>
@@ -103,10 +109,36 @@ int find_rec_head(const StFile& f, RecHeadNames* out) {
     };
     auto is_weight = [&](const std::string& s) { return f.find(s.c_str()) != nullptr; };
 
+    // rank of an activation, traced back to a Transpose through rank-keeping nodes (0: unknown)
+    auto rank_of = [&](std::string x) -> int64_t {
+        for (int hops = 0; hops < 64; ++hops) {
+            x = resolve(x);
+            auto it = producer.find(x);
+            if (it == producer.end()) return 0;
+            const GNode& p = nodes[it->second];
+            if (p.op == "Transpose") {
+                const JVal* perm = p.attrs ? p.attrs->get("perm") : nullptr;
+                return (perm && perm->kind == JVal::kArr) ? (int64_t)perm->arr.size() : 0;
+            }
+            if (p.op == "MatMul" && p.in.size() == 2 && is_weight(resolve(p.in[1]))) {
+                x = p.in[0];
+            } else if (p.op == "Add" && p.in.size() == 2 && is_weight(resolve(p.in[1]))) {
+                x = p.in[0];
+            } else if (p.op == "Add" && p.in.size() == 2 && is_weight(resolve(p.in[0]))) {
+                x = p.in[1];
+            } else {
+                return 0;
+            }
+        }
+        return 0;
+    };
+    auto known_rank = [&](const GNode* mm) -> int64_t { return rank_of(mm->in[0]); };
     for (const GNode& sm : nodes) {
         if (sm.op != "Softmax") continue;
         const JVal* axis = sm.attrs ? sm.attrs->get("axis") : nullptr;
-        if (axis && !(axis->kind == JVal::kNum && axis->is_int && axis->i == -1)) continue;
+        if (axis && !(axis->kind == JVal::kNum && axis->is_int)) continue;
+        const int64_t ax = axis ? axis->i : -1;
+        if (ax != -1 && ax < 0) continue;
         if (!is_output(sm.out[0])) continue;
         const std::string x = resolve(sm.in[0]);
         const GNode* mm = nullptr;
@@ -126,6 +158,7 @@ int find_rec_head(const StFile& f, RecHeadNames* out) {
             if (mm && usage[x] != 1) mm = nullptr;
         }
         if (!mm || mm->in.size() != 2) continue;
+        if (ax != -1 && known_rank(mm) != ax + 1) continue;  // softmax over the classes only
         const StTensor* w = f.find(resolve(mm->in[1]).c_str());
         if (!w || w->dtype != "F32" || w->shape.size() != 2) continue;
         const int64_t k = w->shape[0], n = w->shape[1];
@@ -140,7 +173,7 @@ int find_rec_head(const StFile& f, RecHeadNames* out) {
         out->k = k;
         return PPOCR_OK;
     }
-    return model_fail("no MatMul -> [Add] -> Softmax(axis=-1) segment ending at a graph output");
+    return model_fail("no MatMul -> [Add] -> Softmax(last axis) segment ending at a graph output");
 }
 
 }  // namespace ppocr

@@ -15,7 +15,7 @@ struct RecHeadNames {
     int64_t n = 0, k = 0;
 };
 
-// Finds the first MatMul -> [Add bias] -> Softmax(axis -1) -> graph output segment.
+// Finds the first MatMul -> [Add bias] -> Softmax(last axis) -> graph output segment.
 // Returns PPOCR_OK, or PPOCR_ERR_MODEL with the message set.
 int find_rec_head(const StFile& f, RecHeadNames* out);
 

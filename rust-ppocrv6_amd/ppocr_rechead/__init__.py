@@ -239,7 +239,7 @@ class RecHead:
 
 
 def find_rec_head(path):
-    """The recognition head of a model file: the MatMul -> [Add bias] -> Softmax(axis=-1) ->
+    """The recognition head of a model file: the MatMul -> [Add bias] -> Softmax(last axis) ->
     graph output segment of its graph, as {"weight", "bias" (None if absent), "n", "k"}
     (the segment the engine-level fused hook replaces)."""
     wb, bb = ctypes.create_string_buffer(1024), ctypes.create_string_buffer(1024)

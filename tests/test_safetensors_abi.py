@@ -118,7 +118,8 @@ def test_header_padding_and_metadata_are_accepted(rh, tmp_path):
 def _graph_file(tmp_path, nodes, outputs=("probs",), inputs=("x",), name="g.safetensors", graph=None, n=70, k=120,
                 with_bias=True):
     from safetensors.numpy import save_file
-    t = {"linear_8.w_0": np.zeros((k, n), np.float32), "other.w": np.zeros((4, 4), np.float32)}
+    t = {"linear_8.w_0": np.zeros((k, n), np.float32), "other.w": np.zeros((4, 4), np.float32),
+         "other.b": np.zeros(4, np.float32)}
     if with_bias:
         t["linear_8.b_0"] = np.zeros(n, np.float32)
     g = graph if graph is not None else json.dumps({"inputs": list(inputs), "outputs": list(outputs), "nodes": nodes})
@@ -146,7 +147,8 @@ def test_find_head_in_the_graph(rh, tmp_path):
     assert r == {"weight": "linear_8.w_0", "bias": "linear_8.b_0", "n": 70, "k": 120}
 
 
-@pytest.mark.parametrize("variant", ["bias_first", "no_bias", "identities", "no_axis", "tiny"])
+@pytest.mark.parametrize("variant", ["bias_first", "no_bias", "identities", "no_axis", "tiny", "transpose_axis2",
+                                     "two_matmuls_axis2"])
 def test_find_head_variants(rh, tmp_path, variant):
     nodes = [dict(n) for n in NECK + HEAD]
     n, k, with_bias = 70, 120, True
@@ -165,6 +167,15 @@ def test_find_head_variants(rh, tmp_path, variant):
         del nodes[3]["attrs"]
     elif variant == "tiny":
         n, k = 6906, 80
+    elif variant == "transpose_axis2":  # the small PP-OCRv6 model's tail: a rank-3 softmax on axis 2
+        nodes = [_node("Transpose.8", "Transpose", ["h"], ["x2"], {"perm": [0, 2, 1]})] + [dict(x) for x in HEAD]
+        nodes[-1]["attrs"] = {"axis": 2}
+    elif variant == "two_matmuls_axis2":  # the tiny model's tail: the rank traced through a MatMul and an Add
+        nodes = [_node("Transpose.2", "Transpose", ["h"], ["t"], {"perm": [0, 2, 1]}),
+                 _node("MatMul.0", "MatMul", ["t", "other.w"], ["m0"]),
+                 _node("Add.104", "Add", ["m0", "other.b"], ["a0"]),
+                 _node("Identity.89", "Identity", ["a0"], ["x2"])] + [dict(x) for x in HEAD]
+        nodes[-1]["attrs"] = {"axis": 2}
     r = rh.find_rec_head(_graph_file(tmp_path, nodes, outputs, n=n, k=k, with_bias=with_bias))
     assert r == {"weight": "linear_8.w_0", "bias": None if variant == "no_bias" else "linear_8.b_0", "n": n, "k": k}
 
@@ -172,7 +183,8 @@ def test_find_head_variants(rh, tmp_path, variant):
 @pytest.mark.parametrize("variant,msg", [
     ("axis_1", "no MatMul"), ("not_output", "no MatMul"), ("logits_used_twice", "no MatMul"),
     ("weight_missing", "no MatMul"), ("no_graph", "missing 'graph'"), ("bad_json", "failed to parse graph JSON"),
-    ("empty_outputs", "both must be non-empty"), ("no_outputs", "declares no outputs")])
+    ("empty_outputs", "both must be non-empty"), ("no_outputs", "declares no outputs"),
+    ("transpose_axis1", "no MatMul"), ("axis2_rank_unknown", "no MatMul")])
 def test_find_head_rejects(rh, tmp_path, variant, msg):
     nodes = [dict(n) for n in NECK + HEAD]
     outputs, graph = ("probs",), None
@@ -191,6 +203,11 @@ def test_find_head_rejects(rh, tmp_path, variant, msg):
         nodes[0]["outputs"] = []
     elif variant == "no_outputs":
         outputs = ()
+    elif variant == "transpose_axis1":  # a softmax over the steps, not the classes
+        nodes = [_node("Transpose.8", "Transpose", ["h"], ["x2"], {"perm": [0, 2, 1]})] + [dict(x) for x in HEAD]
+        nodes[-1]["attrs"] = {"axis": 1}
+    elif variant == "axis2_rank_unknown":  # no Transpose to give the rank: axis 2 may not be the last
+        nodes[3]["attrs"] = {"axis": 2}
     if variant == "no_graph":
         from safetensors.numpy import save_file
         path = str(tmp_path / "nograph.safetensors")
@@ -256,3 +273,19 @@ print(sorted(seen))
     seen = set(json.loads(out.stdout.strip().splitlines()[-1]))
     assert seen <= {rh.PPOCR_OK, rh.PPOCR_ERR_MODEL}, seen
     assert rh.PPOCR_ERR_MODEL in seen
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/models"), reason="reference model files not mounted")
+def test_find_head_in_the_reference_models(rh):
+    """The reference's own model files: the small and tiny recognition models' heads are
+    found (Softmax on axis 2 of a rank-3 tensor, the rank traced to Transpose.8); the
+    classifier and the detectors have none."""
+    d = "/root/reference/models"
+    assert rh.find_rec_head(os.path.join(d, "PP-OCRv6_small_rec.safetensors")) == {
+        "weight": "linear_8.w_0", "bias": "linear_8.b_0", "n": 18710, "k": 120}
+    assert rh.find_rec_head(os.path.join(d, "PP-OCRv6_tiny_rec.safetensors")) == {
+        "weight": "linear_1.w_0", "bias": "linear_1.b_0", "n": 6906, "k": 80}
+    for name in ("PP-OCRv6_cls", "PP-OCRv6_small_det", "PP-OCRv6_tiny_det"):
+        with pytest.raises(rh.OcrError) as ei:
+            rh.find_rec_head(os.path.join(d, name + ".safetensors"))
+        assert ei.value.code == rh.PPOCR_ERR_MODEL
