@@ -107,6 +107,34 @@ def test_tiny_head_real_rows(orc, rh):
     head.close()
 
 
+@pytest.mark.parametrize("mode", [0, 2, 3])
+def test_small_head_real_rows_decode(orc, rh, mode):
+    """The whole head on 512 classes of the small model's real weights (its first 256
+    classes, blank included, 128 from the middle and the last 128; golden fixture): ragged
+    lines of seeded activations, some rows x30 (guarded), against the oracle."""
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "pack_rows.npz"))
+    q, s = g["small_rec_q"], g["small_rec_scales"]
+    rng = np.random.default_rng(17)
+    bias = (rng.standard_normal(q.shape[0], dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+    lens = [120, 37, 1, 80]
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    a = rng.standard_normal((int(off[-1]), 120), dtype=np.float32)
+    a[rng.choice(a.shape[0], 12, replace=False)] *= np.float32(30.0)
+    print(f"small real rows decode mode={mode}", flush=True)
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    got = head.decode(a, off, mode)
+    head.close()
+    ref = orc.rechead_lines(a, off, q, s, bias)
+    gap = top2_gap(f64_logits_q(a, q, s, bias))
+    exempt = check_argmax(got["idx"], ref["idx"], gap, label=f"real rows mode {mode}")
+    assert np.abs(got["maxprob"] - ref["maxprob"]).max() < TOL
+    for b in range(len(lens)):
+        if np.any((exempt >= off[b]) & (exempt < off[b + 1])):
+            continue
+        assert np.array_equal(got["seqs"][b], ref["seqs"][b]), (mode, b)
+        assert abs(float(got["score"][b]) - float(ref["score"][b])) < TOL, (mode, b)
+
+
 @pytest.mark.parametrize("mode", [0, 1, 3])
 def test_fp32_head_logits(orc, rh, mode):
     from ppocr_rechead import workloads as wl
