@@ -105,4 +105,6 @@ def test_nct_dev_with_workspace_and_errors(orc, rh):
     with pytest.raises(rh.OcrError):
         head.decode_nct(x.transpose(0, 2, 1), 2)
     assert L.ppocr_rh_decode_nct(head.handle, None, 0, T, 2, None, None, None, None, None) == rh.PPOCR_OK
+    empty = head.decode_nct(np.zeros((3, k, 0), np.float32), 2)  # lines without steps
+    assert [len(x) for x in empty["seqs"]] == [0, 0, 0] and not np.any(empty["score"])
     head.close()
