@@ -115,3 +115,50 @@ def test_head_found_in_the_model_graph(orc, rh, tmp_path):
     assert np.abs(gm["maxprob"] - ref["maxprob"]).max() < 1e-4
     hm.close()
     hs.close()
+
+
+def test_head_found_in_a_pp_ocr_v6_style_graph(orc, rh, tmp_path):
+    """The tail as the reference's small recognition model carries it (Squeeze ->
+    Transpose.8 perm [0,2,1] -> MatMul.12 -> Add.204 -> Identity.210 -> Softmax.2 axis 2 ->
+    fetch_name_0): RecHead.from_model finds the head, and fed the Transpose.8 input
+    (channels first, decode_nct) it gives the results of the head built from the tensor
+    names on the transposed rows, bit for bit, within the bars against the oracle."""
+    import json
+    from safetensors.numpy import save_file
+    from gpu_common import check_argmax, f64_logits_q, top2_gap
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    graph = {"inputs": ["x"], "outputs": ["fetch_name_0"], "nodes": [
+        {"name": "Squeeze.7", "op": "Squeeze", "inputs": ["p2o.pd_op.add.78.0"], "outputs": ["p2o.pd_op.squeeze.0.0"],
+         "attrs": {"axes": [2]}},
+        {"name": "Transpose.8", "op": "Transpose", "inputs": ["p2o.pd_op.squeeze.0.0"],
+         "outputs": ["p2o.pd_op.transpose.8.0"], "attrs": {"perm": [0, 2, 1]}},
+        {"name": "MatMul.12", "op": "MatMul", "inputs": ["p2o.pd_op.transpose.8.0", "linear_8.w_0"],
+         "outputs": ["p2o.pd_op.matmul.12.0"], "attrs": {}},
+        {"name": "Add.204", "op": "Add", "inputs": ["p2o.pd_op.matmul.12.0", "linear_8.b_0"], "outputs": ["Add.205"],
+         "attrs": {}},
+        {"name": "Identity.210", "op": "Identity", "inputs": ["Add.205"], "outputs": ["p2o.pd_op.add.79.0"],
+         "attrs": {}},
+        {"name": "Softmax.2", "op": "Softmax", "inputs": ["p2o.pd_op.add.79.0"], "outputs": ["fetch_name_0"],
+         "attrs": {"axis": 2}}]}
+    path = str(tmp_path / "rec_v6.safetensors")
+    save_file({"linear_8.w_0": np.ascontiguousarray(w_t.T), "linear_8.b_0": bias}, path,
+              metadata={"graph": json.dumps(graph)})
+    print("head from a PP-OCRv6-style graph", flush=True)
+    hm = rh.RecHead.from_model(path)
+    hs = rh.RecHead.from_safetensors(path, "linear_8.w_0", "linear_8.b_0")
+    rng = np.random.default_rng(23)
+    lines, T = 12, 120
+    x = rng.standard_normal((lines, 120, T)).astype(np.float32)  # the Transpose.8 input
+    a = np.ascontiguousarray(x.transpose(0, 2, 1).reshape(-1, 120))
+    off = np.arange(lines + 1, dtype=np.int64) * T
+    gm, gs = hm.decode_nct(x), hs.decode(a, off)
+    _same(gm["idx"], gs["idx"])
+    _same(gm["maxprob"], gs["maxprob"])
+    _same(gm["score"], gs["score"])
+    q, s = orc.pack_int8(w_t)
+    ref = orc.rechead_lines(a, off, q, s, bias)
+    check_argmax(gm["idx"], ref["idx"], top2_gap(f64_logits_q(a, q, s, bias)), label="v6-style graph head")
+    assert np.abs(gm["maxprob"] - ref["maxprob"]).max() < 1e-4
+    hm.close()
+    hs.close()
