@@ -95,6 +95,8 @@ def test_dictionary_loading(rh, tmp_path):
     ref_keys = "/root/reference/models/ppocrv6_keys.txt"
     if os.path.exists(ref_keys):
         assert rh.CtcDecoder.from_file(ref_keys).vocab_size() == 18710
+        # the tiny model's dictionary matches its head's 6906 classes
+        assert rh.CtcDecoder.from_file("/root/reference/models/ppocrv6_tiny_keys.txt").vocab_size() == 6906
 
 
 def test_workloads_are_deterministic():
