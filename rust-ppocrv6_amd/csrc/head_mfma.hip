@@ -13,8 +13,12 @@
 // D[i][j] sits in lane j + 32*((i/4) % 2), register (i % 4) + 4*(i/8).
 //
 // K-concatenation: the product list ("pairs") of a configuration, times the G groups of
-// 8 along k, gives P = pairs*G pair-groups; MFMA step s feeds pair-group 2s to lanes
-// 0-31 and 2s+1 to lanes 32-63 (a half-step past P reads a zero block).
+// 8 along k, gives P = pairs*G (product, group) slots; each MFMA step feeds one slot to
+// lanes 0-31 and one to lanes 32-63 (a slot past the end is a zero block).  The steps walk
+// the groups two at a time and, for each pair of groups, every product in turn, products
+// on the same weight plane adjacent: consecutive steps of the same plane then read the same
+// weight fragment (an INT8 head's activation terms all multiply q), so the two-term mode
+// reads 8 weight fragments per tile for its 15 steps.
 #include <utility>
 
 #include "kernels.hpp"
@@ -56,19 +60,54 @@ struct CfgT<CFG_F3> {  // a0 * w0 + a0 * w1 + a1 * w0
 
 bool mfma_supports_groups(int G) { return G == 15 || G == 10; }
 
-// Tile geometry of a configuration: P pair-groups, S MFMA steps, FRAG bytes of weight
-// fragments per staged tile, REC bytes per tile record (fragments + epilogue constants),
-// BUF bytes per LDS buffer (record + a 512-byte zero block for the half-step past P).
+// Tile geometry of a configuration: P (product, group) slots, S MFMA steps, FRAG bytes of
+// weight fragments per staged tile, REC bytes per tile record (fragments + epilogue
+// constants), BUF bytes per LDS buffer (record + a 512-byte zero block for empty slots).
+struct Slot {
+    int p;  // product (index into CfgT::act / wpl); < 0: the zero block
+    int g;  // group of 8 along k
+};
 template <int C, int G>
 struct Geo {
-    static constexpr int P = CfgT<C>::pairs * G;
+    static constexpr int NPROD = CfgT<C>::pairs;
+    static constexpr int P = NPROD * G;
     static constexpr int S = (P + 1) / 2;
     static constexpr int FRAG = CfgT<C>::wplanes * G * 512;
     static constexpr int REC = FRAG + 512;
     static constexpr int BUF = REC + 512;
-    // LDS byte offset of the fragment of pair-group pg within a staged tile.
-    __host__ __device__ static constexpr int off(int pg) {
-        return pg >= P ? REC : (CfgT<C>::wpl(pg / G) * G + pg % G) * 512;
+    // the x-th product when they are ordered by weight plane (stable), so products that
+    // share a plane are adjacent
+    __host__ __device__ static constexpr int prod(int x) {
+        int n = 0;
+        for (int pl = 0; pl < 2; ++pl)
+            for (int p = 0; p < NPROD; ++p)
+                if (CfgT<C>::wpl(p) == pl && n++ == x) return p;
+        return -1;
+    }
+    // Slot fed to lane half h by MFMA step s: over the G/2 full pairs of groups, one step
+    // per product with groups 2j and 2j+1 on the two halves; an odd last group then takes
+    // the products two per step.
+    __host__ __device__ static constexpr Slot slot(int s, int h) {
+        const int body = (G / 2) * NPROD;
+        if (s < body) return Slot{prod(s % NPROD), 2 * (s / NPROD) + h};
+        const int x = 2 * (s - body) + h;
+        if ((G & 1) && x < NPROD) return Slot{prod(x), G - 1};
+        return Slot{-1, 0};
+    }
+    // LDS byte offset of the weight fragment of step s, half h, within a staged tile
+    __host__ __device__ static constexpr int off(int s, int h) {
+        const Slot sl = slot(s, h);
+        return sl.p < 0 ? REC : (CfgT<C>::wpl(sl.p) * G + sl.g) * 512;
+    }
+    // step s reads a weight fragment other than step s-1's
+    __host__ __device__ static constexpr bool fresh(int s) {
+        return s == 0 || off(s, 0) != off(s - 1, 0) || off(s, 1) != off(s - 1, 1);
+    }
+    // index of the fragment step s uses, counted in step order
+    __host__ __device__ static constexpr int fid(int s) {
+        int f = 0;
+        for (int x = 1; x <= s; ++x) f += fresh(x) ? 1 : 0;
+        return f;
     }
 };
 
@@ -76,10 +115,38 @@ struct Geo {
 // read consecutive fragments, so the address is one per-lane register plus an immediate.
 template <int C, int G>
 __device__ __forceinline__ bf16x8 weight_frag(const uint8_t* buf, int s, int lane_base, int i16, int h) {
-    const int o0 = Geo<C, G>::off(2 * s);
-    const int o1 = Geo<C, G>::off(2 * s + 1);
+    const int o0 = Geo<C, G>::off(s, 0);
+    const int o1 = Geo<C, G>::off(s, 1);
     const int addr = (o1 - o0 == 512) ? lane_base + o0 : i16 + (h ? o1 : o0);
     return *reinterpret_cast<const bf16x8*>(buf + addr);
+}
+
+// Weight fragments in flight, NB register buffers: the fragment of step s sits in buffer
+// fid(s) % NB, and the fragment of step s + NB is read (when it is a new one) right after
+// the MFMAs of step s.  That read overwrites fragment fid(s + NB) - NB, which is at most
+// fid(s) and, when equal, is last used by step s (every step after s up to s + NB starts
+// a new fragment), so no fragment is overwritten while a later step still needs it.
+template <int C, int G, int NB>
+__device__ __forceinline__ void frag_prefetch_first(bf16x8 (&wq)[NB], const uint8_t* buf, int lane_base, int i16,
+                                                    int h) {
+    [&]<int... x>(std::integer_sequence<int, x...>) {
+        ([&] {
+            if constexpr (x < Geo<C, G>::S && Geo<C, G>::fresh(x))
+                wq[Geo<C, G>::fid(x) % NB] = weight_frag<C, G>(buf, x, lane_base, i16, h);
+        }(), ...);
+    }(std::make_integer_sequence<int, NB>{});
+}
+template <int C, int G, int NB, int s>
+__device__ __forceinline__ void frag_prefetch_after(bf16x8 (&wq)[NB], const uint8_t* buf, int lane_base, int i16,
+                                                    int h) {
+    if constexpr (s + NB < Geo<C, G>::S) {
+        if constexpr (Geo<C, G>::fresh(s + NB))
+            wq[Geo<C, G>::fid(s + NB) % NB] = weight_frag<C, G>(buf, s + NB, lane_base, i16, h);
+    }
+}
+template <int C, int G, int NB, int s>
+__device__ __forceinline__ const bf16x8& frag_of(const bf16x8 (&wq)[NB]) {
+    return wq[Geo<C, G>::fid(s) % NB];
 }
 
 // Grid position -> (block of rows, vocabulary chunk).  Workgroups go to the 8 XCDs of
@@ -117,21 +184,22 @@ __device__ __forceinline__ __bf16 split_term(float x, int t) {
 }
 
 // Activation fragment of one lane for MFMA step s: row `row` of a (zero when the row
-// is not valid), the 8 k values of the lane's pair-group, as the bf16 term that pair
-// uses; `amax` is raised to the largest |value| loaded.  `vec`: rows and groups are
-// 16-byte aligned, so each fragment is two float4 loads.  vec < 0 selects the
-// channels-first layout [lines][k][T] of the tensor before the neck's transpose, T = -vec:
-// row r is step r % T of line r / T, and its k values are T floats apart.
-template <int C, int G>
+// is not valid), the 8 k values of the lane's slot, as the bf16 term its product uses;
+// `amax` is raised to the largest |value| loaded.  `vec`: rows and groups are 16-byte
+// aligned, so each fragment is two float4 loads.  vec < 0 selects the channels-first
+// layout [lines][k][T] of the tensor before the neck's transpose, T = -vec: row r is step
+// r % T of line r / T, and its k values are T floats apart.
+template <int C, int G, int s>
 __device__ __forceinline__ bf16x8 act_frag(const float* __restrict__ a, int64_t row, bool valid, int k, int vec,
-                                          int s, int h, float& amax) {
+                                          int h, float& amax) {
     bf16x8 f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = (__bf16)0.0f;
-    const int pg = 2 * s + h;
-    if (pg >= Geo<C, G>::P || !valid) return f;
-    const int p = pg / G, g = pg % G;
-    const int term = CfgT<C>::act(p);
+    constexpr Slot s0 = Geo<C, G>::slot(s, 0), s1 = Geo<C, G>::slot(s, 1);
+    const int p = h ? s1.p : s0.p, g = h ? s1.g : s0.g;
+    if (p < 0 || !valid) return f;
+    constexpr int t0 = s0.p < 0 ? 0 : CfgT<C>::act(s0.p), t1 = s1.p < 0 ? 0 : CfgT<C>::act(s1.p);
+    const int term = h ? t1 : t0;
     const float* src = a + row * (int64_t)k + 8 * g;
     int64_t kst = 1;  // floats between consecutive k
     if (vec < 0) {
@@ -285,6 +353,15 @@ constexpr int epi_pieces() {
     return 13 * MB + 2;
 }
 
+// Largest of three values, as one v_max3_f32.  A quiet NaN operand is ignored (IEEE
+// maxNum, the behaviour of fmaxf); written out because fmaxf on values the compiler cannot
+// prove canonical (loop-carried, MFMA results) costs a v_max_f32 x, x, x per operand first.
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 template <int P, int MB, bool NOREF>
 __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restrict__ ep, int h, int j,
                                           f32x4 (&cs)[2], f32x4 (&cb)[2], const float (&ref)[MB],
@@ -311,12 +388,12 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
         }
     } else if constexpr (P < 4 * per_q + MB) {
         constexpr int b = P - 4 * per_q;
-        const float m01 = fmaxf(fmaxf(t[b][0], t[b][1]), t[b][2]);
-        const float m02 = fmaxf(fmaxf(t[b][3], t[b][4]), t[b][5]);
-        const float m03 = fmaxf(fmaxf(t[b][6], t[b][7]), t[b][8]);
-        const float m04 = fmaxf(fmaxf(t[b][9], t[b][10]), t[b][11]);
-        const float m05 = fmaxf(fmaxf(t[b][12], t[b][13]), t[b][14]);
-        st.tmax[b] = fmaxf(fmaxf(fmaxf(m01, m02), fmaxf(m03, m04)), fmaxf(m05, t[b][15]));
+        const float m01 = max3_f32(t[b][0], t[b][1], t[b][2]);
+        const float m02 = max3_f32(t[b][3], t[b][4], t[b][5]);
+        const float m03 = max3_f32(t[b][6], t[b][7], t[b][8]);
+        const float m04 = max3_f32(t[b][9], t[b][10], t[b][11]);
+        const float m05 = max3_f32(t[b][12], t[b][13], t[b][14]);
+        st.tmax[b] = max3_f32(max3_f32(m01, m02, m03), max3_f32(m04, m05, t[b][15]), -INFINITY);
         st.better[b] = st.tmax[b] > best[b];
     } else if constexpr (P == 4 * per_q + MB) {
 #pragma unroll
@@ -331,7 +408,7 @@ __device__ __forceinline__ void epi_piece(f32x16 (&t)[MB], const float* __restri
     } else {
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
-            best[b] = fmaxf(best[b], st.tmax[b]);
+            best[b] = max3_f32(best[b], st.tmax[b], -INFINITY);
             if constexpr (!NOREF)
                 st.need = st.need | ((best[b] != -INFINITY) & (__builtin_fabsf(best[b] - ref[b]) > 64.0f));
         }
@@ -405,8 +482,9 @@ __global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_
         for (int b = 0; b < MB; ++b) {
             arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
             float amax = 0.0f;
-#pragma unroll
-            for (int s = 0; s < S; ++s) bf[b][s] = act_frag<C, G>(a, arow[b], valid[b], k, vec, s, h, amax);
+            [&]<int... s>(std::integer_sequence<int, s...>) {
+                ((bf[b][s] = act_frag<C, G, s>(a, arow[b], valid[b], k, vec, h, amax)), ...);
+            }(std::make_integer_sequence<int, S>{});
             if (!GATHER && guard_header && chunk == 0)
                 guard_append(amax, amax_limit, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch, guard_cap);
         }
@@ -461,22 +539,21 @@ __global__ __launch_bounds__(64 * kStatsWaves, 8 / kStatsWaves) void stats_main_
                 // weight fragments are read kPrefetch MFMA steps ahead of their use, so a wave
                 // never waits on LDS with epilogue work queued behind the wait
                 bf16x8 wq[kPrefetch];
-#pragma unroll
-                for (int x = 0; x < kPrefetch; ++x) wq[x] = weight_frag<C, G>(bufn, x < S ? x : S - 1, lb, i * 16, h);
+                frag_prefetch_first<C, G, kPrefetch>(wq, bufn, lb, i * 16, h);
                 // each MFMA step: the MFMA of block 0, half of the step's epilogue work, the
                 // MFMAs of the other blocks and the fragment prefetch, the other half; so a
                 // wave always has vector work to issue while its MFMAs run
                 [&]<int... s>(std::integer_sequence<int, s...>) {
                     ([&] {
-                        accM[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[0][s], accM[0], 0, 0, 0);
+                        const bf16x8& wf = frag_of<C, G, kPrefetch, s>(wq);
+                        accM[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[0][s], accM[0], 0, 0, 0);
                         __builtin_amdgcn_sched_barrier(0);
                         epi_pieces_of_half<2 * S, 2 * s, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
                         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                         for (int b = 1; b < MB; ++b)
-                            accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wq[s % kPrefetch], bf[b][s], accM[b], 0, 0, 0);
-                        if constexpr (s + kPrefetch < S)
-                            wq[s % kPrefetch] = weight_frag<C, G>(bufn, s + kPrefetch, lb, i * 16, h);
+                            accM[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, bf[b][s], accM[b], 0, 0, 0);
+                        frag_prefetch_after<C, G, kPrefetch, s>(wq, bufn, lb, i * 16, h);
                         __builtin_amdgcn_sched_barrier(0);
                         epi_pieces_of_half<2 * S, 2 * s + 1, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
                         __builtin_amdgcn_sched_barrier(0);
@@ -660,8 +737,9 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
         const int64_t arow = src.row(j0 + i, m, valid);
         float amax = 0.0f;
         bf16x8 bf[S];
-#pragma unroll
-        for (int s = 0; s < S; ++s) bf[s] = act_frag<C, G>(a, arow, valid, k, vec, s, h, amax);
+        [&]<int... s>(std::integer_sequence<int, s...>) {
+            ((bf[s] = act_frag<C, G, s>(a, arow, valid, k, vec, h, amax)), ...);
+        }(std::make_integer_sequence<int, S>{});
         if (!GATHER && guard_header && chunk == 0)
             guard_append(amax, amax_limit, valid, arow, h, guard_header, guard_rows, guard_epoch, guard_cap);
         // rows of this lane's 16 accumulators (r -> row slot 8*(r/4) + 4*h + (r%4))
@@ -692,14 +770,12 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
             // overlap instead of each MFMA waiting on its own
             constexpr int kAhead = S < 8 ? S : 8;
             bf16x8 wq[kAhead];
-#pragma unroll
-            for (int x = 0; x < kAhead; ++x) wq[x] = weight_frag<C, G>(buf, x, i * 16 + h * 512, i * 16, h);
+            frag_prefetch_first<C, G, kAhead>(wq, buf, i * 16 + h * 512, i * 16, h);
             f32x16 acc = {};
             [&]<int... st>(std::integer_sequence<int, st...>) {
                 ([&] {
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[st], wq[st % kAhead], acc, 0, 0, 0);
-                    if constexpr (st + kAhead < S)
-                        wq[st % kAhead] = weight_frag<C, G>(buf, st + kAhead, i * 16 + h * 512, i * 16, h);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[st], frag_of<C, G, kAhead, st>(wq), acc, 0, 0, 0);
+                    frag_prefetch_after<C, G, kAhead, st>(wq, buf, i * 16 + h * 512, i * 16, h);
                     __builtin_amdgcn_sched_barrier(0);
                 }(), ...);
             }(std::make_integer_sequence<int, S>{});
