@@ -42,9 +42,9 @@ struct ppocr_rh {
     float* d_bias = nullptr;   // [n] bias (0 when absent)
     uint8_t* d_rec = nullptr;  // tiles x rec_bytes MFMA tile records
     size_t device_bytes = 0;
-    // Precision guard of the 2-term split: rows with max|a| above this are recomputed with
-    // three terms.  16 / (largest |dequantised weight|): a single product then carries at
-    // most 16 * 2^-17 of split residual.
+    FmaWeights fma{};          // the device weights above, for the fp32 FMA kernels
+    // Precision guard of the split-activation modes (INT8 two terms, FP32 bf16x3): rows
+    // with max|a| above this are recomputed (three terms, or fp32 FMA).
     float amax_limit = INFINITY;
     // Rows with max|a| at most this have every logit in [-kLogitBound, kLogitBound]:
     // |logit| <= max|a| * max_c sum_k |w_ck| + max_c |b_c|.  Also at most amax_limit.
@@ -360,10 +360,21 @@ ppocr_rh* new_handle(int64_t n, int64_t k, bool quantized, int device) {
     return h;
 }
 
-// Guard limits of an INT8 head from wmax = max_c (float)max|q_c| * scale_c, w1 = max_c
-// sum_k |q_ck| * scale_c and bmax = max_c |b_c| (both in double).
-void set_limits(ppocr_rh* h, float wmax, double w1, double bmax) {
-    h->amax_limit = wmax > 0.0f ? 16.0f / wmax : INFINITY;
+// The split modes' logit error grows with max|a| * ||w_c||_2.  Measured on N(0, 0.05^2)
+// heads (k = 120, 18710 classes, rows scaled to a given max|a|), the largest error over
+// 4.8M logits is about 4.7e-6 * max|a| * L2 for the INT8 head's two activation terms and
+// 9.5e-6 * max|a| * L2 for an FP32 head's three bf16 products (whose floor is the
+// two-plane split of the weight).  These bounds on max|a| * L2 keep it near 5e-5, half the
+// 1e-4 bar; rows above are recomputed.
+constexpr double kSplitBoundInt8 = 8.0;
+constexpr double kSplitBoundF32 = 4.0;
+
+// Guard limits from wmax = max_c max_k |w_ck| (float), w1 = max_c sum_k |w_ck|,
+// l2 = max_c ||w_c||_2 and bmax = max_c |b_c| (double), w the dequantised weight.
+void set_limits(ppocr_rh* h, float wmax, double w1, double l2, double bmax) {
+    double lim = wmax > 0.0f ? 16.0 / (double)wmax : INFINITY;
+    if (l2 > 0.0 && std::isfinite(l2)) lim = std::min(lim, (h->quantized ? kSplitBoundInt8 : kSplitBoundF32) / l2);
+    h->amax_limit = (float)lim;
     // logit range bound: the largest L1 norm of a dequantised weight row and the largest
     // |bias|, rounded up by a small margin
     const double room = (double)kLogitBound - bmax * 1.001;
@@ -372,6 +383,28 @@ void set_limits(ppocr_rh* h, float wmax, double w1, double bmax) {
         h->stats_amax_limit = (float)std::min((double)h->amax_limit, lim);
         h->stats_noref = true;
     }
+}
+
+// Guard limits of a head whose weights, scales and bias are on the device, reduced there
+// (the same kernel for every way of creating a head, so equal weights give equal limits).
+int device_limits(ppocr_rh* h, bool has_bias) {
+    DevBuf lim;
+    if (int e = lim.alloc(sizeof(HeadLimitBits))) return e;
+    PPOCR_HIP(hipMemset(lim.p, 0, sizeof(HeadLimitBits)));
+    if (int e = launch_head_limits(h->d_q, h->d_w, h->d_scale, has_bias ? h->d_bias : nullptr, h->n, h->k,
+                                   lim.as<HeadLimitBits>(), nullptr))
+        return e;
+    HeadLimitBits hl;
+    PPOCR_HIP(hipMemcpy(&hl, lim.p, sizeof(hl), hipMemcpyDeviceToHost));
+    float wmax;
+    double w1, l2, bmax;
+    const unsigned wbits = hl.wmax;
+    std::memcpy(&wmax, &wbits, 4);
+    std::memcpy(&w1, &hl.w1, 8);
+    std::memcpy(&l2, &hl.l2, 8);
+    std::memcpy(&bmax, &hl.bmax, 8);
+    set_limits(h, wmax, w1, l2, bmax);
+    return PPOCR_OK;
 }
 
 int create_common(const int8_t* q, const float* w_t, const float* scales, const float* bias, int64_t n, int64_t k,
@@ -384,23 +417,6 @@ int create_common(const int8_t* q, const float* w_t, const float* scales, const 
 
     std::unique_ptr<ppocr_rh, void (*)(ppocr_rh*)> h(new_handle(n, k, q != nullptr, device), free_handle);
     if (!h) return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: host allocation failed");
-    if (q) {
-        float wmax = 0.0f;
-        double w1 = 0.0, bmax = 0.0;
-        for (int64_t j = 0; j < n; ++j) {
-            int qm = 0;
-            int64_t l1 = 0;
-            for (int64_t kk = 0; kk < k; ++kk) {
-                const int v = std::abs((int)q[j * k + kk]);
-                qm = std::max(qm, v);
-                l1 += v;
-            }
-            wmax = std::max(wmax, (float)qm * scales[j]);
-            w1 = std::max(w1, (double)l1 * (double)scales[j]);
-            if (bias) bmax = std::max(bmax, std::fabs((double)bias[j]));
-        }
-        set_limits(h.get(), wmax, w1, bmax);
-    }
 
     std::vector<float> sc_host;
     const float* sc = scales;
@@ -422,6 +438,8 @@ int create_common(const int8_t* q, const float* w_t, const float* scales, const 
     }
     if (int e = upload(&h->d_scale, sc, (size_t)n, &total)) return e;
     if (int e = upload(&h->d_bias, bi, (size_t)n, &total)) return e;
+    h->fma = FmaWeights{h->d_q, h->d_w, h->d_scale, h->d_bias};
+    if (int e = device_limits(h.get(), bias != nullptr)) return e;
     if (h->mfma_ok) {
         std::vector<uint8_t> rec = build_records(h->geom, n, k, q, w_t, sc, bias);
         if (int e = upload(&h->d_rec, rec.data(), rec.size(), &total)) return e;
@@ -507,9 +525,10 @@ unsigned next_epoch() {
 }
 
 Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws, int64_t m) {
-    return Guard{h->amax_limit, reinterpret_cast<unsigned long long*>(ws + L.guard_header),
-                 reinterpret_cast<int*>(ws + L.guard_rows), (int)std::min<int64_t>(m, INT32_MAX), next_epoch(), h->stats_amax_limit,
-                 h->stats_noref};
+    return Guard{h->amax_limit,       reinterpret_cast<unsigned long long*>(ws + L.guard_header),
+                 reinterpret_cast<int*>(ws + L.guard_rows), (int)std::min<int64_t>(m, INT32_MAX),
+                 next_epoch(),        h->stats_amax_limit,
+                 h->stats_noref,      h->fma};
 }
 
 // Projection + softmax statistics + merge (+ the CTC collapse with `ctc`), on device pointers.
@@ -675,25 +694,8 @@ int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, 
     }
     if (b) PPOCR_HIP(hipMemcpy(h->d_bias, b->data, (size_t)n * 4, hipMemcpyHostToDevice));
     else PPOCR_HIP(hipMemset(h->d_bias, 0, (size_t)n * 4));
-    if (quantize) {
-        // guard limits from the packed weight, reduced on the device
-        DevBuf lim;
-        if (int e = lim.alloc(24)) return e;
-        PPOCR_HIP(hipMemset(lim.p, 0, 24));
-        unsigned long long* l64 = lim.as<unsigned long long>();
-        if (int e = launch_head_limits(h->d_q, h->d_scale, b ? h->d_bias : nullptr, n, k,
-                                       reinterpret_cast<unsigned*>(l64 + 2), l64, l64 + 1, nullptr))
-            return e;
-        unsigned long long hl[3];
-        PPOCR_HIP(hipMemcpy(hl, lim.p, 24, hipMemcpyDeviceToHost));
-        float wmax;
-        double w1, bmax;
-        const unsigned wbits = (unsigned)(hl[2] & 0xffffffffu);
-        std::memcpy(&wmax, &wbits, 4);
-        std::memcpy(&w1, &hl[0], 8);
-        std::memcpy(&bmax, &hl[1], 8);
-        set_limits(h.get(), wmax, w1, bmax);
-    }
+    h->fma = FmaWeights{h->d_q, h->d_w, h->d_scale, h->d_bias};
+    if (int e = device_limits(h.get(), b != nullptr)) return e;
     if (h->mfma_ok) {
         const size_t rec_bytes = (size_t)h->geom.tiles * h->geom.rec_bytes();
         if (int e = dev_alloc((void**)&h->d_rec, rec_bytes)) return e;

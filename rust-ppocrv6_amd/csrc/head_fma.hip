@@ -4,174 +4,205 @@
 // and the (exactly dequantised) weight, fp32 accumulation, then (sum * scale) + bias.
 // Register tile: every thread owns 8 rows x 4 classes of a 128 x 64 block; k is staged
 // through LDS in chunks of 40.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace ppocr {
 
 namespace {
 constexpr int BM = 128, BN = 64, KC = 40;
+constexpr int64_t kFmaRescueSlots = 128;  // row-block slots of a gather-mode (rescue) launch
 constexpr int AST = BM + 4;  // LDS row strides (floats); +4 keeps 16-byte alignment
 constexpr int WST = BN + 1;
 
-enum { EPI_LOGITS = 0, EPI_PROBS = 1, EPI_STATS = 2 };
 
-template <int EPI>
+// Rows of a block: contiguous rows m0 .. m0 + BM - 1, or (GATHER) entries of the precision
+// guard's row list of another kernel's pass (checked, not trusted: an entry outside [0, m)
+// is skipped).  cpc: classes per vocabulary chunk; chunk c covers [c * cpc, (c + 1) * cpc).
+struct FmaRows {
+    const int* list;  // null: contiguous rows
+    int count;
+    __device__ __forceinline__ int64_t row(int64_t j, int64_t m, bool& valid) const {
+        if (list) {
+            const int64_t r = j < count ? (int64_t)list[j] : -1;
+            valid = r >= 0 && r < m;
+            return valid ? r : 0;
+        }
+        valid = j < m;
+        return j;
+    }
+};
+
+template <int EPI, bool GATHER>
 __global__ __launch_bounds__(256) void head_fma_kernel(
     const int8_t* __restrict__ q, const float* __restrict__ w, const float* __restrict__ scale,
-    const float* __restrict__ bias, const float* __restrict__ a, int64_t m, int n, int k,
-    int tiles_per_chunk, float* __restrict__ out, const float* __restrict__ row_max,
-    const float* __restrict__ row_inv, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, int64_t line_len) {
+    const float* __restrict__ bias, const float* __restrict__ a, int64_t m, int n, int k, int cpc,
+    float* __restrict__ out, const float* __restrict__ row_max, const float* __restrict__ row_inv,
+    float* __restrict__ p_best, float* __restrict__ p_sum, int* __restrict__ p_idx, int64_t line_len,
+    const unsigned long long* __restrict__ guard_header, const int* __restrict__ guard_rows, unsigned guard_epoch,
+    int guard_cap) {
     __shared__ __align__(16) float As[KC * AST];
     __shared__ float Ws[KC * WST];
 
     const int tid = threadIdx.x, tm = tid >> 4, tn = tid & 15;
-    const int64_t m0 = (int64_t)blockIdx.y * BM;
     const int chunk = blockIdx.x;
-    const int ntiles = (n + BN - 1) / BN;
-    const int t0 = chunk * tiles_per_chunk;
-    const int t1 = min(t0 + tiles_per_chunk, ntiles);
-
-    RowStat st[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) st[r] = RowStat{-INFINITY, 0.0f, 0.0f, 0};
-    bool refzero = true;
-    float rmax[8], rinv[8];
-    if (EPI == EPI_PROBS) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int64_t row = m0 + 8 * tm + r;
-            rmax[r] = row < m ? row_max[row] : 0.0f;
-            rinv[r] = row < m ? row_inv[row] : 0.0f;
-        }
+    const int c0 = chunk * cpc;
+    const int c1 = min(c0 + cpc, n);
+    FmaRows src{nullptr, 0};
+    if constexpr (GATHER) {
+        const unsigned long long hv = *guard_header;
+        const unsigned c = (unsigned)(hv >> 32) == guard_epoch ? (unsigned)hv : 0u;
+        src = FmaRows{guard_rows, c < (unsigned)guard_cap ? (int)c : guard_cap};
     }
+    const int64_t nrows = GATHER ? (int64_t)src.count : m;
 
-    for (int t = t0; t < t1; ++t) {
-        const int n0 = t * BN;
-        float acc[8][4];
+    for (int64_t m0 = (int64_t)blockIdx.y * BM; m0 < nrows; m0 += (int64_t)gridDim.y * BM) {
+        // this thread's 8 rows (local slots 8 * tm .. 8 * tm + 7 of the block)
+        int64_t rows[8];
+        bool rvalid[8];
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[r][j] = 0.0f;
+        for (int r = 0; r < 8; ++r) rows[r] = src.row(m0 + 8 * tm + r, m, rvalid[r]);
 
-        for (int k0 = 0; k0 < k; k0 += KC) {
-            __syncthreads();
-            if (line_len > 0) {
-                // channels-first [lines][k][line_len]: neighbouring threads take neighbouring steps
-                for (int idx = tid; idx < BM * KC; idx += 256) {
-                    const int mm = idx % BM, kk = idx / BM;
-                    const int64_t row = m0 + mm, line = row / line_len;
-                    As[kk * AST + mm] = (row < m && k0 + kk < k)
-                                            ? a[(line * k + k0 + kk) * line_len + (row - line * line_len)]
-                                            : 0.0f;
+        RowStat st[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) st[r] = RowStat{-INFINITY, 0.0f, 0.0f, 0};
+        bool refzero = true;
+        float rmax[8], rinv[8];
+        if (EPI == EPI_PROBS) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                rmax[r] = rvalid[r] ? row_max[rows[r]] : 0.0f;
+                rinv[r] = rvalid[r] ? row_inv[rows[r]] : 0.0f;
+            }
+        }
+
+        for (int n0 = c0; n0 < c1; n0 += BN) {
+            float acc[8][4];
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[r][j] = 0.0f;
+
+            for (int k0 = 0; k0 < k; k0 += KC) {
+                __syncthreads();
+                if (line_len > 0) {
+                    // channels-first [lines][k][line_len]: neighbouring threads take neighbouring steps
+                    for (int idx = tid; idx < BM * KC; idx += 256) {
+                        const int mm = idx % BM, kk = idx / BM;
+                        bool v;
+                        const int64_t row = src.row(m0 + mm, m, v), line = row / line_len;
+                        As[kk * AST + mm] = (v && k0 + kk < k)
+                                                ? a[(line * k + k0 + kk) * line_len + (row - line * line_len)]
+                                                : 0.0f;
+                    }
+                } else {
+                    for (int idx = tid; idx < BM * KC; idx += 256) {
+                        const int mm = idx / KC, kk = idx % KC;
+                        bool v;
+                        const int64_t row = src.row(m0 + mm, m, v);
+                        As[kk * AST + mm] = (v && k0 + kk < k) ? a[row * k + k0 + kk] : 0.0f;
+                    }
+                }
+                for (int idx = tid; idx < BN * KC; idx += 256) {
+                    const int nn = idx / KC, kk = idx % KC;
+                    const int col = n0 + nn;
+                    float v = 0.0f;
+                    if (col < c1 && k0 + kk < k)
+                        v = q ? (float)q[(int64_t)col * k + k0 + kk] : w[(int64_t)col * k + k0 + kk];
+                    Ws[kk * WST + nn] = v;
+                }
+                __syncthreads();
+                const int kend = min(KC, k - k0);
+                for (int kk = 0; kk < kend; ++kk) {
+                    const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm]);
+                    const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm + 4]);
+                    float wv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) wv[j] = Ws[kk * WST + tn + 16 * j];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            acc[r][j] = fmaf(a0[r], wv[j], acc[r][j]);
+                            acc[r + 4][j] = fmaf(a1[r], wv[j], acc[r + 4][j]);
+                        }
+                    }
+                }
+            }
+
+            if (EPI == EPI_STATS) {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    float tv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int col = n0 + tn + 16 * j;
+                        tv[j] = col < c1 ? fmaf(acc[r][j], scale[col] * kLog2e, bias[col] * kLog2e) : -INFINITY;
+                    }
+                    float tmax = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
+                    const bool better = tmax > st[r].best;
+                    if (better) {
+                        int jj = 3;
+#pragma unroll
+                        for (int j = 2; j >= 0; --j) jj = (tv[j] == tmax) ? j : jj;
+                        st[r].best = tmax;
+                        st[r].idx = n0 + tn + 16 * jj;
+                    }
+                    const bool shift = st[r].best != -INFINITY &&
+                                       (st[r].best > st[r].ref + 64.0f || st[r].best < st[r].ref - 64.0f);
+                    if (__any(shift)) {
+                        if (shift) {
+                            const float nr = st[r].best;
+                            st[r].sum *= __builtin_amdgcn_exp2f(st[r].ref - nr);
+                            st[r].ref = nr;
+                        }
+                        refzero = false;
+                    }
+                    float e = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) e += __builtin_amdgcn_exp2f(refzero ? tv[j] : tv[j] - st[r].ref);
+                    st[r].sum += e;
                 }
             } else {
-                for (int idx = tid; idx < BM * KC; idx += 256) {
-                    const int mm = idx / KC, kk = idx % KC;
-                    const int64_t row = m0 + mm;
-                    As[kk * AST + mm] = (row < m && k0 + kk < k) ? a[row * k + k0 + kk] : 0.0f;
-                }
-            }
-            for (int idx = tid; idx < BN * KC; idx += 256) {
-                const int nn = idx / KC, kk = idx % KC;
-                const int col = n0 + nn;
-                float v = 0.0f;
-                if (col < n && k0 + kk < k)
-                    v = q ? (float)q[(int64_t)col * k + k0 + kk] : w[(int64_t)col * k + k0 + kk];
-                Ws[kk * WST + nn] = v;
-            }
-            __syncthreads();
-            const int kend = min(KC, k - k0);
-            for (int kk = 0; kk < kend; ++kk) {
-                const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm]);
-                const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm + 4]);
-                float wv[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) wv[j] = Ws[kk * WST + tn + 16 * j];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
+                    const int col = n0 + tn + 16 * j;
+                    if (col >= c1) continue;
+                    const float sc = scale[col], bi = bias[col];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        acc[r][j] = fmaf(a0[r], wv[j], acc[r][j]);
-                        acc[r + 4][j] = fmaf(a1[r], wv[j], acc[r + 4][j]);
+                    for (int r = 0; r < 8; ++r) {
+                        if (!rvalid[r]) continue;
+                        float v;
+                        if (EPI == EPI_LOGITS)
+                            v = __fadd_rn(__fmul_rn(acc[r][j], sc), bi);
+                        else
+                            v = __builtin_amdgcn_exp2f(fmaf(acc[r][j], sc * kLog2e, bi * kLog2e) - rmax[r]) * rinv[r];
+                        out[rows[r] * n + col] = v;
                     }
                 }
             }
         }
 
         if (EPI == EPI_STATS) {
+            // the 16 threads of one tm are 16 consecutive lanes: butterfly over them.
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                float tv[4];
+                RowStat s = st[r];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int col = n0 + tn + 16 * j;
-                    tv[j] = col < n ? fmaf(acc[r][j], scale[col] * kLog2e, bias[col] * kLog2e) : -INFINITY;
+                for (int o = 1; o < 16; o <<= 1) {
+                    RowStat other;
+                    other.best = __shfl_xor(s.best, o, 64);
+                    other.sum = __shfl_xor(s.sum, o, 64);
+                    other.ref = __shfl_xor(s.ref, o, 64);
+                    other.idx = __shfl_xor(s.idx, o, 64);
+                    s = stat_merge(s, other);
                 }
-                float tmax = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
-                const bool better = tmax > st[r].best;
-                if (better) {
-                    int jj = 3;
-#pragma unroll
-                    for (int j = 2; j >= 0; --j) jj = (tv[j] == tmax) ? j : jj;
-                    st[r].best = tmax;
-                    st[r].idx = n0 + tn + 16 * jj;
+                if (tn == 0 && rvalid[r]) {
+                    p_best[(int64_t)chunk * m + rows[r]] = s.best;
+                    p_sum[(int64_t)chunk * m + rows[r]] = s.sum;
+                    p_idx[(int64_t)chunk * m + rows[r]] = s.idx;
                 }
-                const bool shift =
-                    st[r].best != -INFINITY && (st[r].best > st[r].ref + 64.0f || st[r].best < st[r].ref - 64.0f);
-                if (__any(shift)) {
-                    if (shift) {
-                        const float nr = st[r].best;
-                        st[r].sum *= __builtin_amdgcn_exp2f(st[r].ref - nr);
-                        st[r].ref = nr;
-                    }
-                    refzero = false;
-                }
-                float e = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) e += __builtin_amdgcn_exp2f(refzero ? tv[j] : tv[j] - st[r].ref);
-                st[r].sum += e;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = n0 + tn + 16 * j;
-                if (col >= n) continue;
-                const float sc = scale[col], bi = bias[col];
-#pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    const int64_t row = m0 + 8 * tm + r;
-                    if (row >= m) continue;
-                    float v;
-                    if (EPI == EPI_LOGITS)
-                        v = __fadd_rn(__fmul_rn(acc[r][j], sc), bi);
-                    else
-                        v = __builtin_amdgcn_exp2f(fmaf(acc[r][j], sc * kLog2e, bi * kLog2e) - rmax[r]) * rinv[r];
-                    out[row * n + col] = v;
-                }
-            }
-        }
-    }
-
-    if (EPI == EPI_STATS) {
-        // the 16 threads of one tm are 16 consecutive lanes: butterfly over them.
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            RowStat s = st[r];
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                RowStat other;
-                other.best = __shfl_xor(s.best, o, 64);
-                other.sum = __shfl_xor(s.sum, o, 64);
-                other.ref = __shfl_xor(s.ref, o, 64);
-                other.idx = __shfl_xor(s.idx, o, 64);
-                s = stat_merge(s, other);
-            }
-            const int64_t row = m0 + 8 * tm + r;
-            if (tn == 0 && row < m) {
-                p_best[(int64_t)chunk * m + row] = s.best;
-                p_sum[(int64_t)chunk * m + row] = s.sum;
-                p_idx[(int64_t)chunk * m + row] = s.idx;
             }
         }
     }
@@ -190,8 +221,9 @@ int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const
     if (m <= 0 || n <= 0) return PPOCR_OK;
     const int ntiles = (int)((n + BN - 1) / BN);
     dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
-    head_fma_kernel<EPI_LOGITS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, 1, out, nullptr,
-                                                      nullptr, nullptr, nullptr, nullptr, 0);
+    head_fma_kernel<EPI_LOGITS, false><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, BN, out,
+                                                             nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
+                                                             nullptr, 0u, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
@@ -203,8 +235,9 @@ int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const 
     if (m <= 0 || n <= 0) return PPOCR_OK;
     const int ntiles = (int)((n + BN - 1) / BN);
     dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
-    head_fma_kernel<EPI_PROBS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, 1, probs, row_max,
-                                                     row_inv, nullptr, nullptr, nullptr, 0);
+    head_fma_kernel<EPI_PROBS, false><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, BN, probs,
+                                                            row_max, row_inv, nullptr, nullptr, nullptr, 0, nullptr,
+                                                            nullptr, 0u, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
@@ -219,8 +252,38 @@ int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const 
     const int ntiles = (int)((n + BN - 1) / BN);
     const int tpc = (ntiles + nsplit - 1) / nsplit;
     dim3 grid(nsplit, (unsigned)((m + BM - 1) / BM));
-    head_fma_kernel<EPI_STATS><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, tpc, nullptr, nullptr,
-                                                     nullptr, p_best, p_sum, p_idx, line_len);
+    head_fma_kernel<EPI_STATS, false><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, tpc * BN,
+                                                            nullptr, nullptr, nullptr, p_best, p_sum, p_idx, line_len,
+                                                            nullptr, nullptr, 0u, 0);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+int launch_rescue_fma(int epi, const FmaWeights& fw, const float* a, int64_t m, int64_t n, int64_t k, int nsplit,
+                      int classes_per_chunk, float* out, const float* row_max, const float* row_inv, float* p_best,
+                      float* p_sum, int* p_idx, int64_t line_len, const Guard& guard, hipStream_t st) {
+    if (int e = check_fma_args(m, n, k)) return e;
+    if (line_len < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
+    if (m <= 0 || n <= 0) return PPOCR_OK;
+    if (!guard.header || !guard.rows) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: rescue without a guard list");
+    // the row count is on the device: a fixed number of row-block slots walk the list
+    const unsigned slots = (unsigned)std::min<int64_t>((m + BM - 1) / BM, kFmaRescueSlots);
+    int cpc = BN, chunks = (int)((n + BN - 1) / BN);
+    if (epi == EPI_STATS) {
+        if (nsplit < 1 || nsplit > 1024 || classes_per_chunk <= 0 || (int64_t)classes_per_chunk * nsplit < n)
+            return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad vocabulary chunks");
+        cpc = classes_per_chunk;
+        chunks = nsplit;
+    }
+    dim3 grid((unsigned)chunks, slots);
+    auto args = [&](auto kern) {
+        kern<<<grid, 256, 0, st>>>(fw.q, fw.w, fw.scale, fw.bias, a, m, (int)n, (int)k, cpc, out, row_max, row_inv,
+                                   p_best, p_sum, p_idx, line_len, guard.header, guard.rows, guard.epoch,
+                                   guard.capacity);
+    };
+    if (epi == EPI_LOGITS) args(head_fma_kernel<EPI_LOGITS, true>);
+    else if (epi == EPI_PROBS) args(head_fma_kernel<EPI_PROBS, true>);
+    else args(head_fma_kernel<EPI_STATS, true>);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

@@ -911,9 +911,20 @@ static int rows_nsplit(int64_t mblocks) {
 // outliers guards many rows) needs the whole GPU.
 constexpr int kRescueSlots = 128;
 
-// Configuration that recomputes the rows flagged by the precision guard of `cfg`
-// (-1: the configuration has no guard).
-static int rescue_cfg(int cfg) { return cfg == CFG_Q2 ? CFG_Q3 : -1; }
+// How the rows flagged by the precision guard of `cfg` are recomputed: an INT8 head's two
+// activation terms become three (exact products with int8 weights); an FP32 head's bf16x3
+// products, whose error floor is the two-plane split of the weight itself, are redone in
+// fp32 FMA.  Other configurations have no guard.
+constexpr int kRescueNone = -1, kRescueFma = -2;
+static int rescue_cfg(int cfg) { return cfg == CFG_Q2 ? CFG_Q3 : cfg == CFG_F3 ? kRescueFma : kRescueNone; }
+
+// The statistics pass of the two-term INT8 mode skips the reference shift of the softmax
+// sum (NOREF) when the head allows it, flagging also the rows whose logits could leave
+// [-kLogitBound, kLogitBound]; its limit is then the lower stats_amax_limit.
+static bool stats_noref_of(int cfg, const Guard& g) { return g.stats_noref && cfg == CFG_Q2; }
+static float stats_limit_of(int cfg, const Guard& g) {
+    return stats_noref_of(cfg, g) ? g.stats_amax_limit : g.amax_limit;
+}
 
 static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
                        int64_t n, int64_t k, const float* row_max, const float* row_inv, float* out,
@@ -929,13 +940,12 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     if (grid > 0x7fffffff) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
     const int vec = vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
-    const bool guarded = guard && guard->header && rcfg >= 0;
+    const bool guarded = guard && guard->header && rcfg != kRescueNone;
     // Probabilities are exp2(t - row_max) * row_inv with row_max and row_inv from the
     // statistics pass, so this pass must compute every t exactly as that pass did: the
     // same rows take three activation terms (that pass's limit, the lower one when it skips
     // the reference shift).  Logits need only the precision limit.
-    const float limit = !guarded ? 0.0f
-                        : (epi == 1 && guard->stats_noref) ? guard->stats_amax_limit : guard->amax_limit;
+    const float limit = !guarded ? 0.0f : epi == 1 ? stats_limit_of(cfg, *guard) : guard->amax_limit;
     if (guarded) {
         // a replay of this call (same epoch) must start from an empty list too
         guard_reset_kernel<<<1, 1, 0, st>>>(guard->header, guard->epoch);
@@ -953,6 +963,9 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
         return PPOCR_OK;
     });
     if (e || !guarded) return e;
+    if (rcfg == kRescueFma)
+        return launch_rescue_fma(epi == 0 ? EPI_LOGITS : EPI_PROBS, guard->fma, a, m, n, k, 0, 0, out, row_max, row_inv,
+                                 nullptr, nullptr, nullptr, 0, *guard, st);
     // rescue: the flagged rows again, one more activation term, every column
     const int slots = (int)std::min<int64_t>(mblocks, kRescueSlots);
     const int rgrid = grid_blocks(slots, nsplit);
@@ -1002,10 +1015,11 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
     const int vec = line_len > 0 ? -(int)line_len : vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
     // No reset launch: the list is emptied by its epoch (first use) and by the merge below.
-    const bool guarded = guard && guard->header && rcfg >= 0;
+    const bool guarded = guard && guard->header && rcfg != kRescueNone;
     // With the guard, rows whose logits could leave [-kLogitBound, kLogitBound] go to the
-    // rescue pass, so the main pass may skip the reference shift (NOREF).
-    const bool noref = guarded && guard->stats_noref;
+    // rescue pass, so the main pass may skip the reference shift (NOREF; built for the
+    // two-term INT8 mode).
+    const bool noref = guarded && stats_noref_of(cfg, *guard);
     int e = dispatch_cfg_g(cfg, tg.G, [&](auto CC, auto GG) -> int {
         constexpr int C = decltype(CC)::value, G = decltype(GG)::value;
         constexpr int MB = mb_of<C>();
@@ -1021,14 +1035,18 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
         }
         kern<<<grid, 64 * kStatsWaves, lds, st>>>(
             a, m, (int)k, vec, rec, tg.tiles, nsplit, tpc, (int)mblocks, p_best, p_sum, p_idx,
-            guarded ? (noref ? guard->stats_amax_limit : guard->amax_limit) : 0.0f,
+            guarded ? stats_limit_of(cfg, *guard) : 0.0f,
             guarded ? guard->header : nullptr, guarded ? guard->rows : nullptr, guarded ? guard->epoch : 0u,
             guarded ? guard->capacity : 0);
         PPOCR_HIP(hipGetLastError());
         return PPOCR_OK;
     });
     if (e) return e;
-    if (guarded) {
+    if (guarded && rcfg == kRescueFma) {
+        e = launch_rescue_fma(EPI_STATS, guard->fma, a, m, n, k, nsplit, tpc * 32, nullptr, nullptr, nullptr, p_best,
+                              p_sum, p_idx, line_len, *guard, st);
+        if (e) return e;
+    } else if (guarded) {
         // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
         // (with exact class indices)
         const int rrpb = stats_rows_per_block_mfma(rcfg, m);

@@ -34,6 +34,7 @@ enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4 };
 // shift of the softmax sum (stats_noref), and the rescue pass, which keeps it, takes the
 // other rows.
 constexpr float kLogitBound = 60.0f;
+struct FmaWeights;
 struct Guard {
     float amax_limit;
     unsigned long long* header;
@@ -42,6 +43,7 @@ struct Guard {
     unsigned epoch;
     float stats_amax_limit;
     bool stats_noref;
+    const FmaWeights& fma;  // the head's fp32 weights, for a rescue in fp32 FMA
 };
 
 // Supported group counts (k = 113..120 and k = 73..80, the PP-OCRv6 small and tiny heads).
@@ -50,15 +52,21 @@ bool mfma_supports_groups(int G);
 int launch_pack_int8(const float* w_t, int64_t n, int64_t k, int8_t* q, float* scales,
                      hipStream_t st);
 
-// Head preparation on the device (a head created from a model file): dst [cols][rows] =
-// src [rows][cols]; the guard limits of an INT8 head as bit patterns of non-negative
-// values (wmax float, w1 and bmax double; maxima taken with atomicMax, so the outputs must
-// start at 0); the MFMA tile records (rec zeroed beforehand; q for an INT8 head, w for an
-// FP32 head).
+// Head preparation on the device: dst [cols][rows] = src [rows][cols]; the quantities
+// behind the guard limits (largest |w|, largest L1 and L2 norm of a dequantised class row,
+// largest |bias|) as bit patterns of non-negative values (maxima taken with atomicMax, so
+// *out must start zeroed), from q and scales (INT8 head) or w (FP32 head); the MFMA tile
+// records (rec zeroed beforehand; q for an INT8 head, w for an FP32 head).
+struct HeadLimitBits {
+    unsigned long long w1;    // double
+    unsigned long long bmax;  // double
+    unsigned long long l2;    // double
+    unsigned wmax;            // float
+    unsigned pad;
+};
 int launch_transpose(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t st);
-int launch_head_limits(const int8_t* q, const float* scales, const float* bias, int64_t n, int64_t k,
-                       unsigned* wmax_bits, unsigned long long* w1_bits, unsigned long long* bmax_bits,
-                       hipStream_t st);
+int launch_head_limits(const int8_t* q, const float* w, const float* scales, const float* bias, int64_t n, int64_t k,
+                       HeadLimitBits* out, hipStream_t st);
 int launch_build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
                          const float* scale, const float* bias, uint8_t* rec, hipStream_t st);
 
@@ -97,6 +105,9 @@ int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const flo
                       int64_t n, int64_t k, const float* row_max, const float* row_inv, float* probs,
                       const Guard* guard, hipStream_t st);
 
+// Epilogues of the projection kernels: logits, probabilities, per-chunk softmax statistics.
+enum Epi : int { EPI_LOGITS = 0, EPI_PROBS = 1, EPI_STATS = 2 };
+
 // fp32 vector FMA path over the packed int8 weights (q != null) or fp32 weights (w != null).
 int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                       const float* a, int64_t m, int64_t n, int64_t k, float* out, hipStream_t st);
@@ -107,6 +118,20 @@ int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const 
 int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                      const float* a, int64_t m, int64_t n, int64_t k, const float* row_max,
                      const float* row_inv, float* probs, hipStream_t st);
+// The fp32 weights of the FMA path: q (INT8 head) or w (FP32 head), scale, bias.
+struct FmaWeights {
+    const int8_t* q;
+    const float* w;
+    const float* scale;
+    const float* bias;
+};
+// Rescue in fp32 FMA of the rows on a guard list (Guard) of an MFMA pass, with the same
+// epilogue: logits or probabilities of every class (epi EPI_LOGITS / EPI_PROBS), or the
+// statistics partials of the MFMA pass's vocabulary chunks (EPI_STATS: nsplit chunks of
+// classes_per_chunk classes), overwriting what that pass wrote for those rows.
+int launch_rescue_fma(int epi, const FmaWeights& fw, const float* a, int64_t m, int64_t n, int64_t k, int nsplit,
+                      int classes_per_chunk, float* out, const float* row_max, const float* row_inv, float* p_best,
+                      float* p_sum, int* p_idx, int64_t line_len, const Guard& guard, hipStream_t st);
 
 // Merge the per-chunk partials of each row: argmax index, max probability, and (when
 // row_max/row_inv are non-null) the row's log2-domain maximum and 1/sum for a probs pass.

@@ -35,46 +35,74 @@ int launch_transpose(const float* src, int64_t rows, int64_t cols, float* dst, h
     return PPOCR_OK;
 }
 
-// Per class row j of an INT8 head (one wave per row): the largest |dequantised weight|
-// (float, (float)max|q| * scale, as the host computes it), the L1 norm of the dequantised
-// row in double, and |bias| in double (NaN ignored, as std::max ignores it on the host).
-// Maxima of non-negative values are taken on their bit patterns, which order the same way.
-__global__ __launch_bounds__(256) void head_limits_kernel(const int8_t* __restrict__ q, const float* __restrict__ scales,
+// Per class row j (one wave per row), for the guard limits of the split-activation modes:
+// the largest |dequantised weight| (float; (float)max|q| * scale for an INT8 head), the L1
+// and L2 norms of the dequantised row and |bias|, in double (NaN ignored).  An INT8 row's
+// sums are exact integers scaled once; an FP32 row's are summed in a fixed order (lane
+// strides, then xor shuffles), so every call gives the same bits.  Maxima of non-negative
+// values are taken on their bit patterns, which order the same way.
+__global__ __launch_bounds__(256) void head_limits_kernel(const int8_t* __restrict__ q, const float* __restrict__ w,
+                                                          const float* __restrict__ scales,
                                                           const float* __restrict__ bias, int64_t n, int64_t k,
-                                                          unsigned* wmax_bits, unsigned long long* w1_bits,
-                                                          unsigned long long* bmax_bits) {
+                                                          HeadLimitBits* __restrict__ out) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;
-    int qm = 0, l1 = 0;
-    for (int64_t i = lane; i < k; i += 64) {
-        const int v = abs((int)q[row * k + i]);
-        qm = max(qm, v);
-        l1 += v;
-    }
+    float wm;
+    double w1, l2;
+    if (q) {
+        int qm = 0, s1 = 0, s2 = 0;
+        for (int64_t i = lane; i < k; i += 64) {
+            const int v = abs((int)q[row * k + i]);
+            qm = max(qm, v);
+            s1 += v;
+            s2 += v * v;
+        }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        qm = max(qm, __shfl_xor(qm, o, 64));
-        l1 += __shfl_xor(l1, o, 64);
+        for (int o = 32; o >= 1; o >>= 1) {
+            qm = max(qm, __shfl_xor(qm, o, 64));
+            s1 += __shfl_xor(s1, o, 64);
+            s2 += __shfl_xor(s2, o, 64);
+        }
+        wm = __fmul_rn((float)qm, scales[row]);
+        w1 = (double)s1 * (double)scales[row];
+        l2 = __dsqrt_rn((double)s2) * (double)scales[row];
+    } else {
+        float m = 0.0f;
+        double s1 = 0.0, s2 = 0.0;
+        for (int64_t i = lane; i < k; i += 64) {
+            const float v = fabsf(w[row * k + i]);
+            m = fmaxf(m, v);
+            s1 += (double)v;
+            s2 = fma((double)v, (double)v, s2);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            m = fmaxf(m, __shfl_xor(m, o, 64));
+            s1 += __shfl_xor(s1, o, 64);
+            s2 += __shfl_xor(s2, o, 64);
+        }
+        wm = m;
+        w1 = s1;
+        l2 = __dsqrt_rn(s2);
     }
     if (lane == 0) {
-        const float wm = __fmul_rn((float)qm, scales[row]);
-        if (wm == wm) atomicMax(wmax_bits, __float_as_uint(wm));
-        const double w1 = (double)l1 * (double)scales[row];
-        if (w1 == w1) atomicMax(w1_bits, (unsigned long long)__double_as_longlong(w1));
+        if (wm == wm) atomicMax(&out->wmax, __float_as_uint(wm));
+        if (w1 == w1) atomicMax(&out->w1, (unsigned long long)__double_as_longlong(w1));
+        if (l2 == l2) atomicMax(&out->l2, (unsigned long long)__double_as_longlong(l2));
         if (bias) {
             const double b = fabs((double)bias[row]);
-            if (b == b) atomicMax(bmax_bits, (unsigned long long)__double_as_longlong(b));
+            if (b == b) atomicMax(&out->bmax, (unsigned long long)__double_as_longlong(b));
         }
     }
 }
 
-int launch_head_limits(const int8_t* q, const float* scales, const float* bias, int64_t n, int64_t k,
-                       unsigned* wmax_bits, unsigned long long* w1_bits, unsigned long long* bmax_bits,
-                       hipStream_t st) {
+int launch_head_limits(const int8_t* q, const float* w, const float* scales, const float* bias, int64_t n, int64_t k,
+                       HeadLimitBits* out, hipStream_t st) {
     if (n <= 0) return PPOCR_OK;
     if ((n + 3) / 4 > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: too many classes");
-    head_limits_kernel<<<(unsigned)((n + 3) / 4), 256, 0, st>>>(q, scales, bias, n, k, wmax_bits, w1_bits, bmax_bits);
+    if (!q && !w) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: no weights");
+    head_limits_kernel<<<(unsigned)((n + 3) / 4), 256, 0, st>>>(q, w, scales, bias, n, k, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

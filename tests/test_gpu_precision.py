@@ -1,0 +1,205 @@
+"""GPU parity where the bars bite: the FP32 head at the 64-line batch size (m = 7680),
+peaked outputs (one class near probability 1, as the real model gives), rows sized
+around the precision guards' limits, and the whole dense 256-line batch.
+
+Probabilities and maximum probabilities are held to 1e-4 absolute and 1e-4 relative
+(rows whose logits exceed 10 in magnitude get a proportionally wider relative bar for the
+fp32 rounding both sides carry); logits to 1e-4; argmax and CTC sequences identical except
+at top-2 logit gaps below 1e-4, which are printed."""
+import numpy as np
+import pytest
+
+from gpu_common import (assert_close_rel, check_argmax, f64_logits_f32, f64_logits_q, oracle_head_f32, peaked_rows,
+                        rel_scale, split_lines, top2_gap)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def head(orc):
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    q, s = orc.pack_int8(w_t)
+    return {"w_t": w_t, "bias": bias, "q": q, "s": s, "wd": q.astype(np.float64) * s.astype(np.float64)[:, None]}
+
+
+def _int8_limit(q, s):
+    """The INT8 head's precision limit on max|a| (two activation terms), computed as the
+    library does: min(16 / max|w|, 8 / max_c ||w_c||_2) on the dequantised weight."""
+    qa = np.abs(q.astype(np.int64))
+    wmax = float(np.max((qa.max(axis=1).astype(np.float32) * s).astype(np.float32)))
+    l2 = float(np.max(np.sqrt((qa * qa).sum(axis=1).astype(np.float64)) * s.astype(np.float64)))
+    return min(16.0 / wmax, 8.0 / l2)
+
+
+def _f32_limit(w_t):
+    w = np.abs(w_t.astype(np.float64))
+    return min(16.0 / float(np.abs(w_t).max()), 4.0 / float(np.sqrt((w * w).sum(axis=1)).max()))
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+def test_fp32_head_m7680_logits(orc, rh, mode):
+    """The FP32 head at 64 lines x T=120 (m = 7680), every row's logits from the GPU, sampled
+    rows (the last row block among them) against matmul_transposed_b."""
+    from ppocr_rechead import workloads as wl
+    wk = wl.make("fp32_64")
+    a, w_t, bias = wk["a"], wk["w_t"], wk["bias"]
+    m = a.shape[0]
+    assert m == 7680
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    print(f"fp32 head m={m} mode={mode} logits", flush=True)
+    got = head.logits(a, mode)
+    head.close()
+    rng = np.random.default_rng(31)
+    sample = np.unique(np.concatenate([rng.choice(m - 128, 256, replace=False), np.arange(m - 128, m)]))
+    ref = orc.matmul_transposed_b(a[sample], w_t, bias, partition_threads=1)
+    err = np.abs(got[sample] - ref).max()
+    print(f"  max|logits gpu-oracle| = {err:.3e} over {sample.size} rows")
+    assert err < TOL
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+def test_fp32_head_m7680_decode(orc, rh, mode):
+    """The fused head (statistics pass, chunk merge, CTC) with the FP32 weight at m = 7680:
+    every row's argmax and maximum probability and every line's sequence and score against
+    the oracle's FP32 head (matmul_transposed_b, softmax, find_argmax, collapse)."""
+    from ppocr_rechead import workloads as wl
+    wk = wl.make("fp32_64")
+    a, w_t, bias, off = wk["a"], wk["w_t"], wk["bias"], wk["line_off"]
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    print(f"fp32 head m={a.shape[0]} mode={mode} decode", flush=True)
+    got = head.decode(a, off, mode)
+    head.close()
+    ref = oracle_head_f32(orc, a, w_t, bias, off)
+    mis = np.nonzero(got["idx"] != ref["idx"])[0]
+    gap = np.full(a.shape[0], np.inf)
+    if mis.size:
+        gap[mis] = top2_gap(f64_logits_f32(a[mis], w_t, bias))
+    exempt = check_argmax(got["idx"], ref["idx"], gap, label=f"fp32 m7680 mode {mode}")
+    assert_close_rel(got["maxprob"], ref["maxprob"], f"fp32 m7680 maxprob mode {mode}")
+    for b in range(len(off) - 1):
+        if np.any((exempt >= off[b]) & (exempt < off[b + 1])):
+            continue
+        assert np.array_equal(got["seqs"][b], ref["seqs"][b]), b
+        assert abs(float(got["score"][b]) - float(ref["score"][b])) <= TOL * max(1e-3, abs(float(ref["score"][b])))
+
+
+@pytest.mark.parametrize("mode", [2, 3])
+def test_peaked_outputs_decode_and_probs(orc, rh, head, mode):
+    """Rows built so that one class dominates (maximum probability ~0.5 .. 0.99, blank and
+    repeated classes among the targets, as in real CTC output): decode and probabilities
+    against the oracle.  Here the 1e-4 bar on the maximum probability is what a lost or
+    doubled term of the softmax sum would break."""
+    rng = np.random.default_rng(32)
+    lens = [120, 80, 37, 1, 120]
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    m = int(off[-1])
+    # a text-like target sequence: runs of the same class separated by blanks
+    targets = np.zeros(m, np.int64)
+    t = 0
+    while t < m:
+        run = int(rng.integers(1, 5))
+        targets[t:t + run] = 0 if rng.random() < 0.4 else int(rng.integers(1, 18710))
+        t += run
+    alpha = rng.uniform(15.0, 30.0, m)
+    a = peaked_rows(head["wd"], targets, alpha, rng)
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    print(f"peaked rows m={m} mode={mode}", flush=True)
+    got = h.decode(a, off, mode)
+    probs = h.probs(a[:200], mode)
+    h.close()
+    ref = orc.rechead_lines(a, off, head["q"], head["s"], head["bias"])
+    lg = f64_logits_q(a, head["q"], head["s"], head["bias"])
+    print(f"  maxprob range {ref['maxprob'].min():.3f} .. {ref['maxprob'].max():.4f}, "
+          f"median {np.median(ref['maxprob']):.3f}; targets hit {np.mean(ref['idx'] == targets):.3f}")
+    assert np.median(ref["maxprob"]) > 0.8
+    exempt = check_argmax(got["idx"], ref["idx"], top2_gap(lg), label=f"peaked mode {mode}")
+    assert_close_rel(got["maxprob"], ref["maxprob"], f"peaked maxprob mode {mode}", row_scale=rel_scale(lg))
+    for b in range(len(lens)):
+        if np.any((exempt >= off[b]) & (exempt < off[b + 1])):
+            continue
+        assert np.array_equal(got["seqs"][b], ref["seqs"][b]), b
+        assert abs(float(got["score"][b]) - float(ref["score"][b])) <= TOL * max(1e-3, abs(float(ref["score"][b])))
+    refp = orc.rechead_lines(a[:200], split_lines(200, 50), head["q"], head["s"], head["bias"], want_probs=True)
+    assert_close_rel(probs, refp["probs"], f"peaked probs mode {mode}", row_scale=rel_scale(lg[:200]))
+
+
+def test_int8_logits_around_the_precision_limit(orc, rh, head):
+    """BF16X2 logits of rows whose max|a| is 0.5 .. 0.99 of the precision limit (two
+    activation terms) and 1.01 .. 3 of it (recomputed with three) against the oracle."""
+    lim = _int8_limit(head["q"], head["s"])
+    rng = np.random.default_rng(33)
+    fr = np.concatenate([np.linspace(0.5, 0.99, 96), np.linspace(1.01, 3.0, 32)])
+    a = rng.standard_normal((fr.size, 120)).astype(np.float32)
+    a = (a / np.abs(a).max(axis=1, keepdims=True) * (fr * lim)[:, None]).astype(np.float32)
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    print(f"int8 logits around the limit {lim:.3f}", flush=True)
+    got = h.logits(a, 2)
+    idx, mp = h.argmax(a, 2)
+    h.close()
+    ref = orc.matmul_quantized_b(a, head["q"], head["s"], head["bias"])
+    err = np.abs(got - ref).max(axis=1)
+    print(f"  max|logits diff| under the limit {err[:96].max():.2e}, over it {err[96:].max():.2e}")
+    assert err.max() < TOL
+    r = orc.rechead_lines(a, split_lines(a.shape[0], 32), head["q"], head["s"], head["bias"])
+    check_argmax(idx, r["idx"], top2_gap(f64_logits_q(a, head["q"], head["s"], head["bias"])), label="int8 limit")
+    assert_close_rel(mp, r["maxprob"], "int8 limit maxprob")
+
+
+def test_fp32_head_precision_guard(orc, rh):
+    """BF16X3 on an FP32 head: rows of max|a| 0.5 .. 0.99 of its precision limit stay on the
+    MFMA path, rows above it (to x50 of an N(0,1) row) are recomputed in fp32 FMA.  Logits,
+    the fused argmax and the probabilities against the oracle."""
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    lim = _f32_limit(w_t)
+    rng = np.random.default_rng(34)
+    fr = np.concatenate([np.linspace(0.5, 0.99, 64), np.linspace(1.01, 3.0, 32)])
+    a = rng.standard_normal((fr.size, 120)).astype(np.float32)
+    a = (a / np.abs(a).max(axis=1, keepdims=True) * (fr * lim)[:, None]).astype(np.float32)
+    big = rng.standard_normal((32, 120)).astype(np.float32) * np.float32(50.0)
+    a = np.concatenate([a, big]).astype(np.float32)
+    head = rh.RecHead(w_t=w_t, bias=bias)
+    print(f"fp32 head guard, limit {lim:.3f}", flush=True)
+    got = head.logits(a, 3)
+    idx, mp = head.argmax(a, 3)
+    probs = head.probs(a, 3)
+    head.close()
+    ref = oracle_head_f32(orc, a, w_t, bias, np.array([0, a.shape[0]], np.int64), want_probs=True)
+    lg = f64_logits_f32(a, w_t, bias)
+    tol = 1e-4 + 1e-5 * np.abs(ref["logits"])  # f32 rounding of |logits| ~ 1e2 alone is ~1e-5
+    err = np.abs(got - ref["logits"])
+    print(f"  max|logits diff|: under {err[:64].max():.2e}, over {err[64:96].max():.2e}, x50 {err[96:].max():.2e}")
+    assert np.all(err <= tol)
+    check_argmax(idx, ref["idx"], top2_gap(lg), label="fp32 guard")
+    assert_close_rel(mp, ref["maxprob"], "fp32 guard maxprob", row_scale=rel_scale(lg))
+    assert_close_rel(probs, ref["probs"], "fp32 guard probs", row_scale=rel_scale(lg))
+
+
+def test_dense_256_whole_batch(orc, rh, head):
+    """The fused decode of the dense 256-line batch (m = 30720) against the oracle on every
+    row and every line."""
+    from ppocr_rechead import workloads as wl
+    a = wl.activations("dense_256")
+    off = wl.line_offsets(wl.lines_for("dense_256"))
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    print("dense_256 whole batch decode", flush=True)
+    got = h.decode(a, off, 2)
+    h.close()
+    ref = orc.rechead_lines(a, off, head["q"], head["s"], head["bias"])
+    mis = np.nonzero(got["idx"] != ref["idx"])[0]
+    gap = np.full(a.shape[0], np.inf)
+    if mis.size:
+        gap[mis] = top2_gap(f64_logits_q(a[mis], head["q"], head["s"], head["bias"]))
+    exempt = check_argmax(got["idx"], ref["idx"], gap, label="dense_256 all rows")
+    assert_close_rel(got["maxprob"], ref["maxprob"], "dense_256 maxprob")
+    same = 0
+    for b in range(len(off) - 1):
+        if np.any((exempt >= off[b]) & (exempt < off[b + 1])):
+            continue
+        assert np.array_equal(got["seqs"][b], ref["seqs"][b]), b
+        assert abs(float(got["score"][b]) - float(ref["score"][b])) <= TOL * max(1e-3, abs(float(ref["score"][b])))
+        same += 1
+    print(f"  {same} of {len(off) - 1} lines identical (the rest hold near-tie rows)")

@@ -6,7 +6,7 @@ without an MFMA path."""
 import numpy as np
 import pytest
 
-from gpu_common import check_argmax, f64_logits_q, top2_gap
+from gpu_common import assert_close_rel, check_argmax, f64_logits_q, top2_gap
 
 pytestmark = pytest.mark.gpu
 
@@ -90,7 +90,7 @@ def test_head_found_in_the_model_graph(orc, rh, tmp_path):
     the same head as naming its tensors; the whole-head decode agrees with the oracle."""
     import json
     from safetensors.numpy import save_file
-    from gpu_common import check_argmax, f64_logits_q, top2_gap
+    from gpu_common import assert_close_rel, check_argmax, f64_logits_q, top2_gap
     from ppocr_rechead import workloads as wl
     w_t, bias = wl.weights()
     graph = {"inputs": ["x"], "outputs": ["probs"], "nodes": [
@@ -112,7 +112,7 @@ def test_head_found_in_the_model_graph(orc, rh, tmp_path):
     q, s = orc.pack_int8(w_t)
     ref = orc.rechead_lines(a, off, q, s, bias)
     check_argmax(gm["idx"], ref["idx"], top2_gap(f64_logits_q(a, q, s, bias)), label="model graph head")
-    assert np.abs(gm["maxprob"] - ref["maxprob"]).max() < 1e-4
+    assert_close_rel(gm["maxprob"], ref["maxprob"], "model-file head maxprob")
     hm.close()
     hs.close()
 
@@ -125,7 +125,7 @@ def test_head_found_in_a_pp_ocr_v6_style_graph(orc, rh, tmp_path):
     names on the transposed rows, bit for bit, within the bars against the oracle."""
     import json
     from safetensors.numpy import save_file
-    from gpu_common import check_argmax, f64_logits_q, top2_gap
+    from gpu_common import assert_close_rel, check_argmax, f64_logits_q, top2_gap
     from ppocr_rechead import workloads as wl
     w_t, bias = wl.weights()
     graph = {"inputs": ["x"], "outputs": ["fetch_name_0"], "nodes": [
@@ -159,6 +159,6 @@ def test_head_found_in_a_pp_ocr_v6_style_graph(orc, rh, tmp_path):
     q, s = orc.pack_int8(w_t)
     ref = orc.rechead_lines(a, off, q, s, bias)
     check_argmax(gm["idx"], ref["idx"], top2_gap(f64_logits_q(a, q, s, bias)), label="v6-style graph head")
-    assert np.abs(gm["maxprob"] - ref["maxprob"]).max() < 1e-4
+    assert_close_rel(gm["maxprob"], ref["maxprob"], "model-file head maxprob")
     hm.close()
     hs.close()
