@@ -199,6 +199,18 @@ int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const 
                         int64_t* d_seq_len, float* d_score, void* d_workspace,
                         size_t workspace_bytes, void* stream);
 
+/* ppocr_rh_decode_dev without a workspace and without any device allocation.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Scratch comes from a fixed 32 MiB device array per GPU, held until the process ends,
+ * which covers m up to 245760 rows of the 18710-class head (PPOCR_ERR_INVALID_ARG beyond
+ * what it holds).  All calls on one GPU share that array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller.  The first
+ * call on a device takes the array's address and clears its list header on `stream`. */
+int ppocr_rh_decode_dev_noalloc(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off,
+                                int64_t lines, int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq,
+                                int64_t* d_seq_len, float* d_score, void* stream);
+
 /* The whole head entered one node earlier, at the neck's Transpose.8 (perm [0,2,1]:
  * Model::forward's Transpose, src/engine/model.rs:1325-1342, x.into_permute then a
  * contiguous copy, src/tensor.rs:621-633): x [lines][k][steps] is the neck's output,

@@ -581,6 +581,40 @@ struct Workspace {
     }
 };
 
+// ---------------------------------------------------------------- allocation-free scratch
+// The scratch of ppocr_rh_decode_dev_noalloc: a file-scope device array standing in for
+// the workspace, one per GPU the library runs on, held until the process ends.  In host
+// code `scratch` names a host-side stand-in, not device memory: its device address is
+// taken once per device with hipGetSymbolAddress (with that device current) and only that
+// address is ever passed to kernels.  Every call on a GPU shares its array, so calls that
+// overlap on one GPU race; what a call needs cleared (the guard list's header) is told
+// apart from what a previous call left by the call's epoch.
+constexpr size_t kNoAllocScratchBytes = 32u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kMaxDevices] = {};
+
+// Device address of this device's scratch (`device` current); the first call on a device
+// takes the address and clears the guard header at its start (a fill kernel on `st`, no
+// memset node, so a captured first call replays correctly).
+int scratch_of(int device, hipStream_t st, uint8_t** out) {
+    if (device < 0 || device >= kMaxDevices)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: device " + std::to_string(device) +
+                                               " beyond the allocation-free scratch table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[device]) {
+        void* p = nullptr;
+        PPOCR_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: no device address for the scratch array");
+        if (int e = launch_guard_clear(static_cast<unsigned long long*>(p), st)) return e;
+        g_scratch[device] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch[device];
+    return PPOCR_OK;
+}
+
 int check_m(int64_t m, const char* op) {
     if (m < 0) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": negative row count");
     if (m > (1LL << 31)) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": too many rows");
@@ -937,9 +971,12 @@ int ppocr_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* li
     return hc.copy_out({seq, seq_len, score});
 }
 
-int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off, int64_t lines,
-                        int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq, int64_t* d_seq_len,
-                        float* d_score, void* d_workspace, size_t workspace_bytes, void* stream) {
+// ppocr_rh_decode_dev and its allocation-free variant (noalloc: the device's scratch array
+// instead of a caller workspace or a stream-ordered allocation).
+static int decode_dev_common(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off,
+                             int64_t lines, int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq,
+                             int64_t* d_seq_len, float* d_score, void* d_workspace, size_t workspace_bytes,
+                             void* stream, bool noalloc) {
     if (int e = check_head(h, "RecHeadHip")) return e;
     if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
     if (int e = check_m(m, "RecHeadHip")) return e;
@@ -948,14 +985,39 @@ int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const 
     if (lines == 0) return PPOCR_OK;
     if (!d_line_off || !d_seq_len || !d_score) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: null pointer");
     if (m > 0 && (!d_a || !d_seq)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    const size_t need = m > 0 ? ws_layout(m, nsplit_for(h, m, cfg)).total : 0;
+    if (noalloc && need > kNoAllocScratchBytes)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: " + std::to_string(m) + " rows need " + std::to_string(need) +
+                                               " bytes of scratch, more than the " +
+                                               std::to_string(kNoAllocScratchBytes) +
+                                               " of the allocation-free entry point; use ppocr_rh_decode_dev");
     DeviceGuard dg(h->device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: hipSetDevice failed");
     hipStream_t st = (hipStream_t)stream;
     const CtcOut ctc{d_line_off, lines, 0, d_seq, d_seq_len, d_score};
     if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
-    const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
+    if (noalloc) {
+        uint8_t* ws = nullptr;
+        if (int e = scratch_of(h->device, st, &ws)) return e;
+        return run_stats(h, cfg, d_a, m, d_idx, d_maxprob, nullptr, nullptr, ws, st, &ctc);
+    }
     Workspace ws;
-    if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;
+    if (int e = ws.get(d_workspace, workspace_bytes, need, st, "RecHeadHip")) return e;
     return run_stats(h, cfg, d_a, m, d_idx, d_maxprob, nullptr, nullptr, ws.p, st, &ctc);
+}
+
+int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off, int64_t lines,
+                        int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq, int64_t* d_seq_len,
+                        float* d_score, void* d_workspace, size_t workspace_bytes, void* stream) {
+    return decode_dev_common(h, d_a, m, d_line_off, lines, mode, d_idx, d_maxprob, d_seq, d_seq_len, d_score,
+                             d_workspace, workspace_bytes, stream, false);
+}
+
+int ppocr_rh_decode_dev_noalloc(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off,
+                                int64_t lines, int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq,
+                                int64_t* d_seq_len, float* d_score, void* stream) {
+    return decode_dev_common(h, d_a, m, d_line_off, lines, mode, d_idx, d_maxprob, d_seq, d_seq_len, d_score,
+                             nullptr, 0, stream, true);
 }
 
 int ppocr_rh_decode(const ppocr_rh_t* h, const float* a, const int64_t* line_off, int64_t lines, int mode,

@@ -57,6 +57,7 @@ SIGNATURES = {
     "ppocr_ctc_greedy_dev": (_int, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp]),
     "ppocr_rh_decode": (_int, [_vp, _vp, _vp, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "ppocr_rh_decode_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ppocr_rh_decode_dev_noalloc": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppocr_rh_decode_nct": (_int, [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "ppocr_rh_decode_nct_dev": (_int, [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
