@@ -170,7 +170,10 @@ int ppocr_rh_argmax_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mo
  * idx (the previous index starts as blank, and is updated on blanks too).  Emitted
  * indices of line i are written to seq[line_off[i] ...], their count to seq_len[i] and
  * score[i] = (f32 sum of the emitted maxprob, in order) / count, 0 when none.  The
- * reference's blank is 0. */
+ * reference's blank is 0.  The host form rejects offsets that do not start at 0 or go
+ * backwards; the `_dev` form reads them on the device and clamps them instead: every line
+ * is cut to [0, line_off[lines]] (idx, maxprob and seq must hold line_off[lines] steps), and
+ * a line whose end precedes its start is empty. */
 int ppocr_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* line_off,
                      int64_t lines, int32_t blank, int32_t* seq, int64_t* seq_len, float* score);
 int ppocr_ctc_greedy_dev(const int32_t* d_idx, const float* d_maxprob, const int64_t* d_line_off,

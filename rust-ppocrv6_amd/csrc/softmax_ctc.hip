@@ -252,7 +252,9 @@ __device__ __forceinline__ float ordered_lane_sum(float sum, float x) {
 // One wavefront per text line.  Steps are taken 64 at a time; the emit mask is a ballot,
 // emitted indices are compacted by prefix popcount, and the score is summed in step order
 // (every lane runs the same sequential sum over the emitting lanes' values, read lane by
-// lane, ordered_lane_sum).
+// lane, ordered_lane_sum).  The offsets live on the device and are not trusted: each line
+// is clamped into [0, line_off[lines]] (the step count the arrays hold) and a line whose end
+// precedes its start is empty, as merge_ctc_kernel does.
 __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restrict__ idx,
                                                          const float* __restrict__ val,
                                                          const int64_t* __restrict__ line_off, int64_t lines,
@@ -261,7 +263,9 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
     const int lane = threadIdx.x & 63;
     const int64_t line = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (line >= lines) return;
-    const int64_t t0 = line_off[line], t1 = line_off[line + 1];
+    const int64_t total = max(line_off[lines], (int64_t)0);
+    const int64_t t0 = min(max(line_off[line], (int64_t)0), total);
+    const int64_t t1 = min(max(line_off[line + 1], t0), total);
     int64_t cnt = 0;
     float sum = -0.0f;
     for (int64_t base = t0; base < t1; base += 64) {

@@ -80,6 +80,29 @@ class QuantizedWeight:
         return self.data.size + 4 * self.scales.size
 
 
+REC_HEAD_BACKENDS = ("cpu", "hip")
+
+
+class OcrEngineConfig:
+    """The recognition-head fields of OcrEngineConfig (src/pipeline.rs:38-40): the reference's
+    INT8 switch `quantize_rec_head` (default False, bit-identical FP32 execution), unchanged,
+    and where the head runs, `rec_head_backend`: "cpu" (the reference's own operators) or
+    "hip" (this library on HIP device `rec_head_device`)."""
+
+    def __init__(self, quantize_rec_head=False, rec_head_backend="cpu", rec_head_device=0):
+        if rec_head_backend not in REC_HEAD_BACKENDS:
+            raise OcrError("ModelError", f"unknown rec_head_backend {rec_head_backend!r} "
+                                         f"(expected one of {', '.join(REC_HEAD_BACKENDS)})")
+        self.quantize_rec_head = bool(quantize_rec_head)
+        self.rec_head_backend = rec_head_backend
+        self.rec_head_device = int(rec_head_device)
+
+    def enable_rec_quantization(self):
+        """OcrEngine::enable_rec_quantization (src/pipeline.rs:267-270): INT8 from now on; a
+        head built for this configuration afterwards is the INT8 one."""
+        self.quantize_rec_head = True
+
+
 class RecHead:
     """The head weight resident in HBM: what Model keeps for MatMul.12 plus its folded bias.
 
@@ -130,6 +153,16 @@ class RecHead:
         GPU from the file's tensors (from_safetensors)."""
         names = find_rec_head(path)
         return cls.from_safetensors(path, names["weight"], names["bias"], quantize=quantize, device=device)
+
+    @classmethod
+    def for_config(cls, config, rec_path):
+        """The head an engine with `config` uses for the recognition model at `rec_path`
+        (OcrEngine::with_config, src/pipeline.rs:195-199): None for the "cpu" backend; for
+        "hip", the INT8 head when quantize_rec_head is set (the packing of
+        Model::quantize_matmul_weights) and the FP32 head otherwise."""
+        if config.rec_head_backend == "cpu":
+            return None
+        return cls.from_model(rec_path, quantize=config.quantize_rec_head, device=config.rec_head_device)
 
     def close(self):
         if self._h:
@@ -319,12 +352,21 @@ class CtcDecoder:
 
     @classmethod
     def from_file(cls, dict_path):
-        """vocab = ["blank"] + dictionary lines + [" "] (src/postprocess/ctc.rs:12-30)."""
+        """vocab = ["blank"] + dictionary lines + [" "] (src/postprocess/ctc.rs:12-30).
+
+        Lines as BufRead::lines gives them: split on '\n' only (a '\r' inside a line stays
+        in it), no empty line after a final '\n', then trailing '\r' and '\n' trimmed.
+        Text that is not UTF-8 is a ModelError ("Dict read error")."""
         try:
-            with open(dict_path, "r", encoding="utf-8") as f:
-                lines = f.read().split("\n")
+            with open(dict_path, "rb") as f:
+                data = f.read()
         except OSError as e:
             raise OcrError("ModelError", f"Failed to open dict file: {e}")
+        try:
+            text = data.decode("utf-8")
+        except UnicodeDecodeError as e:
+            raise OcrError("ModelError", f"Dict read error: {e}")
+        lines = text.split("\n")
         if lines and lines[-1] == "":
             lines = lines[:-1]
         vocab = ["blank"] + [ln.rstrip("\r\n") for ln in lines] + [" "]

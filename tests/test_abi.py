@@ -99,6 +99,41 @@ def test_dictionary_loading(rh, tmp_path):
         assert rh.CtcDecoder.from_file("/root/reference/models/ppocrv6_tiny_keys.txt").vocab_size() == 6906
 
 
+def test_dictionary_lines_split_on_newline_only(rh, tmp_path):
+    """BufRead::lines splits on '\n' alone and trim_end_matches drops trailing '\r' / '\n'
+    (src/postprocess/ctc.rs:20-23): a lone '\r' inside an entry stays in it, so later class
+    indices do not shift; invalid UTF-8 is a ModelError; a missing final newline or an
+    empty file changes nothing else."""
+    p = tmp_path / "keys.txt"
+    p.write_bytes("x\ry\nb\r\r\nc".encode("utf-8"))
+    assert rh.CtcDecoder.from_file(str(p)).vocab == ["blank", "x\ry", "b", "c", " "]
+    p.write_bytes(b"")
+    assert rh.CtcDecoder.from_file(str(p)).vocab == ["blank", " "]
+    p.write_bytes(b"\n\n")
+    assert rh.CtcDecoder.from_file(str(p)).vocab == ["blank", "", "", " "]
+    p.write_bytes(b"a\n\xff\xfe\n")
+    with pytest.raises(rh.OcrError) as e:
+        rh.CtcDecoder.from_file(str(p))
+    assert e.value.op == "ModelError" and "Dict read error" in str(e.value)
+    with pytest.raises(rh.OcrError) as e:
+        rh.CtcDecoder.from_file(str(tmp_path / "missing.txt"))
+    assert e.value.op == "ModelError" and "Failed to open dict file" in str(e.value)
+
+
+def test_engine_config_backend_selector(rh):
+    """OcrEngineConfig keeps the reference's quantize_rec_head default (False) and adds the
+    backend selector; an unknown backend is a ModelError, and the CPU backend builds no
+    head (nothing touches a GPU)."""
+    cfg = rh.OcrEngineConfig()
+    assert cfg.quantize_rec_head is False and cfg.rec_head_backend == "cpu"
+    assert rh.RecHead.for_config(cfg, "/nonexistent/model.safetensors") is None
+    cfg.enable_rec_quantization()
+    assert cfg.quantize_rec_head is True
+    with pytest.raises(rh.OcrError) as e:
+        rh.OcrEngineConfig(rec_head_backend="cuda")
+    assert e.value.op == "ModelError"
+
+
 def test_workloads_are_deterministic():
     from ppocr_rechead import workloads as wl
     w1, b1 = wl.weights()

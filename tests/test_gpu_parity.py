@@ -239,6 +239,43 @@ def test_ctc_collapse_matches_oracle(orc, rh):
     assert [x[0] for x in dec.decode_batch(d)] == ["ab", "b"]
 
 
+def test_ctc_greedy_dev_clamps_device_offsets(orc, rh):
+    """ppocr_ctc_greedy_dev reads the line offsets on the device and clamps them into
+    [0, line_off[lines]]: a negative start, a line running backwards and one past the end
+    give the results of the clamped lines, and nothing is written past the arrays (their
+    tails hold sentinels)."""
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    rng = np.random.default_rng(19)
+    total = 300
+    off = np.array([-7, 100, 60, 60, 250, 1000, total], np.int64)
+    lines = off.size - 1
+    idx = rng.integers(0, 5, total).astype(np.int32)
+    idx[0:100:2] = 0  # line 0 emits at most 50 indices, so its output stays clear of line 3's at 60
+    val = rng.random(total).astype(np.float32)
+    pad = 256
+    d_idx = DeviceArray.from_numpy(np.concatenate([idx, np.full(pad, 3, np.int32)]))
+    d_val = DeviceArray.from_numpy(np.concatenate([val, np.full(pad, 0.5, np.float32)]))
+    d_off = DeviceArray.from_numpy(off)
+    d_seq = DeviceArray.from_numpy(np.full(total + pad, -123, np.int32))
+    d_len = DeviceArray.from_numpy(np.full(lines + 8, -5, np.int64))
+    d_score = DeviceArray.from_numpy(np.full(lines + 8, -7.0, np.float32))
+    print("ctc_greedy_dev with out-of-range offsets", flush=True)
+    rh._check(rh._lib.lib().ppocr_ctc_greedy_dev(d_idx.p, d_val.p, d_off.p, lines, 0, d_seq.p, d_len.p, d_score.p,
+                                                 None))
+    synchronize()
+    seq, seq_len, score = d_seq.numpy(), d_len.numpy(), d_score.numpy()
+    assert np.all(seq[total:] == -123) and np.all(seq_len[lines:] == -5) and np.all(score[lines:] == -7.0)
+    t0 = np.minimum(np.maximum(off[:-1], 0), total)
+    t1 = np.minimum(np.maximum(off[1:], t0), total)
+    clamped = np.stack([t0, t1], axis=1)
+    for b, (a0, a1) in enumerate(clamped):
+        rs, rsc = orc.ctc_collapse(idx[a0:a1], val[a0:a1], np.array([0, a1 - a0], np.int64))
+        assert seq_len[b] == rs[0].size, b
+        assert score[b].view(np.uint32) == rsc[0].view(np.uint32), b
+    # line 0 ([0, 100)) overlaps no other line's output region
+    assert np.array_equal(seq[:seq_len[0]], orc.ctc_collapse(idx[:100], val[:100], np.array([0, 100]))[0][0])
+
+
 @pytest.mark.parametrize("mode", [0, 2, 3])
 def test_fused_argmax_a4_page(orc, rh, head, rhead, mode):
     from ppocr_rechead import workloads as wl

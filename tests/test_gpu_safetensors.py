@@ -162,3 +162,38 @@ def test_head_found_in_a_pp_ocr_v6_style_graph(orc, rh, tmp_path):
     assert_close_rel(gm["maxprob"], ref["maxprob"], "model-file head maxprob")
     hm.close()
     hs.close()
+
+
+def test_backend_switch_builds_the_configured_head(orc, rh, tmp_path):
+    """OcrEngineConfig's INT8 switch is unchanged and the backend selector picks the head:
+    "hip" with quantize_rec_head builds the INT8 head (the packing of
+    Model::quantize_matmul_weights, bit for bit), "hip" without it the FP32 head, and
+    enable_rec_quantization turns a later build INT8 (src/pipeline.rs:38-40, 195-199, 267-270);
+    "cpu" builds nothing on the GPU."""
+    import json
+    from safetensors.numpy import save_file
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights(n=700)
+    graph = {"inputs": ["x"], "outputs": ["probs"], "nodes": [
+        {"name": "MatMul.12", "op": "MatMul", "inputs": ["x", "linear_8.w_0"], "outputs": ["mm"]},
+        {"name": "Add.9", "op": "Add", "inputs": ["mm", "linear_8.b_0"], "outputs": ["logits"]},
+        {"name": "Softmax.2", "op": "Softmax", "inputs": ["logits"], "outputs": ["probs"]}]}
+    path = str(tmp_path / "rec.safetensors")
+    save_file({"linear_8.w_0": np.ascontiguousarray(w_t.T), "linear_8.b_0": bias}, path,
+              metadata={"graph": json.dumps(graph)})
+    print("backend switch", flush=True)
+    assert rh.RecHead.for_config(rh.OcrEngineConfig(quantize_rec_head=True), path) is None
+    cfg = rh.OcrEngineConfig(rec_head_backend="hip")
+    h32 = rh.RecHead.for_config(cfg, path)
+    assert (h32.quantized, h32.n, h32.k) == (False, 700, 120)
+    assert h32.weight_footprint_bytes() == 4 * 700 * 120
+    cfg.enable_rec_quantization()
+    h8 = rh.RecHead.for_config(cfg, path)
+    assert (h8.quantized, h8.n, h8.k) == (True, 700, 120)
+    assert h8.weight_footprint_bytes() == 700 * 120 + 4 * 700
+    q, s = orc.pack_int8(w_t)
+    a = np.random.default_rng(3).standard_normal((50, 120)).astype(np.float32)
+    assert np.abs(h8.logits(a) - orc.matmul_quantized_b(a, q, s, bias)).max() < 1e-4
+    assert np.abs(h32.logits(a) - orc.matmul_transposed_b(a, w_t, bias)).max() < 1e-4
+    h8.close()
+    h32.close()
