@@ -54,6 +54,29 @@ struct ppocr_rh {
 
 namespace {
 
+// Every device allocation of the library goes through these two, so that tests can make
+// them fail: with PPOCR_RECHEAD_FAULT=alloc in the environment (read at each allocation),
+// they return hipErrorOutOfMemory without allocating, as an exhausted HBM would, and the
+// calls report PPOCR_ERR_NO_MEMORY.
+bool alloc_fault() {
+    const char* v = std::getenv("PPOCR_RECHEAD_FAULT");
+    return v && std::strcmp(v, "alloc") == 0;
+}
+hipError_t dev_malloc(void** p, size_t bytes) {
+    if (alloc_fault()) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+hipError_t dev_malloc_async(void** p, size_t bytes, hipStream_t st) {
+    if (alloc_fault()) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMallocAsync(p, bytes, st);
+}
+
 struct DeviceGuard {
     int prev = -1;
     int err = 0;
@@ -153,7 +176,7 @@ public:
             a_->base = nullptr;
             a_->cap = 0;
             void* p = nullptr;
-            if (hipMalloc(&p, total) != hipSuccess) {
+            if (dev_malloc(&p, total) != hipSuccess) {
                 (void)hipGetLastError();
                 return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation of " + std::to_string(total) +
                                                      " bytes failed");
@@ -238,7 +261,7 @@ struct DevBuf {
     }
     int alloc(size_t bytes) {
         if (bytes == 0) bytes = 1;
-        if (hipMalloc(&p, bytes) != hipSuccess) {
+        if (dev_malloc(&p, bytes) != hipSuccess) {
             p = nullptr;
             (void)hipGetLastError();
             return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation of " + std::to_string(bytes) + " bytes failed");
@@ -323,7 +346,7 @@ void free_handle(ppocr_rh* h) {
 template <typename T>
 int upload(T** dst, const T* src, size_t count, size_t* total) {
     const size_t bytes = std::max<size_t>(count * sizeof(T), 1);
-    if (hipMalloc((void**)dst, bytes) != hipSuccess) {
+    if (dev_malloc((void**)dst, bytes) != hipSuccess) {
         *dst = nullptr;
         (void)hipGetLastError();
         return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation failed");
@@ -571,7 +594,7 @@ struct Workspace {
             return PPOCR_OK;
         }
         void* q = nullptr;
-        if (hipMallocAsync(&q, std::max<size_t>(need, kAlign), s) != hipSuccess) {
+        if (dev_malloc_async(&q, std::max<size_t>(need, kAlign), s) != hipSuccess) {
             (void)hipGetLastError();
             return fail(PPOCR_ERR_NO_MEMORY, std::string(op) + ": workspace allocation failed");
         }
@@ -703,7 +726,7 @@ int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, 
     size_t total = 0;
     auto dev_alloc = [&](void** p, size_t bytes) -> int {
         bytes = std::max<size_t>(bytes, 1);
-        if (hipMalloc(p, bytes) != hipSuccess) {
+        if (dev_malloc(p, bytes) != hipSuccess) {
             *p = nullptr;
             (void)hipGetLastError();
             return fail(PPOCR_ERR_NO_MEMORY, "RecHeadHip: device allocation failed");

@@ -6,6 +6,7 @@ malformed cases."""
 import ctypes
 import json
 import os
+import re
 import struct
 
 import numpy as np
@@ -226,18 +227,16 @@ def test_find_head_name_buffer_too_small(rh, tmp_path):
     assert rc == rh.PPOCR_ERR_INVALID_ARG and "does not fit" in rh._lib.last_error()
 
 
-def test_mutated_files_never_crash(rh, tmp_path):
-    """Seeded truncations and byte mutations of a valid model file (header length field,
-    header JSON, graph JSON, data): the parser returns PPOCR_OK or PPOCR_ERR_MODEL for
-    each, never crashes.  Runs in a child process so that a crash fails this test alone."""
-    import subprocess
-    import sys
+def _mutated_files(tmp_path, count=300, seed=77):
+    """Seeded truncations and byte mutations of a valid model file with a graph (header
+    length field, header JSON, graph JSON, data), written under tmp_path; the valid file
+    first."""
     src = _graph_file(tmp_path, NECK + HEAD)
     blob = open(src, "rb").read()
     hlen = struct.unpack("<Q", blob[:8])[0]
-    rng = np.random.default_rng(77)
-    cases = []
-    for x in range(300):
+    rng = np.random.default_rng(seed)
+    cases = [src]
+    for x in range(count):
         b = bytearray(blob)
         kind = x % 4
         if kind == 0:  # truncation anywhere
@@ -254,6 +253,16 @@ def test_mutated_files_never_crash(rh, tmp_path):
         p = tmp_path / f"m{x}.safetensors"
         p.write_bytes(bytes(b))
         cases.append(str(p))
+    return cases
+
+
+def test_mutated_files_never_crash(rh, tmp_path):
+    """The parser returns PPOCR_OK or PPOCR_ERR_MODEL for each seeded mutation of a valid
+    model file, never crashes.  Runs in a child process so that a crash fails this test
+    alone."""
+    import subprocess
+    import sys
+    cases = _mutated_files(tmp_path)
     code = r"""
 import ctypes, os, sys
 import ppocr_rechead as rh
@@ -273,6 +282,31 @@ print(sorted(seen))
     seen = set(json.loads(out.stdout.strip().splitlines()[-1]))
     assert seen <= {rh.PPOCR_OK, rh.PPOCR_ERR_MODEL}, seen
     assert rh.PPOCR_ERR_MODEL in seen
+
+
+def test_mutated_files_under_address_sanitizer(tmp_path):
+    """The host-only sanitizer build of the parser and the graph search (`make asan` in
+    rust-ppocrv6_amd/csrc: AddressSanitizer and UndefinedBehaviorSanitizer, any finding
+    fatal) over the same seeded mutations, more of them, and the reference's model files
+    where they are mounted: no finding, no crash."""
+    import glob
+    import shutil
+    import subprocess
+    if not shutil.which("g++"):
+        pytest.skip("no host C++ compiler")
+    csrc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "rust-ppocrv6_amd", "csrc")
+    build = subprocess.run(["make", "-C", csrc, "asan"], capture_output=True, text=True, timeout=600)
+    assert build.returncode == 0, build.stderr[-2000:]
+    exe = os.path.join(csrc, "..", "lib", "_asan", "parser_check")
+    cases = _mutated_files(tmp_path, count=1200, seed=78)
+    cases += sorted(glob.glob("/root/reference/models/*.safetensors"))
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0", UBSAN_OPTIONS="print_stacktrace=1")
+    out = subprocess.run([exe] + cases, capture_output=True, text=True, timeout=600, env=env)
+    assert out.returncode == 0, (out.returncode, out.stderr[-3000:])
+    assert "Sanitizer" not in out.stderr and "runtime error" not in out.stderr, out.stderr[-3000:]
+    acc, ref = map(int, re.search(r"accepted (\d+) refused (\d+)", out.stdout).groups())
+    print(f"parser under ASan/UBSan: {acc} accepted, {ref} refused")
+    assert acc >= 1 and ref >= 1 and acc + ref == len(cases)
 
 
 @pytest.mark.skipif(not os.path.isdir("/root/reference/models"), reason="reference model files not mounted")
