@@ -26,6 +26,7 @@ for _p in (ROOT, os.path.join(ROOT, "rust-ppocrv6_amd")):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
+MODE_NAMES = {0: "f32", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3", 4: "f16x2"}
 
 
 def parse():
@@ -34,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="dense_256")
-    p.add_argument("--mode", type=int, default=2, help="0 fp32 FMA, 1/2/3 bf16 terms")
+    p.add_argument("--mode", type=int, default=2, help="0 fp32 FMA, 1/2/3 bf16 terms, 4 two fp16 terms")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-others", action="store_true", help="skip the other configurations")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -230,7 +231,7 @@ def other_config(name, modes, steps, warmup):
             r["logits_ms"] = round(ms_l, 4)
             r["logits_GBps"] = round(lb / (ms_l / 1e3) / 1e9, 1)
             dlog.free()
-        res[{0: "fp32_fma", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3"}[mode]] = r
+        res["fp32_fma" if mode == 0 else MODE_NAMES[mode]] = r
         dws.free()
     head.close()
     return res
@@ -374,8 +375,7 @@ def main():
             "higher_is_better": True,
             "scaling": "weak",
             "vs_baseline": None,
-            "dtype": {0: "f32", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3"}[mode] + " MFMA, f32 accumulate, int8 weights"
-            if mode else "f32 FMA, int8 weights",
+            "dtype": MODE_NAMES[mode] + " MFMA, f32 accumulate, int8 weights" if mode else "f32 FMA, int8 weights",
             "data": "synthetic (seeded N(0,1) activations, N(0,0.05^2) weights packed to INT8 on the GPU)",
             "config": {"workload": f"{args.workload}: {lines} lines x T=120, m={m}, k={k}, n={n}, fused "
                                    "projection+softmax-max+argmax+CTC", "mode": mode},

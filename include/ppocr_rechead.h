@@ -44,8 +44,12 @@ typedef enum {
     PPOCR_MODE_FP32_FMA = 0, /* fp32 vector FMA over dequantised weights */
     PPOCR_MODE_BF16X1 = 1,   /* bf16 MFMA, activation rounded to 1 bf16 term */
     PPOCR_MODE_BF16X2 = 2,   /* bf16 MFMA, activation split into 2 bf16 terms (default) */
-    PPOCR_MODE_BF16X3 = 3    /* bf16 MFMA, activation split into 3 bf16 terms; for an
+    PPOCR_MODE_BF16X3 = 3,   /* bf16 MFMA, activation split into 3 bf16 terms; for an
                                 FP32 head, a_hi*w_hi + a_hi*w_lo + a_lo*w_hi */
+    PPOCR_MODE_F16X2 = 4     /* fp16 MFMA, activation split into 2 fp16 terms (22 bits of
+                                it; int8 weights are exact in fp16); for an FP32 head,
+                                a_hi*w_hi + a_hi*w_lo + a_lo*w_hi with fp16 halves (weights
+                                below 32768 in magnitude) */
 } ppocr_mode_t;
 
 typedef struct ppocr_rh ppocr_rh_t;
@@ -123,9 +127,12 @@ size_t ppocr_rh_workspace_bytes(const ppocr_rh_t* h, int64_t m, int mode);
  * Replaces matmul_quantized_b (src/ops/matmul.rs:1204-1336) for an INT8 head and
  * matmul_transposed_b (src/ops/matmul.rs:514-897) for an FP32 head:
  * out[r][j] = (sum_k a[r][k] * w[j][k]) * scale[j] + bias[j], a [m][k] -> out [m][n].
- * In PPOCR_MODE_BF16X2 rows whose largest |a| times the head's largest |w| exceeds 16 are
- * recomputed with three activation terms (a precision guard; the same applies to the
- * probs/argmax entry points). */
+ * The split modes carry a precision guard (the same in the probs/argmax/decode entry
+ * points): in PPOCR_MODE_BF16X2 and PPOCR_MODE_F16X2, rows whose largest |a| exceeds a
+ * limit set by the head's weights (the largest L2 norm of a dequantised class row; for
+ * F16X2 also the fp16 range) are recomputed with three bf16 activation terms (INT8 head) or
+ * in fp32 FMA (FP32 head, and PPOCR_MODE_BF16X3 on an FP32 head), so logits stay within
+ * 1e-4 of the reference. */
 int ppocr_rh_logits(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* out);
 int ppocr_rh_logits_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mode, float* d_out,
                         void* d_workspace, size_t workspace_bytes, void* stream);

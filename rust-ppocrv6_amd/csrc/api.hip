@@ -40,16 +40,20 @@ struct ppocr_rh {
     float* d_w = nullptr;      // [n][k] fp32 W^T (FP32 head)
     float* d_scale = nullptr;  // [n] per-class scale (1.0 for an FP32 head)
     float* d_bias = nullptr;   // [n] bias (0 when absent)
-    uint8_t* d_rec = nullptr;  // tiles x rec_bytes MFMA tile records
+    uint8_t* d_rec = nullptr;    // tiles x rec_bytes MFMA tile records, bf16 fragments
+    uint8_t* d_rec_h = nullptr;  // the same with fp16 fragments (F16X2)
     size_t device_bytes = 0;
-    FmaWeights fma{};          // the device weights above, for the fp32 FMA kernels
-    // Precision guard of the split-activation modes (INT8 two terms, FP32 bf16x3): rows
-    // with max|a| above this are recomputed (three terms, or fp32 FMA).
+    FmaWeights fma{};            // the device weights above, for the fp32 FMA kernels
+    // Precision guards of the split modes: rows with max|a| above the limit are recomputed
+    // (three bf16 terms for an INT8 head, fp32 FMA for an FP32 head).  amax_limit: bf16
+    // terms (BF16X2, an FP32 head's BF16X3); amax_limit_h: fp16 terms (F16X2).
     float amax_limit = INFINITY;
-    // Rows with max|a| at most this have every logit in [-kLogitBound, kLogitBound]:
-    // |logit| <= max|a| * max_c sum_k |w_ck| + max_c |b_c|.  Also at most amax_limit.
-    float stats_amax_limit = 0.0f;
-    bool stats_noref = false;
+    float amax_limit_h = INFINITY;
+    bool f16_ok = true;  // the weights fit fp16 (always for INT8; |w| < 32768 for FP32)
+    // Rows with max|a| at most range_limit have every logit in [-kLogitBound, kLogitBound]:
+    // |logit| <= max|a| * max_c sum_k |w_ck| + max_c |b_c| (range_ok: such a bound exists).
+    float range_limit = 0.0f;
+    bool range_ok = false;
 };
 
 namespace {
@@ -289,8 +293,11 @@ float bf16_to_float(uint16_t b) {
 }
 
 // Build the MFMA tile records on the host (see TileGeom in kernels.hpp).
+uint16_t f16_bits_rne(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+float f16_to_float(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
 std::vector<uint8_t> build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
-                                   const float* scale, const float* bias) {
+                                   const float* scale, const float* bias, bool f16) {
     std::vector<uint8_t> rec((size_t)g.tiles * g.rec_bytes(), 0);
     for (int t = 0; t < g.tiles; ++t) {
         uint8_t* r = rec.data() + (size_t)t * g.rec_bytes();
@@ -301,7 +308,11 @@ std::vector<uint8_t> build_records(const TileGeom& g, int64_t n, int64_t k, cons
             for (int64_t kk = 0; kk < k; ++kk) {
                 const int gg = (int)(kk / 8), e = (int)(kk % 8);
                 uint16_t hi, lo = 0;
-                if (q) {
+                if (f16) {
+                    const float v = q ? (float)q[row * k + kk] : w[row * k + kk];
+                    hi = f16_bits_rne(v);  // exact for int8 values
+                    if (!q) lo = f16_bits_rne(v - f16_to_float(hi));
+                } else if (q) {
                     hi = bf16_bits_rne((float)q[row * k + kk]);  // exact
                 } else {
                     const float v = w[row * k + kk];
@@ -340,6 +351,7 @@ void free_handle(ppocr_rh* h) {
     if (h->d_scale) (void)hipFree(h->d_scale);
     if (h->d_bias) (void)hipFree(h->d_bias);
     if (h->d_rec) (void)hipFree(h->d_rec);
+    if (h->d_rec_h) (void)hipFree(h->d_rec_h);
     delete h;
 }
 
@@ -391,20 +403,33 @@ ppocr_rh* new_handle(int64_t n, int64_t k, bool quantized, int device) {
 // 1e-4 bar; rows above are recomputed.
 constexpr double kSplitBoundInt8 = 8.0;
 constexpr double kSplitBoundF32 = 4.0;
+// Two fp16 terms keep 22 bits of the activation: measured the same way, the largest error
+// is about 8.7e-8 * max|a| * L2 (INT8 head) and 6.6e-7 * max|a| * L2 (an FP32 head with fp16
+// halves of both operands, as accurate as the fp32 product itself).  An fp16 term also
+// caps the magnitude: rows with max|a| above kF16Range are recomputed whatever the weights.
+constexpr double kSplitBoundF16Int8 = 512.0;
+constexpr double kSplitBoundF16F32 = 64.0;
+constexpr double kF16Range = 32768.0;
 
 // Guard limits from wmax = max_c max_k |w_ck| (float), w1 = max_c sum_k |w_ck|,
 // l2 = max_c ||w_c||_2 and bmax = max_c |b_c| (double), w the dequantised weight.
 void set_limits(ppocr_rh* h, float wmax, double w1, double l2, double bmax) {
     double lim = wmax > 0.0f ? 16.0 / (double)wmax : INFINITY;
-    if (l2 > 0.0 && std::isfinite(l2)) lim = std::min(lim, (h->quantized ? kSplitBoundInt8 : kSplitBoundF32) / l2);
+    double lim_h = kF16Range;
+    if (l2 > 0.0 && std::isfinite(l2)) {
+        lim = std::min(lim, (h->quantized ? kSplitBoundInt8 : kSplitBoundF32) / l2);
+        lim_h = std::min(lim_h, (h->quantized ? kSplitBoundF16Int8 : kSplitBoundF16F32) / l2);
+    }
+    if (!std::isfinite(l2)) lim = lim_h = 0.0;  // inf or NaN weights: every row goes to the rescue
     h->amax_limit = (float)lim;
+    h->amax_limit_h = (float)lim_h;
+    h->f16_ok = h->quantized || (double)wmax < kF16Range;
     // logit range bound: the largest L1 norm of a dequantised weight row and the largest
     // |bias|, rounded up by a small margin
     const double room = (double)kLogitBound - bmax * 1.001;
     if (room > 0.0 && std::isfinite(w1) && std::isfinite(bmax)) {
-        const double lim = w1 > 0.0 ? room / (w1 * 1.001) : INFINITY;
-        h->stats_amax_limit = (float)std::min((double)h->amax_limit, lim);
-        h->stats_noref = true;
+        h->range_limit = (float)(w1 > 0.0 ? room / (w1 * 1.001) : INFINITY);
+        h->range_ok = true;
     }
 }
 
@@ -464,8 +489,10 @@ int create_common(const int8_t* q, const float* w_t, const float* scales, const 
     h->fma = FmaWeights{h->d_q, h->d_w, h->d_scale, h->d_bias};
     if (int e = device_limits(h.get(), bias != nullptr)) return e;
     if (h->mfma_ok) {
-        std::vector<uint8_t> rec = build_records(h->geom, n, k, q, w_t, sc, bias);
-        if (int e = upload(&h->d_rec, rec.data(), rec.size(), &total)) return e;
+        for (int half = 0; half < 2; ++half) {
+            std::vector<uint8_t> rec = build_records(h->geom, n, k, q, w_t, sc, bias, half != 0);
+            if (int e = upload(half ? &h->d_rec_h : &h->d_rec, rec.data(), rec.size(), &total)) return e;
+        }
     }
     h->device_bytes = total;
     *out = h.release();
@@ -485,10 +512,16 @@ int mode_cfg(const ppocr_rh* h, int mode, int* cfg) {
         case PPOCR_MODE_BF16X2:
             if (!h->quantized)
                 return fail(PPOCR_ERR_INVALID_ARG,
-                            "MatMulTransposedB: an FP32 head supports modes FP32_FMA, BF16X1 and BF16X3");
+                            "MatMulTransposedB: an FP32 head supports modes FP32_FMA, BF16X1, BF16X3 and F16X2");
             *cfg = CFG_Q2;
             break;
         case PPOCR_MODE_BF16X3: *cfg = h->quantized ? CFG_Q3 : CFG_F3; break;
+        case PPOCR_MODE_F16X2:
+            if (!h->f16_ok)
+                return fail(PPOCR_ERR_INVALID_ARG,
+                            "MatMulTransposedB: weights beyond the fp16 range (|w| >= 32768); use BF16X3 or FP32_FMA");
+            *cfg = h->quantized ? CFG_H2 : CFG_HF3;
+            break;
         default: return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: unknown mode " + std::to_string(mode));
     }
     if (!h->mfma_ok)
@@ -547,12 +580,22 @@ unsigned next_epoch() {
     return x | 0x80000000u;
 }
 
-Guard make_guard(const ppocr_rh* h, const WsLayout& L, uint8_t* ws, int64_t m) {
-    return Guard{h->amax_limit,       reinterpret_cast<unsigned long long*>(ws + L.guard_header),
-                 reinterpret_cast<int*>(ws + L.guard_rows), (int)std::min<int64_t>(m, INT32_MAX),
-                 next_epoch(),        h->stats_amax_limit,
-                 h->stats_noref,      h->fma};
+// The guard of configuration cfg: the precision limit of its term type, and the lower
+// statistics limit (the logit range bound as well) when the head has one.
+Guard make_guard(const ppocr_rh* h, int cfg, const WsLayout& L, uint8_t* ws, int64_t m) {
+    const float prec = cfg_is_f16(cfg) ? h->amax_limit_h : h->amax_limit;
+    return Guard{prec,
+                 reinterpret_cast<unsigned long long*>(ws + L.guard_header),
+                 reinterpret_cast<int*>(ws + L.guard_rows),
+                 (int)std::min<int64_t>(m, INT32_MAX),
+                 next_epoch(),
+                 h->range_ok ? std::min(prec, h->range_limit) : prec,
+                 h->range_ok,
+                 h->fma};
 }
+
+// The tile records configuration cfg reads.
+const uint8_t* rec_of(const ppocr_rh* h, int cfg) { return cfg_is_f16(cfg) ? h->d_rec_h : h->d_rec; }
 
 // Projection + softmax statistics + merge (+ the CTC collapse with `ctc`), on device pointers.
 // line_len > 0: d_a is channels-first, [m / line_len][k][line_len].
@@ -565,8 +608,8 @@ int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* 
     float* p_sum = reinterpret_cast<float*>(ws + L.p_sum);
     int* p_idx = reinterpret_cast<int*>(ws + L.p_idx);
     if (cfg >= 0) {
-        const Guard g = make_guard(h, L, ws, m);
-        return launch_stats_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, d_idx,
+        const Guard g = make_guard(h, cfg, L, ws, m);
+        return launch_stats_mfma(cfg, h->geom, rec_of(h, cfg), h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum, p_idx, &g, d_idx,
                                  d_maxprob, d_row_max, d_row_inv, ctc, st, line_len);
     }
     if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
@@ -755,11 +798,14 @@ int ppocr_rh_create_from_safetensors(const char* path, const char* weight_name, 
     if (int e = device_limits(h.get(), b != nullptr)) return e;
     if (h->mfma_ok) {
         const size_t rec_bytes = (size_t)h->geom.tiles * h->geom.rec_bytes();
-        if (int e = dev_alloc((void**)&h->d_rec, rec_bytes)) return e;
-        PPOCR_HIP(hipMemset(h->d_rec, 0, rec_bytes));
-        if (int e = launch_build_records(h->geom, n, k, h->d_q, h->d_w, h->d_scale, b ? h->d_bias : nullptr, h->d_rec,
-                                         nullptr))
-            return e;
+        for (int half = 0; half < 2; ++half) {
+            uint8_t** dst = half ? &h->d_rec_h : &h->d_rec;
+            if (int e = dev_alloc((void**)dst, rec_bytes)) return e;
+            PPOCR_HIP(hipMemset(*dst, 0, rec_bytes));
+            if (int e = launch_build_records(h->geom, n, k, h->d_q, h->d_w, h->d_scale, b ? h->d_bias : nullptr,
+                                             half != 0, *dst, nullptr))
+                return e;
+        }
     }
     PPOCR_HIP(hipDeviceSynchronize());
     h->device_bytes = total;
@@ -822,8 +868,8 @@ int ppocr_rh_logits_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mo
     const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
     Workspace ws;
     if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, op)) return e;
-    const Guard g = make_guard(h, L, ws.p, m);
-    return launch_logits_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, d_out, &g, st);
+    const Guard g = make_guard(h, cfg, L, ws.p, m);
+    return launch_logits_mfma(cfg, h->geom, rec_of(h, cfg), h->d_rec, d_a, m, h->n, h->k, d_out, &g, st);
 }
 
 int ppocr_rh_logits(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* out) {
@@ -938,8 +984,8 @@ int ppocr_rh_probs_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, int mod
     if (int e = run_stats(h, cfg, d_a, m, nullptr, nullptr, rmax, rinv, ws.p, st)) return e;
     if (cfg < 0)
         return launch_probs_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, rmax, rinv, d_probs, st);
-    const Guard g = make_guard(h, L, ws.p, m);
-    return launch_probs_mfma(cfg, h->geom, h->d_rec, d_a, m, h->n, h->k, rmax, rinv, d_probs, &g, st);
+    const Guard g = make_guard(h, cfg, L, ws.p, m);
+    return launch_probs_mfma(cfg, h->geom, rec_of(h, cfg), h->d_rec, d_a, m, h->n, h->k, rmax, rinv, d_probs, &g, st);
 }
 
 int ppocr_rh_probs(const ppocr_rh_t* h, const float* a, int64_t m, int mode, float* probs) {

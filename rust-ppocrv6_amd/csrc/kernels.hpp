@@ -7,8 +7,10 @@ namespace ppocr {
 
 // ---------------------------------------------------------------- tile records
 // The projection weights live in HBM as one record per 32-class tile:
-//   [plane][group g][row i][8 x bf16]   bf16 weight fragments, g = k / 8
+//   [plane][group g][row i][8 x 16 bit]  weight fragments, g = k / 8 (bf16 or fp16)
 //   [4][32] f32                          scale*log2e, bias*log2e, scale, bias
+// A head holds two record sets with the same layout: bf16 fragments (the BF16Xn modes) and
+// fp16 fragments (F16X2).
 // Rows past n hold zero weights, scale 0, bias 0 and bias*log2e = -inf, so they never
 // win a maximum and add exp2(-inf) = 0 to a softmax sum.
 struct TileGeom {
@@ -20,8 +22,56 @@ struct TileGeom {
 };
 
 // Arithmetic configurations of the MFMA kernels: which activation term multiplies which
-// weight plane in each of the K-concatenated products.
-enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4 };
+// weight plane in each of the K-concatenated products, in bf16 (Q*, F*) or fp16 (H*).
+//   Q1, Q2, Q3   INT8 head, 1 / 2 / 3 bf16 activation terms
+//   F1, F3       FP32 head (two bf16 weight planes): a0*w0; a0*w0 + a0*w1 + a1*w0
+//   H2           INT8 head, 2 fp16 activation terms
+//   HF3          FP32 head, a0*w0 + a0*w1 + a1*w0 with fp16 halves
+enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4, CFG_H2 = 5, CFG_HF3 = 6 };
+inline bool cfg_is_f16(int cfg) { return cfg == CFG_H2 || cfg == CFG_HF3; }
+inline bool cfg_is_fp32_head(int cfg) { return cfg == CFG_F1 || cfg == CFG_F3 || cfg == CFG_HF3; }
+
+// Arguments of one launch of the statistics kernels and of the writer (head_mfma.hpp).
+struct StatsLaunch {
+    const float* a;
+    int64_t m;
+    int k, vec;
+    const uint8_t* rec;
+    int tiles, nsplit, tpc, mblocks;
+    float* p_best;
+    float* p_sum;
+    int* p_idx;
+    float amax_limit;
+    unsigned long long* guard_header;
+    int* guard_rows;
+    unsigned guard_epoch;
+    int guard_cap;
+};
+struct RowsLaunch {
+    const float* a;
+    int64_t m;
+    int k, vec;
+    const uint8_t* rec;
+    int tiles, n, nsplit, tpc, mblocks;
+    const float* row_max;
+    const float* row_inv;
+    float* out;
+    float amax_limit;
+    unsigned long long* guard_header;
+    int* guard_rows;
+    unsigned guard_epoch;
+    int guard_cap;
+};
+constexpr int kStatsWaves = 4;   // waves per workgroup of the statistics pass: two workgroups per CU
+constexpr int kWriterWaves = 4;  // consumer waves of the writer, 32 rows each (plus one loader)
+
+// Per-configuration launchers, explicitly instantiated in head_cfg_*.hip.
+template <int C, int G>
+int stats_main_cfg(const StatsLaunch& x, int mb, bool noref, unsigned grid, hipStream_t st);
+template <int C, int G>
+int stats_gather_cfg(const StatsLaunch& x, unsigned grid, hipStream_t st);
+template <int C, int G, bool GATHER>
+int rows_cfg(const RowsLaunch& x, int epi, unsigned grid, hipStream_t st);
 
 // Precision guard of the split-activation modes: rows whose max |a| exceeds amax_limit
 // are collected in rows[0 .. count) and recomputed with one more activation term.  The
@@ -68,14 +118,16 @@ int launch_transpose(const float* src, int64_t rows, int64_t cols, float* dst, h
 int launch_head_limits(const int8_t* q, const float* w, const float* scales, const float* bias, int64_t n, int64_t k,
                        HeadLimitBits* out, hipStream_t st);
 int launch_build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
-                         const float* scale, const float* bias, uint8_t* rec, hipStream_t st);
+                         const float* scale, const float* bias, bool f16, uint8_t* rec, hipStream_t st);
 
 // Writes an empty guard header (epoch 0, which no call uses): run once on every workspace
 // the library allocates, before its first use.
 int launch_guard_clear(unsigned long long* guard_header, hipStream_t st);
 
-int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
-                       int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
+// rec: the records the configuration reads (fp16 for H*, bf16 otherwise); rec_rescue: the
+// bf16 records of the three-term rescue of guarded rows (INT8 heads).
+int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a,
+                       int64_t m, int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.
 int stats_nsplit(int64_t m, int rows_per_block, int tiles);
 int stats_rows_per_block_mfma(int cfg, int64_t m);
@@ -97,11 +149,11 @@ struct CtcOut {
 // With `ctc`, the final merge also runs the CTC collapse (row_max and row_inv unused).
 // line_len > 0: `a` is channels-first, [m / line_len][k][line_len] (the tensor before the
 // neck's transpose); row r is step r % line_len of line r / line_len.
-int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
+int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a, int64_t m,
                       int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
                       const Guard* guard, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
                       const CtcOut* ctc, hipStream_t st, int64_t line_len = 0);
-int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const float* a, int64_t m,
+int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a, int64_t m,
                       int64_t n, int64_t k, const float* row_max, const float* row_inv, float* probs,
                       const Guard* guard, hipStream_t st);
 

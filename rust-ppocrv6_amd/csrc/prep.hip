@@ -116,14 +116,15 @@ __device__ __forceinline__ unsigned short bf16_bits_rne_dev(float x) {
     return (unsigned short)(u >> 16);
 }
 
-// One thread per (tile, class i, group g): the 8 bf16 weights of that group (and the low
-// plane of an FP32 head); the threads of group 0 also write the class's epilogue
+// One thread per (tile, class i, group g): the 8 weights of that group as bf16, or fp16 with
+// f16 (and the low plane of an FP32 head); the threads of group 0 also write the class's epilogue
 // constants.  Entries past k stay zero, classes past n get zero weights, scale 0 and
 // bias*log2e = -inf.
 __global__ __launch_bounds__(256) void build_records_kernel(int tiles, int G, int wplanes, int64_t n, int64_t k,
                                                             const int8_t* __restrict__ q, const float* __restrict__ w,
                                                             const float* __restrict__ scale,
-                                                            const float* __restrict__ bias, uint8_t* __restrict__ rec) {
+                                                            const float* __restrict__ bias, bool f16,
+                                                            uint8_t* __restrict__ rec) {
     const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t per_tile = 32LL * G;
     if (x >= (int64_t)tiles * per_tile) return;
@@ -139,7 +140,13 @@ __global__ __launch_bounds__(256) void build_records_kernel(int tiles, int G, in
         const int64_t kk = (int64_t)g * 8 + e;
         unsigned short hi = 0, lo = 0;
         if (row < n && kk < k) {
-            if (q) {
+            if (f16) {
+                // fp16 halves, rounded to nearest even; int8 values are exact
+                const float v = q ? (float)q[row * k + kk] : w[row * k + kk];
+                const _Float16 h = (_Float16)v;
+                hi = __builtin_bit_cast(unsigned short, h);
+                if (!q) lo = __builtin_bit_cast(unsigned short, (_Float16)__fsub_rn(v, (float)h));
+            } else if (q) {
                 hi = bf16_bits_rne_dev((float)q[row * k + kk]);  // exact
             } else {
                 const float v = w[row * k + kk];
@@ -168,14 +175,14 @@ __global__ __launch_bounds__(256) void build_records_kernel(int tiles, int G, in
 }
 
 int launch_build_records(const TileGeom& g, int64_t n, int64_t k, const int8_t* q, const float* w,
-                         const float* scale, const float* bias, uint8_t* rec, hipStream_t st) {
+                         const float* scale, const float* bias, bool f16, uint8_t* rec, hipStream_t st) {
     if (k > 8LL * g.G || g.tiles != (int)((n + 31) / 32) || (q == nullptr) != (g.wplanes == 2))
         return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
     const int64_t threads = (int64_t)g.tiles * 32 * g.G;
     if (threads <= 0) return PPOCR_OK;
     if ((threads + 255) / 256 > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: too many classes");
     build_records_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(g.tiles, g.G, g.wplanes, n, k, q, w, scale,
-                                                                             bias, rec);
+                                                                             bias, f16, rec);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

@@ -14,12 +14,17 @@ const SOURCES: &[&str] = &[
     "pack.hip",
     "prep.hip",
     "head_mfma.hip",
+    "head_cfg_q.hip",
+    "head_cfg_f.hip",
+    "head_cfg_h.hip",
+    "head_cfg_rescue.hip",
     "head_fma.hip",
     "softmax_ctc.hip",
     "safetensors.cpp",
     "model_graph.cpp",
 ];
-const HEADERS: &[&str] = &["common.hpp", "kernels.hpp", "safetensors.hpp", "json.hpp", "model_graph.hpp"];
+const HEADERS: &[&str] =
+    &["common.hpp", "kernels.hpp", "head_mfma.hpp", "safetensors.hpp", "json.hpp", "model_graph.hpp"];
 const FLAGS: &[&str] = &[
     "--offload-arch=gfx950",
     "-O3",

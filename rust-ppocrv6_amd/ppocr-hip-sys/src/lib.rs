@@ -27,6 +27,7 @@ pub const PPOCR_MODE_FP32_FMA: c_int = 0;
 pub const PPOCR_MODE_BF16X1: c_int = 1;
 pub const PPOCR_MODE_BF16X2: c_int = 2;
 pub const PPOCR_MODE_BF16X3: c_int = 3;
+pub const PPOCR_MODE_F16X2: c_int = 4;
 
 /// Opaque head handle (`ppocr_rh_t`).
 #[repr(C)]

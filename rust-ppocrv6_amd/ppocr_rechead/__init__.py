@@ -19,12 +19,12 @@ import os
 import numpy as np
 
 from . import _lib
-from ._lib import (MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
+from ._lib import (MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_F16X2, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
                    PPOCR_ERR_INVALID_ARG, PPOCR_ERR_MODEL, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
 
 __all__ = [
     "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "find_rec_head", "matmul_quantized_b", "matmul_transposed_b",
-    "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3",
+    "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3", "MODE_F16X2",
 ]
 
 

@@ -20,6 +20,7 @@ MODE_FP32_FMA = 0
 MODE_BF16X1 = 1
 MODE_BF16X2 = 2
 MODE_BF16X3 = 3
+MODE_F16X2 = 4
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

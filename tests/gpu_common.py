@@ -82,3 +82,12 @@ def peaked_rows(wd, targets, alpha, rng, noise=0.3):
     w /= np.linalg.norm(w, axis=1, keepdims=True)
     a = alpha[:, None] * w + noise * rng.standard_normal(w.shape)
     return a.astype(np.float32)
+
+
+def dot_tol(a, wd, base=1e-4):
+    """Logit bar for rows of large magnitude: base plus the fp32 rounding a length-k dot
+    product carries, 8 sqrt(k) ulps (2^-24) of the magnitude of its terms sum_k |a_k w_k|
+    (the reference's own arithmetic carries that much; for ordinary rows it adds ~2e-5)."""
+    k = a.shape[1]
+    mag = np.abs(a.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T
+    return base + 8.0 * np.sqrt(k) * 2.0 ** -24 * mag

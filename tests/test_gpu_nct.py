@@ -24,6 +24,9 @@ CASES = [
     (6, 117, 500, 3, 1, 2, False),       # one step per line
     (7, 120, 2049, 4, 97, 3, True),      # FP32 head, bf16x3
     (8, 119, 2049, 4, 50, 0, True),      # FP32 head, fp32 FMA
+    (9, 120, 18710, 80, 120, 4, False),  # fp16 terms, two blocks per wave
+    (10, 80, 6906, 6, 33, 4, False),     # fp16 terms, tiny head
+    (11, 120, 2049, 4, 97, 4, True),     # FP32 head, fp16 halves
 ]
 
 

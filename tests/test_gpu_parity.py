@@ -61,7 +61,7 @@ def test_pack_edge_shapes(orc, rh):
         assert np.array_equal(qw.data, q) and np.array_equal(qw.scales.view(np.uint32), s.view(np.uint32))
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("m", [1, 33, 120, 257])
 def test_int8_logits(orc, rh, head, rhead, mode, m):
     rng = np.random.default_rng(100 + m)
@@ -85,7 +85,7 @@ def test_int8_logits_no_bias_small_n(orc, rh):
         q, s = orc.pack_int8(w)
         a = rng.standard_normal((70, k), dtype=np.float32)
         head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=None)
-        for mode in (0, 2, 3):
+        for mode in (0, 2, 3, 4):
             print(f"int8 logits n={n} k={k} mode={mode} no bias", flush=True)
             got = head.logits(a, mode)
             ref = orc.matmul_quantized_b(a, q, s, None)
@@ -100,14 +100,14 @@ def test_tiny_head_real_rows(orc, rh):
     a = rng.standard_normal((50, 80), dtype=np.float32)
     bias = (rng.standard_normal(q.shape[0], dtype=np.float32) * np.float32(0.01)).astype(np.float32)
     head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
-    for mode in (0, 2, 3):
+    for mode in (0, 2, 3, 4):
         print(f"tiny real rows mode={mode}", flush=True)
         got = head.logits(a, mode)
         assert np.abs(got - orc.matmul_quantized_b(a, q, s, bias)).max() < TOL
     head.close()
 
 
-@pytest.mark.parametrize("mode", [0, 2, 3])
+@pytest.mark.parametrize("mode", [0, 2, 3, 4])
 def test_small_head_real_rows_decode(orc, rh, mode):
     """The whole head on 512 classes of the small model's real weights (its first 256
     classes, blank included, 128 from the middle and the last 128; golden fixture): ragged
@@ -135,7 +135,7 @@ def test_small_head_real_rows_decode(orc, rh, mode):
         assert abs(float(got["score"][b]) - float(ref["score"][b])) < TOL, (mode, b)
 
 
-@pytest.mark.parametrize("mode", [0, 1, 3])
+@pytest.mark.parametrize("mode", [0, 1, 3, 4])
 def test_fp32_head_logits(orc, rh, mode):
     from ppocr_rechead import workloads as wl
     w_t, bias = wl.weights()
@@ -276,7 +276,7 @@ def test_ctc_greedy_dev_clamps_device_offsets(orc, rh):
     assert np.array_equal(seq[:seq_len[0]], orc.ctc_collapse(idx[:100], val[:100], np.array([0, 100]))[0][0])
 
 
-@pytest.mark.parametrize("mode", [0, 2, 3])
+@pytest.mark.parametrize("mode", [0, 2, 3, 4])
 def test_fused_argmax_a4_page(orc, rh, head, rhead, mode):
     from ppocr_rechead import workloads as wl
     a = wl.activations("a4_page")
@@ -288,7 +288,7 @@ def test_fused_argmax_a4_page(orc, rh, head, rhead, mode):
     assert_close_rel(mp, ref["maxprob"], f"a4_page maxprob mode {mode}")
 
 
-@pytest.mark.parametrize("mode", [0, 2, 3])
+@pytest.mark.parametrize("mode", [0, 2, 3, 4])
 def test_fused_probs_single_line(orc, rh, head, rhead, mode):
     from ppocr_rechead import workloads as wl
     a = wl.activations("single_line")

@@ -9,8 +9,8 @@ at top-2 logit gaps below 1e-4, which are printed."""
 import numpy as np
 import pytest
 
-from gpu_common import (assert_close_rel, check_argmax, f64_logits_f32, f64_logits_q, oracle_head_f32, peaked_rows,
-                        rel_scale, split_lines, top2_gap)
+from gpu_common import (assert_close_rel, check_argmax, dot_tol, f64_logits_f32, f64_logits_q, oracle_head_f32,
+                        peaked_rows, rel_scale, split_lines, top2_gap)
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +39,14 @@ def _f32_limit(w_t):
     return min(16.0 / float(np.abs(w_t).max()), 4.0 / float(np.sqrt((w * w).sum(axis=1)).max()))
 
 
-@pytest.mark.parametrize("mode", [0, 3])
+def _f16_limit_int8(q, s):
+    """The INT8 head's limit with two fp16 activation terms: min(32768, 512 / L2)."""
+    qa = np.abs(q.astype(np.int64))
+    l2 = float(np.max(np.sqrt((qa * qa).sum(axis=1).astype(np.float64)) * s.astype(np.float64)))
+    return min(32768.0, 512.0 / l2)
+
+
+@pytest.mark.parametrize("mode", [0, 3, 4])
 def test_fp32_head_m7680_logits(orc, rh, mode):
     """The FP32 head at 64 lines x T=120 (m = 7680), every row's logits from the GPU, sampled
     rows (the last row block among them) against matmul_transposed_b."""
@@ -60,7 +67,7 @@ def test_fp32_head_m7680_logits(orc, rh, mode):
     assert err < TOL
 
 
-@pytest.mark.parametrize("mode", [0, 3])
+@pytest.mark.parametrize("mode", [0, 3, 4])
 def test_fp32_head_m7680_decode(orc, rh, mode):
     """The fused head (statistics pass, chunk merge, CTC) with the FP32 weight at m = 7680:
     every row's argmax and maximum probability and every line's sequence and score against
@@ -86,7 +93,7 @@ def test_fp32_head_m7680_decode(orc, rh, mode):
         assert abs(float(got["score"][b]) - float(ref["score"][b])) <= TOL * max(1e-3, abs(float(ref["score"][b])))
 
 
-@pytest.mark.parametrize("mode", [2, 3])
+@pytest.mark.parametrize("mode", [2, 3, 4])
 def test_peaked_outputs_decode_and_probs(orc, rh, head, mode):
     """Rows built so that one class dominates (maximum probability ~0.5 .. 0.99, blank and
     repeated classes among the targets, as in real CTC output): decode and probabilities
@@ -203,3 +210,77 @@ def test_dense_256_whole_batch(orc, rh, head):
         assert abs(float(got["score"][b]) - float(ref["score"][b])) <= TOL * max(1e-3, abs(float(ref["score"][b])))
         same += 1
     print(f"  {same} of {len(off) - 1} lines identical (the rest hold near-tie rows)")
+
+
+def test_f16x2_around_its_limit_and_range(orc, rh, head):
+    """F16X2 (two fp16 activation terms) logits and fused argmax for rows of max|a| 0.5 ..
+    0.99 of its precision limit, 1.01 .. 3 of it (recomputed with three bf16 terms), and
+    rows beyond the fp16 range (|a| up to 1e5, recomputed) against the oracle; the logits'
+    bar grows with the magnitude of the products by the fp32 rounding the reference itself
+    carries (dot_tol)."""
+    lim = _f16_limit_int8(head["q"], head["s"])
+    rng = np.random.default_rng(35)
+    fr = np.concatenate([np.linspace(0.5, 0.99, 64), np.linspace(1.01, 3.0, 32)])
+    a = rng.standard_normal((fr.size, 120)).astype(np.float32)
+    a = (a / np.abs(a).max(axis=1, keepdims=True) * (fr * lim)[:, None]).astype(np.float32)
+    huge = rng.standard_normal((16, 120)).astype(np.float32) * np.float32(3e4)
+    a = np.concatenate([a, huge]).astype(np.float32)
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    print(f"f16x2 around the limit {lim:.1f} and beyond the fp16 range", flush=True)
+    got = h.logits(a, 4)
+    idx, mp = h.argmax(a, 4)
+    h.close()
+    ref = orc.matmul_quantized_b(a, head["q"], head["s"], head["bias"])
+    tol = dot_tol(a, head["wd"])
+    err = np.abs(got - ref)
+    print(f"  max|logits diff|: under {err[:64].max():.2e}, over {err[64:96].max():.2e}, beyond range "
+          f"{err[96:].max():.2e} (|logit| up to {np.abs(ref).max():.0f})")
+    assert np.all(err <= tol)
+    lg = f64_logits_q(a, head["q"], head["s"], head["bias"])
+    r = orc.rechead_lines(a, split_lines(a.shape[0], 16), head["q"], head["s"], head["bias"])
+    check_argmax(idx, r["idx"], top2_gap(lg), label="f16x2 limit")
+    assert_close_rel(mp, r["maxprob"], "f16x2 limit maxprob", row_scale=rel_scale(lg))
+
+
+@pytest.mark.parametrize("mode", [2, 4])
+def test_tiny_activations(orc, rh, head, mode):
+    """Rows of magnitude 1e-3 .. 1e-7 (fp16 terms in and below the subnormal range, bf16
+    terms far from it): logits within 1e-4 and the fused argmax against the oracle."""
+    rng = np.random.default_rng(36)
+    a = np.concatenate([rng.standard_normal((32, 120)) * sc for sc in (1e-3, 1e-4, 1e-5, 1e-7)]).astype(np.float32)
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    print(f"tiny activations mode {mode}", flush=True)
+    got = h.logits(a, mode)
+    idx, mp = h.argmax(a, mode)
+    h.close()
+    ref = orc.matmul_quantized_b(a, head["q"], head["s"], head["bias"])
+    err = np.abs(got - ref).max()
+    print(f"  max|logits diff| {err:.2e}")
+    assert err < TOL
+    r = orc.rechead_lines(a, split_lines(a.shape[0], 32), head["q"], head["s"], head["bias"])
+    check_argmax(idx, r["idx"], top2_gap(f64_logits_q(a, head["q"], head["s"], head["bias"])), label="tiny")
+    assert_close_rel(mp, r["maxprob"], f"tiny maxprob mode {mode}")
+
+
+def test_f16x2_outlier_head_needs_no_rescue_for_ordinary_rows(orc, rh):
+    """The stress head (0.5% of its classes hold a single +-5 weight): with fp16 terms its
+    precision limit stays far above ordinary rows' magnitudes, and the logits of N(0,1) rows
+    (max|a| ~ 3..5) meet the bar on the two-term path itself.  Checked on rows that the
+    bf16 limit would send to the rescue."""
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights(stress=True)
+    q, s = orc.pack_int8(w_t)
+    lim16 = _f16_limit_int8(q, s)
+    lim_bf = _int8_limit(q, s)
+    rng = np.random.default_rng(37)
+    a = rng.standard_normal((256, 120)).astype(np.float32)
+    amax = np.abs(a).max(axis=1)
+    print(f"stress head: bf16 limit {lim_bf:.2f}, fp16 limit {lim16:.1f}; rows over the bf16 limit "
+          f"{int((amax > lim_bf).sum())}/256, over the fp16 limit {int((amax > lim16).sum())}/256", flush=True)
+    assert (amax > lim_bf).mean() > 0.9 and not np.any(amax > lim16)
+    h = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    got = h.logits(a, 4)
+    h.close()
+    err = np.abs(got - orc.matmul_quantized_b(a, q, s, bias)).max()
+    print(f"  max|logits diff| {err:.2e}")
+    assert err < TOL

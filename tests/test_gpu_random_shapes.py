@@ -27,6 +27,9 @@ CASES = [
     (8, 119, 2049, [25] * 12, 2),
     (9, 120, 18710, [3, 120, 77], 2),
     (10, 80, 64, [0, 10, 0, 5], 2),
+    (11, 120, 18710, [120, 37, 1], 4),
+    (12, 80, 6906, [40, 97, 12], 4),
+    (13, 115, 500, [1, 2, 3, 4, 5, 6, 7, 8], 4),
 ]
 
 
@@ -115,7 +118,8 @@ def test_logits_and_probs_random_shapes(orc, rh, seed, k, n, lens, mode):
     assert_close_rel(probs, orc.softmax_rows(ref), f"seed {seed} probs", row_scale=rel_scale(f64_logits_q(a, q, s, bias)))
 
 
-@pytest.mark.parametrize("k,n,mode", [(120, 500, 0), (120, 500, 3), (80, 6906, 3), (77, 33, 0), (119, 2049, 3)])
+@pytest.mark.parametrize("k,n,mode", [(120, 500, 0), (120, 500, 3), (80, 6906, 3), (77, 33, 0), (119, 2049, 3),
+                                      (120, 500, 4), (80, 6906, 4), (117, 2049, 4)])
 def test_fp32_head_random_shapes(orc, rh, k, n, mode):
     """FP32 heads (W^T in fp32, matmul_transposed_b): logits, probabilities and the whole
     head against the oracle, for the fp32 FMA and the three-term MFMA modes."""

@@ -46,7 +46,7 @@ def test_int8_head_from_file_equals_host_packed(orc, rh, tmp_path, k, n, with_bi
     assert hf.device_bytes() == hh.device_bytes()
     a = rng.standard_normal((300, k)).astype(np.float32)
     a[::37] *= np.float32(40.0)        # rows over the precision guard
-    modes = (0, 2, 3) if k in (120, 80) else (0,)
+    modes = (0, 2, 3, 4) if k in (120, 80) else (0,)
     for mode in modes:
         _same(hf.logits(a, mode), hh.logits(a, mode))
         i1, p1 = hf.argmax(a, mode)
@@ -75,7 +75,7 @@ def test_fp32_head_from_file_equals_host_transposed(rh, tmp_path, k, n):
     assert hf.weight_footprint_bytes() == hh.weight_footprint_bytes() == 4 * n * k
     assert hf.device_bytes() == hh.device_bytes()
     a = rng.standard_normal((200, k)).astype(np.float32)
-    for mode in ((0, 1, 3) if k in (120, 80) else (0,)):
+    for mode in ((0, 1, 3, 4) if k in (120, 80) else (0,)):
         _same(hf.logits(a, mode), hh.logits(a, mode))
         i1, p1 = hf.argmax(a, mode)
         i2, p2 = hh.argmax(a, mode)

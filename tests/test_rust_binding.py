@@ -81,7 +81,7 @@ def test_crate_constants_match_the_header():
 
 def test_build_script_compiles_every_library_source_for_gfx950_only():
     b = open(os.path.join(CRATE, "build.rs")).read()
-    mk = open(os.path.join(ROOT, "rust-ppocrv6_amd", "csrc", "Makefile")).read()
+    mk = open(os.path.join(ROOT, "rust-ppocrv6_amd", "csrc", "Makefile")).read().replace("\\\n", " ")
     srcs = re.findall(r"(\w+\.(?:hip|cpp))", re.search(r"HIP_SRCS = ([^\n]*)\nCPP_SRCS = ([^\n]*)", mk).group(0))
     listed = re.findall(r'"(\w+\.(?:hip|cpp))"', b)
     assert sorted(srcs) == sorted(listed)
