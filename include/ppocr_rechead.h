@@ -46,10 +46,15 @@ typedef enum {
     PPOCR_MODE_BF16X2 = 2,   /* bf16 MFMA, activation split into 2 bf16 terms (default) */
     PPOCR_MODE_BF16X3 = 3,   /* bf16 MFMA, activation split into 3 bf16 terms; for an
                                 FP32 head, a_hi*w_hi + a_hi*w_lo + a_lo*w_hi */
-    PPOCR_MODE_F16X2 = 4     /* fp16 MFMA, activation split into 2 fp16 terms (22 bits of
+    PPOCR_MODE_F16X2 = 4,    /* fp16 MFMA, activation split into 2 fp16 terms (22 bits of
                                 it; int8 weights are exact in fp16); for an FP32 head,
                                 a_hi*w_hi + a_hi*w_lo + a_lo*w_hi with fp16 halves (weights
                                 below 32768 in magnitude) */
+    PPOCR_MODE_AUTO = 5      /* chosen per head from its weights: the bf16 split (BF16X2, or
+                                BF16X3 for an FP32 head) when its precision guard leaves rows
+                                of magnitude up to 8 on the split path, F16X2 otherwise (heads
+                                with large weight rows, whose bf16 guard would send ordinary
+                                rows to the rescue).  ppocr_rh_auto_mode tells which. */
 } ppocr_mode_t;
 
 typedef struct ppocr_rh ppocr_rh_t;
@@ -114,6 +119,10 @@ size_t ppocr_rh_footprint_bytes(const ppocr_rh_t* h);
 size_t ppocr_rh_device_bytes(const ppocr_rh_t* h);
 /* n, k and whether the head is INT8 (1) or FP32 (0). */
 int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized);
+/* The mode PPOCR_MODE_AUTO runs for this head (PPOCR_MODE_BF16X2, PPOCR_MODE_BF16X3 or
+ * PPOCR_MODE_F16X2), -1 for a null handle.  No counterpart in the reference, whose CPU
+ * kernels have one precision. */
+int ppocr_rh_auto_mode(const ppocr_rh_t* h);
 
 /* Device workspace needed by the `_dev` entry points below for m rows (0 if none).  A
  * NULL workspace makes the call allocate one on its stream (stream-ordered) and free it

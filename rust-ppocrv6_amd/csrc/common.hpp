@@ -89,4 +89,26 @@ __device__ __forceinline__ RowStat stat_merge(RowStat a, RowStat b) {
     return r;
 }
 
+// stat_merge of two normalised statistics (ref = best, or best = -inf with sum = 0), as the
+// merge of chunk partials sees them: the winner's own term is sum * exp2(0) = sum, so only
+// the loser's rescaling needs an exp2 (stat_merge takes four).  The same value as
+// stat_merge up to the rounding of the last addition (the loser's term is added to the
+// winner's sum, with contraction); non-finite maxima give a NaN sum as there (best - best
+// is NaN).  Sums are never -0, so w.sum + 0 = w.sum.
+__device__ __forceinline__ RowStat stat_merge_norm(RowStat a, RowStat b) {
+    const bool take_a = (a.best > b.best) || (a.best == b.best && a.idx <= b.idx);
+    const RowStat w = take_a ? a : b;
+    const RowStat l = take_a ? b : a;
+    const float m = w.best;
+    float s = 0.0f;
+    if (w.best != -INFINITY) s = w.sum + (w.best - w.best);
+    if (l.best != -INFINITY) s += (l.sum + (l.best - l.best)) * exp2f(l.best - m);
+    RowStat r;
+    r.best = m;
+    r.idx = w.idx;
+    r.sum = s;
+    r.ref = (m == -INFINITY) ? 0.0f : m;
+    return r;
+}
+
 }  // namespace ppocr

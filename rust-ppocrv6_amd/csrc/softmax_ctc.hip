@@ -198,9 +198,10 @@ __device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, 
 #pragma unroll
             for (int x = 0; x < kMergeBatch; ++x) {
                 if (c0 + x * kMergeLanes < nsplit) {
-                    // partial sums are relative to their own maximum
+                    // partial sums are relative to their own maximum: both operands are
+                    // normalised
                     const RowStat o{bv[x], sv[x], (bv[x] == -INFINITY) ? 0.0f : bv[x], iv[x]};
-                    s = stat_merge(s, o);
+                    s = stat_merge_norm(s, o);
                 }
             }
         }
@@ -209,7 +210,7 @@ __device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, 
     for (int off = 1; off < kMergeLanes; off <<= 1) {
         const RowStat o{__shfl_xor(s.best, off, 64), __shfl_xor(s.sum, off, 64), __shfl_xor(s.ref, off, 64),
                         __shfl_xor(s.idx, off, 64)};
-        s = stat_merge(s, o);
+        s = stat_merge_norm(s, o);
     }
     // s.sum is relative to s.best, so the maximum itself contributes exp2(0) = 1 and the
     // sum is at least 1 (rounding of the rescaling could leave it an ulp below).

@@ -28,6 +28,7 @@ pub const PPOCR_MODE_BF16X1: c_int = 1;
 pub const PPOCR_MODE_BF16X2: c_int = 2;
 pub const PPOCR_MODE_BF16X3: c_int = 3;
 pub const PPOCR_MODE_F16X2: c_int = 4;
+pub const PPOCR_MODE_AUTO: c_int = 5;
 
 /// Opaque head handle (`ppocr_rh_t`).
 #[repr(C)]
@@ -59,6 +60,8 @@ extern "C" {
     pub fn ppocr_rh_footprint_bytes(h: *const ppocr_rh_t) -> usize;
     pub fn ppocr_rh_device_bytes(h: *const ppocr_rh_t) -> usize;
     pub fn ppocr_rh_shape(h: *const ppocr_rh_t, n: *mut i64, k: *mut i64, quantized: *mut c_int) -> c_int;
+    /// The mode PPOCR_MODE_AUTO runs for this head (no counterpart in the reference).
+    pub fn ppocr_rh_auto_mode(h: *const ppocr_rh_t) -> c_int;
     pub fn ppocr_rh_workspace_bytes(h: *const ppocr_rh_t, m: i64, mode: c_int) -> usize;
 
     // ---- MatMul.12: matmul_quantized_b (src/ops/matmul.rs:1204-1336) / matmul_transposed_b

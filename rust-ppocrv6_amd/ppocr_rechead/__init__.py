@@ -19,12 +19,12 @@ import os
 import numpy as np
 
 from . import _lib
-from ._lib import (MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_F16X2, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
+from ._lib import (MODE_AUTO, MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_F16X2, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
                    PPOCR_ERR_INVALID_ARG, PPOCR_ERR_MODEL, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
 
 __all__ = [
     "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "find_rec_head", "matmul_quantized_b", "matmul_transposed_b",
-    "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3", "MODE_F16X2",
+    "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3", "MODE_F16X2", "MODE_AUTO",
 ]
 
 
@@ -128,7 +128,7 @@ class RecHead:
             self.n, self.k = w_t.shape
             _check(_lib.lib().ppocr_rh_create_f32(_ptr(w_t), _ptr(bias_c), self.n, self.k, device,
                                                   ctypes.byref(self._h)))
-        self.default_mode = MODE_BF16X2 if self.quantized else MODE_BF16X3
+        self.default_mode = MODE_AUTO
 
     @classmethod
     def from_safetensors(cls, path, weight_name, bias_name=None, quantize=True, device=0):
@@ -144,7 +144,7 @@ class RecHead:
         n, k, q = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
         _check(_lib.lib().ppocr_rh_shape(self._h, ctypes.byref(n), ctypes.byref(k), ctypes.byref(q)))
         self.n, self.k, self.quantized = n.value, k.value, bool(q.value)
-        self.default_mode = MODE_BF16X2 if self.quantized else MODE_BF16X3
+        self.default_mode = MODE_AUTO
         return self
 
     @classmethod
@@ -185,6 +185,10 @@ class RecHead:
 
     def device_bytes(self):
         return int(_lib.lib().ppocr_rh_device_bytes(self._h))
+
+    def auto_mode(self):
+        """The mode MODE_AUTO (the default) runs for this head's weights."""
+        return int(_lib.lib().ppocr_rh_auto_mode(self._h))
 
     def workspace_bytes(self, m, mode=None):
         return int(_lib.lib().ppocr_rh_workspace_bytes(self._h, m, self.default_mode if mode is None else mode))

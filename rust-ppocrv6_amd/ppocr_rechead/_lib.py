@@ -21,6 +21,7 @@ MODE_BF16X1 = 1
 MODE_BF16X2 = 2
 MODE_BF16X3 = 3
 MODE_F16X2 = 4
+MODE_AUTO = 5
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -43,6 +44,7 @@ SIGNATURES = {
     "ppocr_rh_footprint_bytes": (_sz, [_vp]),
     "ppocr_rh_device_bytes": (_sz, [_vp]),
     "ppocr_rh_shape": (_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_int)]),
+    "ppocr_rh_auto_mode": (_int, [_vp]),
     "ppocr_rh_workspace_bytes": (_sz, [_vp, _i64, _int]),
     "ppocr_rh_logits": (_int, [_vp, _vp, _i64, _int, _vp]),
     "ppocr_rh_logits_dev": (_int, [_vp, _vp, _i64, _int, _vp, _vp, _sz, _vp]),

@@ -68,8 +68,9 @@ impl GpuHead {
     fn from_handle(h: *mut sys::ppocr_rh_t) -> Result<Self> {
         let (mut n, mut k, mut q) = (0i64, 0i64, 0i32);
         check("RecHeadHip", unsafe { sys::ppocr_rh_shape(h, &mut n, &mut k, &mut q) })?;
-        // INT8: two bf16 activation terms with the precision guard; FP32: three products
-        let mode = if q != 0 { sys::PPOCR_MODE_BF16X2 } else { sys::PPOCR_MODE_BF16X3 };
+        // the split the library picks for these weights (bf16 or fp16 terms), with the
+        // precision guard
+        let mode = sys::PPOCR_MODE_AUTO;
         Ok(Self { h, n: n as usize, k: k as usize, quantized: q != 0, mode })
     }
 

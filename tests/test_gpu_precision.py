@@ -284,3 +284,34 @@ def test_f16x2_outlier_head_needs_no_rescue_for_ordinary_rows(orc, rh):
     err = np.abs(got - orc.matmul_quantized_b(a, q, s, bias)).max()
     print(f"  max|logits diff| {err:.2e}")
     assert err < TOL
+
+
+def test_auto_mode_picks_per_head_and_matches_the_explicit_mode(orc, rh):
+    """MODE_AUTO, the default: the bf16 split for a head whose bf16 limit is at least 8 (the
+    synthetic INT8 head, ~11.7), the fp16 split for one whose large weight rows pull it
+    below (the stress head, ~1.6; the synthetic FP32 head, ~5.8).  Its results are those of
+    the explicit mode, bit for bit, on logits and on the decode."""
+    from ppocr_rechead import workloads as wl
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((512, 120)).astype(np.float32)
+    off = np.array([0, 40, 40, 300, 512], np.int64)
+    cases = []
+    w_t, bias = wl.weights()
+    q, s = orc.pack_int8(w_t)
+    cases.append(("int8", rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias), _int8_limit(q, s)))
+    w_t2, bias2 = wl.weights(stress=True)
+    q2, s2 = orc.pack_int8(w_t2)
+    cases.append(("int8 stress", rh.RecHead(qw=rh.QuantizedWeight(q2, s2), bias=bias2), _int8_limit(q2, s2)))
+    cases.append(("fp32", rh.RecHead(w_t=w_t, bias=bias), _f32_limit(w_t)))
+    for name, h, lim in cases:
+        want = (rh.MODE_BF16X2 if h.quantized else rh.MODE_BF16X3) if lim >= 8.0 else rh.MODE_F16X2
+        print(f"{name}: bf16 limit {lim:.2f} -> auto mode {h.auto_mode()}", flush=True)
+        assert h.auto_mode() == want
+        assert h.default_mode == rh.MODE_AUTO
+        np.testing.assert_array_equal(h.logits(a), h.logits(a, want))
+        d_auto, d_want = h.decode(a, off), h.decode(a, off, mode=want)
+        for key in ("idx", "maxprob", "score"):
+            np.testing.assert_array_equal(d_auto[key], d_want[key])
+        for x, y in zip(d_auto["seqs"], d_want["seqs"]):
+            np.testing.assert_array_equal(x, y)
+        h.close()
