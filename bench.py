@@ -26,7 +26,8 @@ for _p in (ROOT, os.path.join(ROOT, "rust-ppocrv6_amd")):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
-MODE_NAMES = {0: "f32", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3", 4: "f16x2"}
+MODE_NAMES = {0: "f32", 1: "bf16x1", 2: "bf16x2", 3: "bf16x3", 4: "f16x2", 5: "auto"}
+TERMS = {1: 1, 2: 2, 3: 3, 4: 2}  # MFMA products per logit of an INT8 head in each mode
 
 
 def parse():
@@ -35,7 +36,8 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="dense_256")
-    p.add_argument("--mode", type=int, default=2, help="0 fp32 FMA, 1/2/3 bf16 terms, 4 two fp16 terms")
+    p.add_argument("--mode", type=int, default=5,
+                   help="0 fp32 FMA, 1/2/3 bf16 terms, 4 two fp16 terms, 5 auto (the library's default)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-others", action="store_true", help="skip the other configurations")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -95,6 +97,29 @@ def agreement(wk, q, s, ref, gpu):
             "score_max_abs_diff": float(np.abs(ref["score"] - gpu["score"]).max())}
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def fp32_accuracy(samples):
+    """Config fp32_64's variants against the oracle (the C restatement of the reference's
+    FP32 matmul_transposed_b, src/ops/matmul.rs:514-897) on the sampled rows their logits
+    were kept for: max |GPU logit - oracle logit|."""
+    from oracle import oracle as orc
+    out = {}
+    for variant, (rows, a, w_t, bias, got) in samples.items():
+        ref = orc.matmul_transposed_b(a[rows], w_t, bias)
+        out[variant] = {"logits_max_abs_vs_oracle": float(np.abs(got - ref).max()), "rows_checked": int(rows.size)}
+    return out
+
+
 def cpu_baseline(wk, q, s, seconds, gpu=None):
     """The oracle's line-parallel head (one line per worker, inner serial, as
     src/pipeline.rs:417-433): whole passes over the same batch, repeated to about
@@ -115,6 +140,7 @@ def cpu_baseline(wk, q, s, seconds, gpu=None):
         orc.rechead_lines(a, off, q, s, wk["bias"], exec_threads=threads)
     dt = time.perf_counter() - t0
     out = {"value": round(passes * rows / dt, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+           "cpu_model": cpu_model(),
            "sample": f"{passes} passes over the batch ({lines} lines x T=120 = {rows} rows each, "
                      f"{passes * rows} rows), INT8 AVX2 path of the reference restated in C, one line per "
                      f"OpenMP thread, {dt:.1f} s"}
@@ -174,9 +200,11 @@ def make_workload(name):
     return wl.make(name, pack=pack if name == "stress_1024" else None)
 
 
-def other_config(name, modes, steps, warmup):
+def other_config(name, modes, steps, warmup, samples=None):
     """Fused decode step (argmax + CTC) of another configuration, per mode; for an FP32
-    head also the logits kernel alone (the unfused projection)."""
+    head also the logits kernel alone (the unfused projection), whose logits of a row
+    sample (the first and last 128 rows and 256 seeded others) go to `samples` for the
+    accuracy check; for a head whose mode has a precision guard, the rows over it."""
     import ppocr_rechead as rh
     from ppocr_rechead import workloads as wl
     from ppocr_rechead.hip import DeviceArray, Stream
@@ -198,7 +226,9 @@ def other_config(name, modes, steps, warmup):
     doff = DeviceArray.from_numpy(wk["line_off"])
     didx, dmp, dseq = DeviceArray((m,), np.int32), DeviceArray((m,), np.float32), DeviceArray((m,), np.int32)
     dlen, dscore = DeviceArray((lines,), np.int64), DeviceArray((lines,), np.float32)
-    res = {"rows": m, "lines": lines, "head": "int8" if wk["quantized"] else "fp32"}
+    res = {"rows": m, "lines": lines, "head": "int8" if wk["quantized"] else "fp32",
+           "auto_mode": MODE_NAMES[head.auto_mode()]}
+    amax = np.abs(a).max(axis=1)
     for mode in modes:
         ws = head.workspace_bytes(m, mode)
         dws = DeviceArray((max(ws, 1),), np.uint8)
@@ -211,6 +241,10 @@ def other_config(name, modes, steps, warmup):
         flops = 2.0 * m * n * k
         r = {"ms_per_step": round(ms, 4), "rows_per_s": round(m / (ms / 1e3), 1),
              "TFLOPs": round(flops / (ms / 1e3) / 1e12, 2)}
+        lim, _ = head.guard_limits(mode)
+        if np.isfinite(lim):
+            r["guarded_rows"] = int((amax > lim).sum())
+            r["guard_limit"] = round(lim, 4)
         if wk["quantized"] and m <= 8192:
             # the same step from host arrays (ppocr_rh_decode): what one call per page costs
             off = wk["line_off"]
@@ -230,6 +264,12 @@ def other_config(name, modes, steps, warmup):
             lb = 4.0 * m * n + 4.0 * m * k + 4.0 * n * k + 4.0 * n
             r["logits_ms"] = round(ms_l, 4)
             r["logits_GBps"] = round(lb / (ms_l / 1e3) / 1e9, 1)
+            if samples is not None:
+                rng = np.random.default_rng(0x5EED0200)
+                rows = np.unique(np.concatenate([np.arange(min(128, m)), np.arange(max(0, m - 128), m),
+                                                 rng.integers(0, m, 256)]))
+                samples["fp32_fma" if mode == 0 else MODE_NAMES[mode]] = (rows, a, wk["w_t"], wk["bias"],
+                                                                          dlog.numpy()[rows])
             dlog.free()
         res["fp32_fma" if mode == 0 else MODE_NAMES[mode]] = r
         dws.free()
@@ -257,6 +297,7 @@ def main():
     qw = rh.QuantizedWeight.from_f32_transposed(wk["w_t"])  # GPU packer
     head = rh.RecHead(qw=qw, bias=wk["bias"])
     mode = args.mode
+    rmode = head.auto_mode() if mode == 5 else mode  # the arithmetic the mode runs on this head
 
     stream = Stream()
     st = stream.h
@@ -350,20 +391,33 @@ def main():
     peaks = measured_peaks() if args.only == "" else None
 
     others = None
+    fp32_samples = {}
     if args.only == "" and not args.no_others:
-        others = {"single_line": other_config("single_line", (2,), args.steps, args.warmup),
-                  "a4_page": other_config("a4_page", (2, 3), args.steps, args.warmup),
-                  "fp32_64": other_config("fp32_64", (0, 3), args.steps, args.warmup),
-                  "stress_1024": other_config("stress_1024", (2,), max(3, args.steps // 4), 2)}
+        others = {"single_line": other_config("single_line", (2, 4), args.steps, args.warmup),
+                  "a4_page": other_config("a4_page", (2, 3, 4), args.steps, args.warmup),
+                  args.workload: other_config(args.workload, tuple(x for x in (2, 3, 4) if x != rmode),
+                                              args.steps, args.warmup),
+                  "fp32_64": other_config("fp32_64", (0, 3, 4), args.steps, args.warmup, fp32_samples),
+                  "stress_1024": other_config("stress_1024", (2, 4), max(3, args.steps // 4), 2)}
 
     cpu = None
     if not args.no_cpu and args.only == "":
         cpu = cpu_baseline(wk, qw.data, qw.scales, args.cpu_seconds, gpu_res if "fused" in out else None)
+        if fp32_samples:
+            for variant, acc in fp32_accuracy(fp32_samples).items():
+                others["fp32_64"][variant].update(acc)
 
     if "fused" in out:
         ms_step, wall_ms, ms_head = out["fused"]
         achieved = flops / (ms_head / 1e3) / 1e12
-        peak = FP32_PEAK_TFLOPS if mode == 0 else BF16_PEAK_TFLOPS
+        peak = FP32_PEAK_TFLOPS if rmode == 0 else BF16_PEAK_TFLOPS
+        ceiling = None
+        if peaks and rmode in TERMS:
+            # t products per logit: at most 1/t of the measured dense MFMA rate is useful work
+            t = TERMS[rmode]
+            ceiling = {"terms": t, "measured_mfma_TFLOPs": peaks["bf16_mfma_TFLOPs"],
+                       "ceiling_TFLOPs": round(peaks["bf16_mfma_TFLOPs"] / t, 1),
+                       "frac_of_ceiling": round(achieved / (peaks["bf16_mfma_TFLOPs"] / t), 4)}
         line = {
             "metric": "rec-head rows/s (B*T x 18710 INT8 proj+softmax+CTC)",
             "value": round(m / (ms_step / 1e3), 1),
@@ -375,16 +429,18 @@ def main():
             "higher_is_better": True,
             "scaling": "weak",
             "vs_baseline": None,
-            "dtype": MODE_NAMES[mode] + " MFMA, f32 accumulate, int8 weights" if mode else "f32 FMA, int8 weights",
+            "dtype": MODE_NAMES[rmode] + " MFMA, f32 accumulate, int8 weights" if rmode else "f32 FMA, int8 weights",
             "data": "synthetic (seeded N(0,1) activations, N(0,0.05^2) weights packed to INT8 on the GPU)",
             "config": {"workload": f"{args.workload}: {lines} lines x T=120, m={m}, k={k}, n={n}, fused "
-                                   "projection+softmax-max+argmax+CTC", "mode": mode},
-            "roofline": {"bound": "mfma" if mode else "valu",
+                                   "projection+softmax-max+argmax+CTC",
+                       "mode": MODE_NAMES[mode] + (f" ({MODE_NAMES[rmode]})" if mode == 5 else "")},
+            "roofline": {"bound": "mfma" if rmode else "valu",
                          "kernel": "ppocr_rh_argmax_dev: stats_main_kernel (>= 95% of the time) + "
                                    "guarded-row rescue and merge kernels",
                          "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles("stats_main_kernel_dense_256"),
-                         "algorithmic_flops_per_launch": flops, "kernel_ms": round(ms_head, 5)},
+                         "algorithmic_flops_per_launch": flops, "kernel_ms": round(ms_head, 5),
+                         "split_ceiling": ceiling},
             "measured_peaks": peaks,
             "wall_ms_per_step": round(wall_ms, 5),
             "host_arrays": host,

@@ -123,6 +123,11 @@ int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized);
  * PPOCR_MODE_F16X2), -1 for a null handle.  No counterpart in the reference, whose CPU
  * kernels have one precision. */
 int ppocr_rh_auto_mode(const ppocr_rh_t* h);
+/* The precision guard of `mode` on this head: rows whose max |a| exceeds *stats_limit go to
+ * the rescue pass in argmax / decode / probabilities, rows above *logits_limit in logits
+ * (INFINITY: the mode has no guard).  No counterpart in the reference; for callers that
+ * want to know how many rows of a batch take the slower path. */
+int ppocr_rh_guard_limits(const ppocr_rh_t* h, int mode, float* stats_limit, float* logits_limit);
 
 /* Device workspace needed by the `_dev` entry points below for m rows (0 if none).  A
  * NULL workspace makes the call allocate one on its stream (stream-ordered) and free it

@@ -860,6 +860,22 @@ int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized) 
 
 int ppocr_rh_auto_mode(const ppocr_rh_t* h) { return h ? auto_mode(h) : -1; }
 
+int ppocr_rh_guard_limits(const ppocr_rh_t* h, int mode, float* stats_limit, float* logits_limit) {
+    if (!h || !stats_limit || !logits_limit) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+    int cfg;
+    if (int e = mode_cfg(h, mode, &cfg)) return e;
+    *stats_limit = *logits_limit = INFINITY;
+    if (cfg == CFG_Q2 || cfg == CFG_H2 || cfg == CFG_F3 || cfg == CFG_HF3) {
+        const float prec = cfg_is_f16(cfg) ? h->amax_limit_h : h->amax_limit;
+        *logits_limit = prec;
+        // the two-term INT8 statistics pass skips the reference shift when the head has a
+        // logit range bound, and then also rescues the rows that could leave that range
+        const bool noref = h->range_ok && (cfg == CFG_Q2 || cfg == CFG_H2);
+        *stats_limit = noref ? std::min(prec, h->range_limit) : prec;
+    }
+    return PPOCR_OK;
+}
+
 size_t ppocr_rh_workspace_bytes(const ppocr_rh_t* h, int64_t m, int mode) {
     if (!h || m <= 0) return 0;
     int cfg;

@@ -2,6 +2,8 @@
 // transpose (src/engine/model.rs:565-605), the precision and range limits of the split
 // activation modes, and the MFMA tile records.  Each produces exactly what the host path
 // of ppocr_rh_create / ppocr_rh_create_f32 computes from host arrays.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace ppocr {
@@ -35,65 +37,90 @@ int launch_transpose(const float* src, int64_t rows, int64_t cols, float* dst, h
     return PPOCR_OK;
 }
 
-// Per class row j (one wave per row), for the guard limits of the split-activation modes:
-// the largest |dequantised weight| (float; (float)max|q| * scale for an INT8 head), the L1
-// and L2 norms of the dequantised row and |bias|, in double (NaN ignored).  An INT8 row's
-// sums are exact integers scaled once; an FP32 row's are summed in a fixed order (lane
-// strides, then xor shuffles), so every call gives the same bits.  Maxima of non-negative
-// values are taken on their bit patterns, which order the same way.
+// Per class row j (one wave per row, rows strided over the grid), for the guard limits of
+// the split-activation modes: the largest |dequantised weight| (float; (float)max|q| *
+// scale for an INT8 head), the L1 and L2 norms of the dequantised row and |bias|, in
+// double (NaN ignored).  An INT8 row's sums are exact integers scaled once; an FP32 row's
+// are summed in a fixed order (lane strides, then xor shuffles), so every call gives the
+// same bits.  Each wave keeps its maxima, the workgroup combines its four in LDS and one
+// thread publishes them with atomic maxima (one set per workgroup: the four result words
+// would serialise an atomic per row).  Maxima of non-negative values are taken on their
+// bit patterns, which order the same way.
+constexpr int kLimitBlocks = 512;
 __global__ __launch_bounds__(256) void head_limits_kernel(const int8_t* __restrict__ q, const float* __restrict__ w,
                                                           const float* __restrict__ scales,
                                                           const float* __restrict__ bias, int64_t n, int64_t k,
                                                           HeadLimitBits* __restrict__ out) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= n) return;
-    float wm;
-    double w1, l2;
-    if (q) {
-        int qm = 0, s1 = 0, s2 = 0;
-        for (int64_t i = lane; i < k; i += 64) {
-            const int v = abs((int)q[row * k + i]);
-            qm = max(qm, v);
-            s1 += v;
-            s2 += v * v;
-        }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned wm_bits = 0;
+    unsigned long long w1_bits = 0, l2_bits = 0, b_bits = 0;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < n; row += (int64_t)gridDim.x * 4) {
+        float wm;
+        double w1, l2;
+        if (q) {
+            int qm = 0, s1 = 0, s2 = 0;
+            for (int64_t i = lane; i < k; i += 64) {
+                const int v = abs((int)q[row * k + i]);
+                qm = max(qm, v);
+                s1 += v;
+                s2 += v * v;
+            }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            qm = max(qm, __shfl_xor(qm, o, 64));
-            s1 += __shfl_xor(s1, o, 64);
-            s2 += __shfl_xor(s2, o, 64);
-        }
-        wm = __fmul_rn((float)qm, scales[row]);
-        w1 = (double)s1 * (double)scales[row];
-        l2 = __dsqrt_rn((double)s2) * (double)scales[row];
-    } else {
-        float m = 0.0f;
-        double s1 = 0.0, s2 = 0.0;
-        for (int64_t i = lane; i < k; i += 64) {
-            const float v = fabsf(w[row * k + i]);
-            m = fmaxf(m, v);
-            s1 += (double)v;
-            s2 = fma((double)v, (double)v, s2);
-        }
+            for (int o = 32; o >= 1; o >>= 1) {
+                qm = max(qm, __shfl_xor(qm, o, 64));
+                s1 += __shfl_xor(s1, o, 64);
+                s2 += __shfl_xor(s2, o, 64);
+            }
+            wm = __fmul_rn((float)qm, scales[row]);
+            w1 = (double)s1 * (double)scales[row];
+            l2 = __dsqrt_rn((double)s2) * (double)scales[row];
+        } else {
+            float m = 0.0f;
+            double s1 = 0.0, s2 = 0.0;
+            for (int64_t i = lane; i < k; i += 64) {
+                const float v = fabsf(w[row * k + i]);
+                m = fmaxf(m, v);
+                s1 += (double)v;
+                s2 = fma((double)v, (double)v, s2);
+            }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            m = fmaxf(m, __shfl_xor(m, o, 64));
-            s1 += __shfl_xor(s1, o, 64);
-            s2 += __shfl_xor(s2, o, 64);
+            for (int o = 32; o >= 1; o >>= 1) {
+                m = fmaxf(m, __shfl_xor(m, o, 64));
+                s1 += __shfl_xor(s1, o, 64);
+                s2 += __shfl_xor(s2, o, 64);
+            }
+            wm = m;
+            w1 = s1;
+            l2 = __dsqrt_rn(s2);
         }
-        wm = m;
-        w1 = s1;
-        l2 = __dsqrt_rn(s2);
-    }
-    if (lane == 0) {
-        if (wm == wm) atomicMax(&out->wmax, __float_as_uint(wm));
-        if (w1 == w1) atomicMax(&out->w1, (unsigned long long)__double_as_longlong(w1));
-        if (l2 == l2) atomicMax(&out->l2, (unsigned long long)__double_as_longlong(l2));
+        if (wm == wm) wm_bits = max(wm_bits, __float_as_uint(wm));
+        if (w1 == w1) w1_bits = max(w1_bits, (unsigned long long)__double_as_longlong(w1));
+        if (l2 == l2) l2_bits = max(l2_bits, (unsigned long long)__double_as_longlong(l2));
         if (bias) {
             const double b = fabs((double)bias[row]);
-            if (b == b) atomicMax(&out->bmax, (unsigned long long)__double_as_longlong(b));
+            if (b == b) b_bits = max(b_bits, (unsigned long long)__double_as_longlong(b));
         }
+    }
+    __shared__ unsigned s_wm[4];
+    __shared__ unsigned long long s_w1[4], s_l2[4], s_b[4];
+    if (lane == 0) {
+        s_wm[wave] = wm_bits;
+        s_w1[wave] = w1_bits;
+        s_l2[wave] = l2_bits;
+        s_b[wave] = b_bits;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int x = 1; x < 4; ++x) {
+            wm_bits = max(wm_bits, s_wm[x]);
+            w1_bits = max(w1_bits, s_w1[x]);
+            l2_bits = max(l2_bits, s_l2[x]);
+            b_bits = max(b_bits, s_b[x]);
+        }
+        atomicMax(&out->wmax, wm_bits);
+        atomicMax(&out->w1, w1_bits);
+        atomicMax(&out->l2, l2_bits);
+        if (bias) atomicMax(&out->bmax, b_bits);
     }
 }
 
@@ -102,7 +129,8 @@ int launch_head_limits(const int8_t* q, const float* w, const float* scales, con
     if (n <= 0) return PPOCR_OK;
     if ((n + 3) / 4 > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: too many classes");
     if (!q && !w) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: no weights");
-    head_limits_kernel<<<(unsigned)((n + 3) / 4), 256, 0, st>>>(q, w, scales, bias, n, k, out);
+    head_limits_kernel<<<(unsigned)std::min<int64_t>((n + 3) / 4, kLimitBlocks), 256, 0, st>>>(q, w, scales, bias,
+                                                                                             n, k, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

@@ -107,8 +107,9 @@ class RecHead:
     """The head weight resident in HBM: what Model keeps for MatMul.12 plus its folded bias.
 
     Build it once (INT8: from a QuantizedWeight; FP32: from W^T), then run any number of
-    batches.  `mode` picks the arithmetic (MODE_BF16X2 default for INT8, MODE_BF16X3 for
-    FP32)."""
+    batches.  `mode` picks the arithmetic; the default, MODE_AUTO, takes the bf16 split
+    (MODE_BF16X2 for INT8, MODE_BF16X3 for FP32) or MODE_F16X2, whichever the head's weights
+    suit (auto_mode())."""
 
     def __init__(self, qw=None, bias=None, w_t=None, device=0):
         self._h = ctypes.c_void_p()
@@ -189,6 +190,14 @@ class RecHead:
     def auto_mode(self):
         """The mode MODE_AUTO (the default) runs for this head's weights."""
         return int(_lib.lib().ppocr_rh_auto_mode(self._h))
+
+    def guard_limits(self, mode=None):
+        """(stats_limit, logits_limit): rows whose max |a| exceeds them take the rescue pass
+        of argmax / decode / probabilities, resp. of logits (inf: no guard in this mode)."""
+        st, lg = ctypes.c_float(), ctypes.c_float()
+        _check(_lib.lib().ppocr_rh_guard_limits(self._h, self.default_mode if mode is None else mode,
+                                                ctypes.byref(st), ctypes.byref(lg)))
+        return float(st.value), float(lg.value)
 
     def workspace_bytes(self, m, mode=None):
         return int(_lib.lib().ppocr_rh_workspace_bytes(self._h, m, self.default_mode if mode is None else mode))

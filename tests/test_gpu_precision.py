@@ -262,6 +262,27 @@ def test_tiny_activations(orc, rh, head, mode):
     assert_close_rel(mp, r["maxprob"], f"tiny maxprob mode {mode}")
 
 
+def test_guard_limits_query(orc, rh):
+    """ppocr_rh_guard_limits reports the limits the kernels apply: for the INT8 head the
+    precision limits of the bf16 and fp16 splits (logits) and, for the statistics pass,
+    the lower of those and the logit range bound (60 - 1.001 max|bias|) / (1.001 max_c
+    ||w_c||_1); no guard (inf) in the one- and three-term modes and in fp32 FMA."""
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights(stress=True)
+    q, s = orc.pack_int8(w_t)
+    h = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    wd = np.abs(q.astype(np.float64)) * s.astype(np.float64)[:, None]
+    rng_lim = (60.0 - 1.001 * float(np.abs(bias).max())) / (1.001 * float(wd.sum(axis=1).max()))
+    for mode, prec in ((2, _int8_limit(q, s)), (4, _f16_limit_int8(q, s))):
+        st, lg = h.guard_limits(mode)
+        print(f"mode {mode}: stats limit {st:.4f}, logits limit {lg:.4f} (precision {prec:.4f}, range {rng_lim:.4f})")
+        assert abs(lg - prec) <= 1e-5 * prec
+        assert abs(st - min(prec, rng_lim)) <= 1e-5 * min(prec, rng_lim)
+    for mode in (0, 1, 3):
+        assert h.guard_limits(mode) == (np.inf, np.inf)
+    h.close()
+
+
 def test_f16x2_outlier_head_needs_no_rescue_for_ordinary_rows(orc, rh):
     """The stress head (0.5% of its classes hold a single +-5 weight): with fp16 terms its
     precision limit stays far above ordinary rows' magnitudes, and the logits of N(0,1) rows
@@ -308,6 +329,10 @@ def test_auto_mode_picks_per_head_and_matches_the_explicit_mode(orc, rh):
         print(f"{name}: bf16 limit {lim:.2f} -> auto mode {h.auto_mode()}", flush=True)
         assert h.auto_mode() == want
         assert h.default_mode == rh.MODE_AUTO
+        st, lg = h.guard_limits(want)
+        assert st <= lg and (st == lg or h.quantized)
+        if want != rh.MODE_F16X2:
+            assert abs(lg - lim) <= 1e-5 * lim, (lg, lim)
         np.testing.assert_array_equal(h.logits(a), h.logits(a, want))
         d_auto, d_want = h.decode(a, off), h.decode(a, off, mode=want)
         for key in ("idx", "maxprob", "score"):
