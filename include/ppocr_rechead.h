@@ -43,7 +43,7 @@ extern "C" {
 typedef enum {
     PPOCR_MODE_FP32_FMA = 0, /* fp32 vector FMA over dequantised weights */
     PPOCR_MODE_BF16X1 = 1,   /* bf16 MFMA, activation rounded to 1 bf16 term */
-    PPOCR_MODE_BF16X2 = 2,   /* bf16 MFMA, activation split into 2 bf16 terms (default) */
+    PPOCR_MODE_BF16X2 = 2,   /* bf16 MFMA, activation split into 2 bf16 terms */
     PPOCR_MODE_BF16X3 = 3,   /* bf16 MFMA, activation split into 3 bf16 terms; for an
                                 FP32 head, a_hi*w_hi + a_hi*w_lo + a_lo*w_hi */
     PPOCR_MODE_F16X2 = 4,    /* fp16 MFMA, activation split into 2 fp16 terms (22 bits of
@@ -249,6 +249,73 @@ int ppocr_rh_decode_nct_dev(const ppocr_rh_t* h, const float* d_x, int64_t lines
                             int mode, int32_t* d_idx, float* d_maxprob, int32_t* d_seq,
                             int64_t* d_seq_len, float* d_score, void* d_workspace,
                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- the SVTR neck tail
+ * The recognition model's mixing tail before the head, PP-OCRv6_small_rec's graph from
+ * Transpose.0 (perm [0,2,1]) to Transpose.8: `blocks` transformer blocks over the T tokens
+ * of each text line,
+ *     x = x + proj(attention(LayerNorm1(x)))      LayerNorm, MatMul.0 + Add (qkv), Reshape
+ *                                                 [0,-1,3,heads,dim/heads], Mul(scale),
+ *                                                 MatMul(q, k^T), Softmax over the keys,
+ *                                                 MatMul(p, v), MatMul.3 + Add
+ *     x = x + fc2(swish(fc1(LayerNorm2(x))))      MatMul.4 + Add, Sigmoid and Mul, MatMul.5 + Add
+ * then the final LayerNorm plus the convolution shortcut (Add.202), whose sum, as token
+ * rows, is the input of the head's MatMul.12.  The reference runs these nodes one by one in
+ * its executor (Model::forward, src/engine/model.rs: MatMul 1245-1272, LayerNorm 1274-1284
+ * after the fusion of src/engine/model.rs:2143-2245, Softmax 1286-1302, Sigmoid 953-963;
+ * src/ops/layernorm.rs:5-244, src/ops/matmul.rs:9-96, src/ops/softmax.rs:199-285,
+ * src/ops/activation.rs:25-94).  All arithmetic is fp32.  The kernels are built for
+ * dim = 120, 8 heads of 15 and hidden = 240 (PPOCR_ERR_INVALID_ARG otherwise). */
+typedef struct ppocr_rn ppocr_rn_t;
+
+/* Input and output layouts of the neck (per text line b with T_b steps, the lines packed
+ * back to back, line b starting at token row t0_b). */
+#define PPOCR_NECK_ROWS 0           /* token rows [m][dim] (the tensor after Transpose.0) */
+#define PPOCR_NECK_CHANNELS_FIRST 1 /* line b as [dim][T_b] at dim * t0_b (the graph's
+                                       [1, dim, T] flatten output and shortcut) */
+
+/* One block's weights, host pointers, MatMul weights row-major [K][N] as the model stores
+ * them: ln1 (w, b [dim], eps), qkv [dim][3 dim] + [3 dim], proj [dim][dim] + [dim],
+ * ln2, fc1 [dim][hidden] + [hidden], fc2 [hidden][dim] + [dim]. */
+typedef struct {
+    const float* ln1_w;
+    const float* ln1_b;
+    float ln1_eps;
+    const float* qkv_w;
+    const float* qkv_b;
+    const float* proj_w;
+    const float* proj_b;
+    const float* ln2_w;
+    const float* ln2_b;
+    float ln2_eps;
+    const float* fc1_w;
+    const float* fc1_b;
+    const float* fc2_w;
+    const float* fc2_b;
+} ppocr_rn_block_t;
+
+/* The neck's weights resident in HBM (Model keeps them in its weight map,
+ * src/engine/loader.rs:34-92).  scale: the attention's Mul constant. */
+int ppocr_rn_create(const ppocr_rn_block_t* blocks, int nblocks, const float* lnf_w, const float* lnf_b,
+                    float lnf_eps, int64_t dim, int64_t heads, int64_t hidden, float scale, int device,
+                    ppocr_rn_t** out);
+/* The neck of a model file: the transformer blocks, the final LayerNorm and the shortcut
+ * Add found in its graph between Transpose.0 and the head (PPOCR_ERR_MODEL when the graph
+ * has no such tail, e.g. PP-OCRv6_tiny_rec), weights uploaded from the file. */
+int ppocr_rn_create_from_model(const char* path, int device, ppocr_rn_t** out);
+void ppocr_rn_destroy(ppocr_rn_t* h);
+/* dim, heads, hidden and the number of blocks. */
+int ppocr_rn_shape(const ppocr_rn_t* h, int64_t* dim, int64_t* heads, int64_t* hidden, int* blocks);
+/* Device workspace of ppocr_rn_forward_dev for m token rows. */
+size_t ppocr_rn_workspace_bytes(const ppocr_rn_t* h, int64_t m);
+/* out [m][dim] token rows = the tail applied to x and shortcut (both in `layout`), lines
+ * by d_line_off[0..lines] (read on the device, clamped into [0, m]; attention never mixes
+ * tokens of different lines). */
+int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_shortcut, int64_t m,
+                         const int64_t* d_line_off, int64_t lines, int layout, float* d_out, void* d_workspace,
+                         size_t workspace_bytes, void* stream);
+int ppocr_rn_forward(const ppocr_rn_t* h, const float* x, const float* shortcut, const int64_t* line_off,
+                     int64_t lines, int layout, float* out);
 
 #ifdef __cplusplus
 }

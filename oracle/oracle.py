@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  The oracle restates the reference's CPU path for the
 recognition head (packer, W8A32 projection, FP32 projection, softmax, argmax, CTC
-collapse) with the reference's own AVX2 intrinsic sequence.  Only tests/, the smoke
+collapse) with the reference's own AVX2 intrinsic sequence, and the SVTR neck tail before
+it (LayerNorm, sigmoid, the activation MatMuls, attention) from the same pieces.  Only tests/, the smoke
 check in __graft_entry__.py and the CPU-baseline leg of bench.py import this module;
 the product package never does.
 """
@@ -52,6 +53,10 @@ def lib():
         L.orc_rechead_lines.argtypes = [_f32p, _i64p, _i64, _i8p, _f32p, ctypes.c_void_p, _i64, _i64,
                                         _int, _int, _i32p, _f32p, _i32p, _i64p, _f32p, ctypes.c_void_p]
         L.orc_rechead_lines.restype = None
+        L.orc_layer_norm_rows.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, ctypes.c_float, _int, _f32p]
+        L.orc_layer_norm_rows.restype = None
+        L.orc_sigmoid.argtypes = [_f32p, _i64, _f32p]
+        L.orc_sigmoid.restype = None
         _lib = L
     return _lib
 
@@ -189,3 +194,78 @@ def rechead_lines(a, line_off, q, scales, bias, use_avx2=True, exec_threads=None
     seqs = [seq[line_off[b]:line_off[b] + seq_len[b]].copy() for b in range(lines)]
     return {"idx": idx[:rows], "maxprob": maxprob[:rows], "seqs": seqs, "score": score[:lines],
             "probs": probs}
+
+
+# ---------------------------------------------------------------- the SVTR neck tail
+def layer_norm_rows(x, w, b, eps, use_avx2=True):
+    """layer_norm over the last axis (src/ops/layernorm.rs:5-244)."""
+    x = _c(x, np.float32)
+    n = x.shape[-1]
+    out = np.empty_like(x)
+    if x.size:
+        lib().orc_layer_norm_rows(x.reshape(-1), x.size // n, n, _c(w, np.float32), _c(b, np.float32),
+                                  float(eps), int(bool(use_avx2)), out.reshape(-1))
+    return out
+
+
+def sigmoid(x):
+    """sigmoid_inplace (src/ops/activation.rs:31-94) on a copy."""
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    if x.size:
+        lib().orc_sigmoid(x.reshape(-1), x.size, out.reshape(-1))
+    return out
+
+
+def matmul_act(a, w):
+    """MatMul of an activation by a weight or another activation (matmul_with_bias without
+    bias, src/ops/matmul.rs:9-96, whose parallel_sgemm_2d / gemm_row_major blocking is not
+    restated): the products summed in float64 and rounded once to float32, the correctly
+    rounded value every fp32 summation order approximates."""
+    return (np.asarray(a, np.float64) @ np.asarray(w, np.float64)).astype(np.float32)
+
+
+def linear(a, w, bias):
+    """MatMul then Add(bias), two nodes and two roundings (src/engine/model.rs:1245-1272)."""
+    return (matmul_act(a, w) + _c(bias, np.float32)).astype(np.float32)
+
+
+def attention_line(qkv, heads, scale):
+    """The attention of one line's T tokens (graph nodes Reshape [0,-1,3,H,D/H], Transpose
+    [2,0,3,1,4], Mul(scale), MatMul(q, k^T), Softmax over the keys (softmax_inplace,
+    src/ops/softmax.rs:199-285), MatMul(p, v), Transpose [0,2,1,3], Reshape [0,-1,D]):
+    qkv [T][3D] -> [T][D]."""
+    t, d3 = qkv.shape
+    d = d3 // 3
+    hd = d // heads
+    x = qkv.reshape(t, 3, heads, hd).transpose(1, 2, 0, 3)  # [3][H][T][hd]
+    out = np.empty((heads, t, hd), np.float32)
+    for h in range(heads):
+        q = (x[0, h] * np.float32(scale)).astype(np.float32)
+        s = matmul_act(q, x[1, h].T)
+        p = softmax_rows(s)
+        out[h] = matmul_act(p, x[2, h])
+    return out.transpose(1, 0, 2).reshape(t, d)
+
+
+def svtr_neck(x, shortcut, line_off, blocks, lnf_w, lnf_b, lnf_eps, heads, scale):
+    """The SVTR tail on token rows x [m][D] (after Transpose.0), lines by line_off, blocks a
+    list of dicts with the fields of ppocr_rn_block_t: per block
+    x = x + proj(attention(LN1(x))), x = x + fc2(swish(fc1(LN2(x)))) (swish = Mul(h,
+    Sigmoid(h))); then LN(x) + shortcut (rows [m][D])."""
+    x = _c(x, np.float32).copy()
+    line_off = np.asarray(line_off, np.int64)
+    for b in blocks:
+        y = layer_norm_rows(x, b["ln1_w"], b["ln1_b"], b["ln1_eps"])
+        qkv = linear(y, b["qkv_w"], b["qkv_b"])
+        att = np.zeros_like(x)
+        for i in range(line_off.size - 1):
+            t0, t1 = int(line_off[i]), int(line_off[i + 1])
+            if t1 > t0:
+                att[t0:t1] = attention_line(qkv[t0:t1], heads, scale)
+        x = (x + linear(att, b["proj_w"], b["proj_b"])).astype(np.float32)
+        y = layer_norm_rows(x, b["ln2_w"], b["ln2_b"], b["ln2_eps"])
+        h = linear(y, b["fc1_w"], b["fc1_b"])
+        h = (h * sigmoid(h)).astype(np.float32)
+        x = (x + linear(h, b["fc2_w"], b["fc2_b"])).astype(np.float32)
+    return (layer_norm_rows(x, lnf_w, lnf_b, lnf_eps) + _c(shortcut, np.float32)).astype(np.float32)

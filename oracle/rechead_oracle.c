@@ -525,6 +525,83 @@ static void softmax_row_scalar(float* row, int64_t n) {
 
 /* softmax_inplace over contiguous rows, src/ops/softmax.rs:199-285 (an empty tensor is a
  * no-op, 226-229). */
+/* compute_layer_norm_row_fma, src/ops/layernorm.rs:146-244: 8-lane sums of x, the lanes
+ * added in order, the scalar tail; the same for fma(d, d, .) of the differences; inv_std =
+ * 1 / sqrt(var + eps); out = fma((x - mean) * inv_std, w, b) in 8-wide steps, scalar tail
+ * ((x - mean) * inv_std) * w + b. */
+static void layer_norm_row_avx2(const float* x, int64_t n, const float* w, const float* b, float eps, float* out) {
+    __m256 vs = _mm256_setzero_ps();
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) vs = _mm256_add_ps(vs, _mm256_loadu_ps(x + i));
+    float buf[8];
+    _mm256_storeu_ps(buf, vs);
+    float sum = 0.0f;
+    for (int l = 0; l < 8; ++l) sum += buf[l];
+    for (; i < n; ++i) sum += x[i];
+    const float mean = sum / (float)n;
+    const __m256 vm = _mm256_set1_ps(mean);
+    __m256 vv = _mm256_setzero_ps();
+    for (i = 0; i + 8 <= n; i += 8) {
+        const __m256 d = _mm256_sub_ps(_mm256_loadu_ps(x + i), vm);
+        vv = _mm256_fmadd_ps(d, d, vv);
+    }
+    _mm256_storeu_ps(buf, vv);
+    float vsum = 0.0f;
+    for (int l = 0; l < 8; ++l) vsum += buf[l];
+    for (; i < n; ++i) {
+        const float d = x[i] - mean;
+        vsum += d * d;
+    }
+    const float var = vsum / (float)n;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    const __m256 vi = _mm256_set1_ps(inv_std);
+    for (i = 0; i + 8 <= n; i += 8) {
+        const __m256 v = _mm256_mul_ps(_mm256_sub_ps(_mm256_loadu_ps(x + i), vm), vi);
+        _mm256_storeu_ps(out + i, _mm256_fmadd_ps(v, _mm256_loadu_ps(w + i), _mm256_loadu_ps(b + i)));
+    }
+    for (; i < n; ++i) {
+        float v = (x[i] - mean) * inv_std;
+        v *= w[i];
+        v += b[i];
+        out[i] = v;
+    }
+}
+
+/* compute_layer_norm_row, src/ops/layernorm.rs:120-144: iterator sums (sequential). */
+static void layer_norm_row_scalar(const float* x, int64_t n, const float* w, const float* b, float eps, float* out) {
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; ++i) sum += x[i];
+    const float mean = sum / (float)n;
+    float vs = 0.0f;
+    for (int64_t i = 0; i < n; ++i) vs += (x[i] - mean) * (x[i] - mean);
+    const float var = vs / (float)n;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    for (int64_t i = 0; i < n; ++i) {
+        float v = (x[i] - mean) * inv_std;
+        v *= w[i];
+        v += b[i];
+        out[i] = v;
+    }
+}
+
+void orc_layer_norm_rows(const float* x, int64_t rows, int64_t n, const float* w, const float* b, float eps,
+                         int use_avx2, float* out) {
+    for (int64_t r = 0; r < rows; ++r) {
+        if (use_avx2) layer_norm_row_avx2(x + r * n, n, w, b, eps, out + r * n);
+        else layer_norm_row_scalar(x + r * n, n, w, b, eps, out + r * n);
+    }
+}
+
+void orc_sigmoid(const float* x, int64_t count, float* out) {
+    const __m256 zero = _mm256_setzero_ps(), one = _mm256_set1_ps(1.0f);
+    int64_t i = 0;
+    for (; i + 8 <= count; i += 8) {
+        const __m256 e = exp_ps_avx2(_mm256_sub_ps(zero, _mm256_loadu_ps(x + i)));
+        _mm256_storeu_ps(out + i, _mm256_div_ps(one, _mm256_add_ps(one, e)));
+    }
+    for (; i < count; ++i) out[i] = 1.0f / (1.0f + expf(-x[i]));
+}
+
 void orc_softmax_rows(float* x, int64_t rows, int64_t n, int use_avx2, int exec_threads) {
     if (rows <= 0 || n <= 0) return;
     if (exec_threads < 1) exec_threads = 1;

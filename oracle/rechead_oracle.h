@@ -51,6 +51,18 @@ void orc_exp_ps(const float* x, int64_t count, float* out);
  * compute_row_avx2 (313-416) or compute_row_scalar (418-436). */
 void orc_softmax_rows(float* x, int64_t rows, int64_t n, int use_avx2, int exec_threads);
 
+/* layer_norm over the last axis of x [rows][n] with weight and bias (both required),
+ * src/ops/layernorm.rs:5-244: rows by compute_layer_norm_row_fma (146-244) with use_avx2,
+ * compute_layer_norm_row (120-144) without. */
+void orc_layer_norm_rows(const float* x, int64_t rows, int64_t n, const float* w, const float* b, float eps,
+                         int use_avx2, float* out);
+
+/* sigmoid_inplace, src/ops/activation.rs:31-94 (sigmoid_avx2_chunk: 16- then 8-wide
+ * 1 / (1 + avx2_exp_ps(0 - x)), scalar tail 1 / (1 + expf(-x))), on `count` floats as one
+ * chunk (the reference's 16384-float rayon chunks are multiples of 8, so only the tensor's
+ * last count % 8 floats take the scalar tail either way). */
+void orc_sigmoid(const float* x, int64_t count, float* out);
+
 /* find_argmax, src/postprocess/ctc.rs:178-258.  Returns the index; *val gets the value. */
 int64_t orc_find_argmax(const float* x, int64_t n, int use_avx2, float* val);
 

@@ -13,6 +13,7 @@
 
 #include "kernels.hpp"
 #include "model_graph.hpp"
+#include "neck.hpp"
 #include "safetensors.hpp"
 
 namespace ppocr {
@@ -1195,6 +1196,258 @@ int ppocr_rh_decode_nct(const ppocr_rh_t* h, const float* x, int64_t lines, int6
                                         hc.out<float>(2), hc.ws(), hc.ws_bytes(), hc.stream()))
         return e;
     return hc.copy_out({seq, seq_len, score, idx, maxprob});
+}
+
+
+// ---------------------------------------------------------------- the SVTR neck tail
+struct ppocr_rn {
+    int device = 0;
+    ppocr::NeckDev dev;
+    float* d_weights = nullptr;  // every weight of the neck in one allocation
+    size_t device_bytes = 0;
+};
+
+namespace {
+
+void free_neck(ppocr_rn* h) {
+    if (!h) return;
+    if (h->d_weights) {
+        DeviceGuard dg(h->device);
+        (void)hipFree(h->d_weights);
+    }
+    delete h;
+}
+
+// Host pointers of the neck's weights, in upload order, with their float counts.
+struct NeckHost {
+    int64_t dim = 0, heads = 0, hidden = 0;
+    float scale = 0.0f, lnf_eps = 0.0f;
+    std::vector<ppocr_rn_block_t> blocks;
+    const float *lnf_w = nullptr, *lnf_b = nullptr;
+};
+
+int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
+    const char* op = "RecNeckHip";
+    if (!out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null output handle");
+    *out = nullptr;
+    if (nh.dim != kNeckDim || nh.hidden != kNeckHidden || nh.heads <= 0 || nh.heads * kNeckHeadDim != nh.dim)
+        return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": unsupported geometry dim " + std::to_string(nh.dim) +
+                                               ", heads " + std::to_string(nh.heads) + ", hidden " +
+                                               std::to_string(nh.hidden) + " (built for 120, 8 x 15, 240)");
+    if (nh.blocks.empty() || nh.blocks.size() > (size_t)kNeckMaxBlocks)
+        return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": 1 to " + std::to_string(kNeckMaxBlocks) + " blocks");
+    if (!nh.lnf_w || !nh.lnf_b || !(nh.scale == nh.scale) || !(nh.lnf_eps >= 0.0f))
+        return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null final LayerNorm or bad constants");
+    const int64_t D = nh.dim, H = nh.hidden;
+    // per block: ln1 w,b (D each), qkv (D*3D + 3D), proj (D*D + D), ln2 (2D), fc1 (D*H + H), fc2 (H*D + D)
+    std::vector<std::pair<const float*, int64_t>> parts;
+    for (const ppocr_rn_block_t& b : nh.blocks) {
+        const float* ptrs[12] = {b.ln1_w, b.ln1_b, b.qkv_w, b.qkv_b, b.proj_w, b.proj_b,
+                                 b.ln2_w, b.ln2_b, b.fc1_w, b.fc1_b, b.fc2_w, b.fc2_b};
+        const int64_t counts[12] = {D, D, D * 3 * D, 3 * D, D * D, D, D, D, D * H, H, H * D, D};
+        for (int i = 0; i < 12; ++i) {
+            if (!ptrs[i]) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null weight pointer");
+            parts.push_back({ptrs[i], counts[i]});
+        }
+        if (!(b.ln1_eps >= 0.0f) || !(b.ln2_eps >= 0.0f))
+            return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": bad LayerNorm epsilon");
+    }
+    parts.push_back({nh.lnf_w, D});
+    parts.push_back({nh.lnf_b, D});
+    int64_t total = 0;
+    for (const auto& pt : parts) total += (pt.second + 3) / 4 * 4;  // each part 16-byte aligned
+    if (device < 0) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": negative device");
+    DeviceGuard dg(device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, std::string(op) + ": hipSetDevice failed");
+    std::unique_ptr<ppocr_rn, void (*)(ppocr_rn*)> h(new (std::nothrow) ppocr_rn, free_neck);
+    if (!h) return fail(PPOCR_ERR_NO_MEMORY, std::string(op) + ": host allocation failed");
+    h->device = device;
+    void* p = nullptr;
+    if (dev_malloc(&p, (size_t)total * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(PPOCR_ERR_NO_MEMORY, std::string(op) + ": device allocation failed");
+    }
+    h->d_weights = static_cast<float*>(p);
+    h->device_bytes = (size_t)total * 4;
+    std::vector<float> host((size_t)total, 0.0f);
+    std::vector<const float*> dev_ptr;
+    int64_t off = 0;
+    for (const auto& pt : parts) {
+        std::memcpy(host.data() + off, pt.first, (size_t)pt.second * 4);
+        dev_ptr.push_back(h->d_weights + off);
+        off += (pt.second + 3) / 4 * 4;
+    }
+    PPOCR_HIP(hipMemcpy(h->d_weights, host.data(), (size_t)total * 4, hipMemcpyHostToDevice));
+    NeckDev& nd = h->dev;
+    nd.dim = (int)D;
+    nd.heads = (int)nh.heads;
+    nd.hidden = (int)H;
+    nd.scale = nh.scale;
+    nd.blocks = (int)nh.blocks.size();
+    size_t q = 0;
+    for (size_t i = 0; i < nh.blocks.size(); ++i) {
+        NeckBlockDev& b = nd.block[i];
+        b.ln1_w = dev_ptr[q++];
+        b.ln1_b = dev_ptr[q++];
+        b.qkv_w = dev_ptr[q++];
+        b.qkv_b = dev_ptr[q++];
+        b.proj_w = dev_ptr[q++];
+        b.proj_b = dev_ptr[q++];
+        b.ln2_w = dev_ptr[q++];
+        b.ln2_b = dev_ptr[q++];
+        b.fc1_w = dev_ptr[q++];
+        b.fc1_b = dev_ptr[q++];
+        b.fc2_w = dev_ptr[q++];
+        b.fc2_b = dev_ptr[q++];
+        b.ln1_eps = nh.blocks[i].ln1_eps;
+        b.ln2_eps = nh.blocks[i].ln2_eps;
+    }
+    nd.lnf_w = dev_ptr[q++];
+    nd.lnf_b = dev_ptr[q++];
+    nd.lnf_eps = nh.lnf_eps;
+    *out = h.release();
+    return PPOCR_OK;
+}
+
+int check_neck(const ppocr_rn_t* h) {
+    if (!h) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null neck handle");
+    return PPOCR_OK;
+}
+
+}  // namespace
+
+int ppocr_rn_create(const ppocr_rn_block_t* blocks, int nblocks, const float* lnf_w, const float* lnf_b,
+                    float lnf_eps, int64_t dim, int64_t heads, int64_t hidden, float scale, int device,
+                    ppocr_rn_t** out) {
+    if (out) *out = nullptr;
+    if (!blocks || nblocks <= 0) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: no blocks");
+    NeckHost nh;
+    nh.dim = dim;
+    nh.heads = heads;
+    nh.hidden = hidden;
+    nh.scale = scale;
+    nh.lnf_w = lnf_w;
+    nh.lnf_b = lnf_b;
+    nh.lnf_eps = lnf_eps;
+    nh.blocks.assign(blocks, blocks + nblocks);
+    return neck_create(nh, device, out);
+}
+
+int ppocr_rn_create_from_model(const char* path, int device, ppocr_rn_t** out) {
+    if (out) *out = nullptr;
+    StFile f;
+    if (int e = f.open(path)) return e;
+    RecNeckNames nn;
+    if (int e = find_rec_neck(f, &nn)) return e;
+    auto vec = [&](const std::string& name, int64_t count, const float** dst) -> int {
+        const StTensor* t = f.find(name.c_str());
+        if (!t || t->dtype != "F32" || (int64_t)(t->bytes / 4) != count)
+            return fail(PPOCR_ERR_MODEL, "Model: tensor '" + name + "' must be F32 with " + std::to_string(count) +
+                                             " values");
+        *dst = reinterpret_cast<const float*>(t->data);  // the map is 4-byte aligned for F32 data
+        return PPOCR_OK;
+    };
+    NeckHost nh;
+    nh.dim = nn.dim;
+    nh.heads = nn.heads;
+    nh.hidden = nn.hidden;
+    nh.scale = nn.scale;
+    nh.lnf_eps = nn.lnf_eps;
+    const int64_t D = nn.dim, H = nn.hidden;
+    // tensor data in the file need not be 4-byte aligned: copy each into owned storage
+    std::vector<std::vector<float>> keep;
+    auto owned = [&](const std::string& name, int64_t count, const float** dst) -> int {
+        const float* src;
+        if (int e = vec(name, count, &src)) return e;
+        keep.emplace_back((size_t)count);
+        std::memcpy(keep.back().data(), src, (size_t)count * 4);
+        *dst = keep.back().data();
+        return PPOCR_OK;
+    };
+    keep.reserve(nn.blocks.size() * 12 + 2);
+    for (const RecNeckBlockNames& b : nn.blocks) {
+        ppocr_rn_block_t hb{};
+        if (int e = owned(b.ln1_w, D, &hb.ln1_w)) return e;
+        if (int e = owned(b.ln1_b, D, &hb.ln1_b)) return e;
+        if (int e = owned(b.qkv_w, D * 3 * D, &hb.qkv_w)) return e;
+        if (int e = owned(b.qkv_b, 3 * D, &hb.qkv_b)) return e;
+        if (int e = owned(b.proj_w, D * D, &hb.proj_w)) return e;
+        if (int e = owned(b.proj_b, D, &hb.proj_b)) return e;
+        if (int e = owned(b.ln2_w, D, &hb.ln2_w)) return e;
+        if (int e = owned(b.ln2_b, D, &hb.ln2_b)) return e;
+        if (int e = owned(b.fc1_w, D * H, &hb.fc1_w)) return e;
+        if (int e = owned(b.fc1_b, H, &hb.fc1_b)) return e;
+        if (int e = owned(b.fc2_w, H * D, &hb.fc2_w)) return e;
+        if (int e = owned(b.fc2_b, D, &hb.fc2_b)) return e;
+        hb.ln1_eps = b.ln1_eps;
+        hb.ln2_eps = b.ln2_eps;
+        nh.blocks.push_back(hb);
+    }
+    if (int e = owned(nn.lnf_w, D, &nh.lnf_w)) return e;
+    if (int e = owned(nn.lnf_b, D, &nh.lnf_b)) return e;
+    return neck_create(nh, device, out);
+}
+
+void ppocr_rn_destroy(ppocr_rn_t* h) { free_neck(h); }
+
+int ppocr_rn_shape(const ppocr_rn_t* h, int64_t* dim, int64_t* heads, int64_t* hidden, int* blocks) {
+    if (int e = check_neck(h)) return e;
+    if (dim) *dim = h->dev.dim;
+    if (heads) *heads = h->dev.heads;
+    if (hidden) *hidden = h->dev.hidden;
+    if (blocks) *blocks = h->dev.blocks;
+    return PPOCR_OK;
+}
+
+size_t ppocr_rn_workspace_bytes(const ppocr_rn_t* h, int64_t m) {
+    if (!h || m <= 0 || m > INT64_MAX / (kNeckWsFloatsPerRow * 4)) return 0;
+    return (size_t)(m * kNeckWsFloatsPerRow * 4);
+}
+
+int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_shortcut, int64_t m,
+                         const int64_t* d_line_off, int64_t lines, int layout, float* d_out, void* d_workspace,
+                         size_t workspace_bytes, void* stream) {
+    if (int e = check_neck(h)) return e;
+    if (m < 0 || lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: negative row or line count");
+    if (layout != PPOCR_NECK_ROWS && layout != PPOCR_NECK_CHANNELS_FIRST)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: unknown layout " + std::to_string(layout));
+    if (m == 0) return PPOCR_OK;
+    if (m > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
+    if (!d_x || !d_shortcut || !d_out || !d_line_off || lines == 0)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null pointer or no lines");
+    const size_t need = ppocr_rn_workspace_bytes(h, m);
+    DeviceGuard dg(h->device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecNeckHip: hipSetDevice failed");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, need, st, "RecNeckHip")) return e;
+    return launch_neck(h->dev, d_x, d_shortcut, m, d_line_off, lines, 0, layout, d_out,
+                       reinterpret_cast<float*>(ws.p), st);
+}
+
+int ppocr_rn_forward(const ppocr_rn_t* h, const float* x, const float* shortcut, const int64_t* line_off,
+                     int64_t lines, int layout, float* out) {
+    if (int e = check_neck(h)) return e;
+    if (lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: negative line count");
+    if (layout != PPOCR_NECK_ROWS && layout != PPOCR_NECK_CHANNELS_FIRST)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: unknown layout " + std::to_string(layout));
+    if (lines == 0) return PPOCR_OK;
+    if (!line_off) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null line offsets");
+    if (int e = check_offsets(line_off, lines)) return e;
+    const int64_t m = line_off[lines];
+    if (m == 0) return PPOCR_OK;
+    if (!x || !shortcut || !out) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null pointer");
+    if (m > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
+    DeviceGuard dg(h->device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecNeckHip: hipSetDevice failed");
+    const size_t xb = (size_t)m * h->dev.dim * 4;
+    HostCall hc;
+    if (int e = hc.begin({xb, xb, (size_t)(lines + 1) * 8}, {xb}, ppocr_rn_workspace_bytes(h, m))) return e;
+    if (int e = hc.copy_in({x, shortcut, line_off})) return e;
+    if (int e = launch_neck(h->dev, hc.in<float>(0), hc.in<float>(1), m, hc.in<int64_t>(2), lines, 0, layout,
+                           hc.out<float>(0), reinterpret_cast<float*>(hc.ws()), hc.stream()))
+        return e;
+    return hc.copy_out({out});
 }
 
 }  // extern "C"

@@ -14,6 +14,7 @@
 // tiny one).  Graph validity checks are those of Model::load (src/engine/model.rs:40-66).
 #include "model_graph.hpp"
 
+#include <cstring>
 #include <map>
 
 #include "../../include/ppocr_rechead.h"
@@ -44,15 +45,37 @@ bool str_array(const JVal* v, std::vector<std::string>* out) {
 
 }  // namespace
 
-int find_rec_head(const StFile& f, RecHeadNames* out) {
+namespace {
+
+// The graph of a model file: its nodes in order, Identity aliases resolved, the producer
+// and the number of uses of every value (Identity nodes excluded, graph outputs counted).
+struct Graph {
+    std::vector<std::string> in, out;
+    std::vector<GNode> nodes;
+    std::map<std::string, std::string> alias;
+    std::map<std::string, int> usage;
+    std::map<std::string, size_t> producer;
+    JVal root;
+    std::string resolve(std::string s) const {
+        for (int hops = 0; hops < 1000; ++hops) {
+            auto it = alias.find(s);
+            if (it == alias.end()) break;
+            s = it->second;
+        }
+        return s;
+    }
+};
+
+int load_graph(const StFile& f, Graph* gr) {
     const std::string* g = f.metadata("graph");
     if (!g) return model_fail("model metadata missing 'graph' definition");
     Json js{g->data(), g->data() + g->size(), {}};
-    JVal root;
+    JVal& root = gr->root;
     if (!js.value(&root)) return model_fail("failed to parse graph JSON: " + js.err);
     js.ws();
     if (js.p != js.end || root.kind != JVal::kObj) return model_fail("failed to parse graph JSON: not one object");
-    std::vector<std::string> g_in, g_out;
+    std::vector<std::string>& g_in = gr->in;
+    std::vector<std::string>& g_out = gr->out;
     if (!str_array(root.get("inputs"), &g_in) || !str_array(root.get("outputs"), &g_out))
         return model_fail("graph inputs and outputs must be lists of names");
     if (g_in.empty()) return model_fail("graph declares no inputs");
@@ -60,7 +83,7 @@ int find_rec_head(const StFile& f, RecHeadNames* out) {
     const JVal* jn = root.get("nodes");
     if (!jn || jn->kind != JVal::kArr) return model_fail("graph has no node list");
 
-    std::vector<GNode> nodes;
+    std::vector<GNode>& nodes = gr->nodes;
     for (const JVal& v : jn->arr) {
         GNode n;
         const JVal* name = v.get("name");
@@ -78,26 +101,28 @@ int find_rec_head(const StFile& f, RecHeadNames* out) {
     }
 
     // Identity nodes are aliases of their input
-    std::map<std::string, std::string> alias;
     for (const GNode& n : nodes)
-        if (n.op == "Identity") alias[n.out[0]] = n.in[0];
-    auto resolve = [&](std::string s) {
-        for (int hops = 0; hops < 1000; ++hops) {
-            auto it = alias.find(s);
-            if (it == alias.end()) break;
-            s = it->second;
-        }
-        return s;
-    };
-    std::map<std::string, int> usage;
-    std::map<std::string, size_t> producer;
+        if (n.op == "Identity") gr->alias[n.out[0]] = n.in[0];
     for (size_t i = 0; i < nodes.size(); ++i) {
         const GNode& n = nodes[i];
         if (n.op == "Identity") continue;
-        for (const std::string& x : n.in) ++usage[resolve(x)];
-        producer[n.out[0]] = i;
+        for (const std::string& x : n.in) ++gr->usage[gr->resolve(x)];
+        gr->producer[n.out[0]] = i;
     }
-    for (const std::string& o : g_out) ++usage[resolve(o)];
+    for (const std::string& o : g_out) ++gr->usage[gr->resolve(o)];
+    return PPOCR_OK;
+}
+
+}  // namespace
+
+int find_rec_head(const StFile& f, RecHeadNames* out) {
+    Graph gr;
+    if (int e = load_graph(f, &gr)) return e;
+    const std::vector<GNode>& nodes = gr.nodes;
+    const std::vector<std::string>& g_out = gr.out;
+    auto resolve = [&](const std::string& s) { return gr.resolve(s); };
+    std::map<std::string, int>& usage = gr.usage;
+    const std::map<std::string, size_t>& producer = gr.producer;
     auto is_output = [&](const std::string& s) {
         for (const std::string& o : g_out)
             if (resolve(o) == s) return true;
@@ -174,6 +199,230 @@ int find_rec_head(const StFile& f, RecHeadNames* out) {
         return PPOCR_OK;
     }
     return model_fail("no MatMul -> [Add] -> Softmax(last axis) segment ending at a graph output");
+}
+
+// The neck is read in graph order, node by node (Identity nodes are aliases and skipped),
+// with each step's activation input checked against the previous step's output:
+//   LayerNorm (the nine-node sub-graph the reference fuses, src/engine/model.rs:2143-2245:
+//   ReduceMean, Sub, Pow(2), ReduceMean, Add(eps), Sqrt, Div, Mul(w), Add(b)),
+//   MatMul [D][3D] + Add, Reshape [0, -1, 3, H, D/H], the attention (up to the next MatMul
+//   with a weight: one Mul by a scalar constant, two MatMuls of activations, one Softmax),
+//   MatMul [D][D] + Add, Add(residual), LayerNorm, MatMul [D][F] + Add, Sigmoid, Mul,
+//   MatMul [F][D] + Add, Add(residual); blocks repeat while a LayerNorm is followed by a
+//   MatMul [D][3D]; then the final LayerNorm, Reshape (after the nodes computing its shape),
+//   Transpose [0,3,1,2], Add(shortcut), Squeeze and the Transpose [0,2,1] that feeds the
+//   head's MatMul.
+int find_rec_neck(const StFile& f, RecNeckNames* out) {
+    RecHeadNames head;
+    if (int e = find_rec_head(f, &head)) return e;
+    Graph gr;
+    if (int e = load_graph(f, &gr)) return e;
+    auto bad = [](const std::string& why) { return model_fail("no SVTR neck tail before the head: " + why); };
+    std::vector<const GNode*> ord;
+    for (const GNode& n : gr.nodes)
+        if (n.op != "Identity") ord.push_back(&n);
+    auto R = [&](const std::string& s) { return gr.resolve(s); };
+    auto weight = [&](const std::string& s) { return f.find(R(s).c_str()); };
+    auto f32_vec = [&](const std::string& s, int64_t n) {
+        const StTensor* t = weight(s);
+        return t && t->dtype == "F32" && (int64_t)(t->bytes / 4) == n && t->shape.size() >= 1;
+    };
+    auto f32_mat = [&](const std::string& s, int64_t k, int64_t n) {
+        const StTensor* t = weight(s);
+        return t && t->dtype == "F32" && t->shape.size() == 2 && t->shape[0] == k && (n < 0 || t->shape[1] == n);
+    };
+    auto scalar = [&](const std::string& s, float* v) {
+        const StTensor* t = weight(s);
+        if (!t || t->dtype != "F32" || t->bytes != 4) return false;
+        std::memcpy(v, t->data, 4);
+        return true;
+    };
+    auto perm_is = [&](const GNode* n, std::initializer_list<int64_t> want) {
+        const JVal* perm = n->attrs ? n->attrs->get("perm") : nullptr;
+        if (!perm || perm->kind != JVal::kArr || perm->arr.size() != want.size()) return false;
+        size_t i = 0;
+        for (int64_t v : want)
+            if (!perm->arr[i].is_int || perm->arr[i++].i != v) return false;
+        return true;
+    };
+    auto other = [&](const GNode* n, const std::string& x, std::string* o) {
+        if (n->in.size() != 2) return false;
+        if (R(n->in[0]) == x) *o = R(n->in[1]);
+        else if (R(n->in[1]) == x) *o = R(n->in[0]);
+        else return false;
+        return true;
+    };
+    size_t p = 0;
+    auto at = [&](const char* op) { return p < ord.size() && ord[p]->op == op; };
+
+    // LayerNorm sub-graph at p over activation x (empty: any); advances p past it
+    struct Ln {
+        std::string x, out, w, b;
+        float eps = 0.0f;
+    };
+    auto layer_norm = [&](size_t q, Ln* ln) {
+        static const char* kOps[9] = {"ReduceMean", "Sub", "Pow", "ReduceMean", "Add", "Sqrt", "Div", "Mul", "Add"};
+        if (q + 9 > ord.size()) return false;
+        for (int i = 0; i < 9; ++i)
+            if (ord[q + i]->op != kOps[i]) return false;
+        const GNode *rm = ord[q], *sub = ord[q + 1], *pw = ord[q + 2], *rm2 = ord[q + 3], *ae = ord[q + 4],
+                    *sq = ord[q + 5], *dv = ord[q + 6], *mu = ord[q + 7], *ad = ord[q + 8];
+        const std::string x = R(rm->in[0]), mean = rm->out[0], diff = sub->out[0];
+        std::string two, eps, w, b;
+        float v2 = 0.0f;
+        if (sub->in.size() != 2 || R(sub->in[0]) != x || R(sub->in[1]) != mean) return false;
+        if (pw->in.size() != 2 || R(pw->in[0]) != diff || !scalar(pw->in[1], &v2) || v2 != 2.0f) return false;
+        if (R(rm2->in[0]) != pw->out[0] || !other(ae, rm2->out[0], &eps) || !scalar(eps, &ln->eps)) return false;
+        if (R(sq->in[0]) != ae->out[0] || dv->in.size() != 2 || R(dv->in[0]) != diff || R(dv->in[1]) != sq->out[0])
+            return false;
+        if (!other(mu, dv->out[0], &w) || !other(ad, mu->out[0], &b)) return false;
+        ln->x = x;
+        ln->out = ad->out[0];
+        ln->w = w;
+        ln->b = b;
+        return true;
+    };
+    // MatMul(x, W [k][n]) + Add(bias [n]) at p; advances p; n < 0: any, returned in *n
+    auto linear = [&](const std::string& x, int64_t k, int64_t* n, std::string* w, std::string* b,
+                      std::string* y) {
+        if (!at("MatMul") || ord[p]->in.size() != 2 || R(ord[p]->in[0]) != x || !f32_mat(ord[p]->in[1], k, *n))
+            return false;
+        *w = R(ord[p]->in[1]);
+        *n = weight(*w)->shape[1];
+        const std::string mm = ord[p]->out[0];
+        ++p;
+        if (!at("Add") || !other(ord[p], mm, b) || !f32_vec(*b, *n)) return false;
+        *y = ord[p]->out[0];
+        ++p;
+        return true;
+    };
+
+    Ln ln;
+    while (p < ord.size() && !layer_norm(p, &ln)) ++p;
+    if (p >= ord.size()) return bad("no LayerNorm sub-graph");
+    {
+        auto it = gr.producer.find(ln.x);
+        if (it == gr.producer.end() || gr.nodes[it->second].op != "Transpose" ||
+            !perm_is(&gr.nodes[it->second], {0, 2, 1}))
+            return bad("the first LayerNorm does not read a Transpose [0,2,1]");
+        out->input = R(gr.nodes[it->second].in[0]);
+    }
+    const StTensor* lw = weight(ln.w);
+    if (!lw || lw->dtype != "F32" || lw->shape.empty()) return bad("LayerNorm weight");
+    const int64_t D = (int64_t)(lw->bytes / 4);
+    out->dim = D;
+    std::string x = ln.x;
+    for (;;) {
+        RecNeckBlockNames bk;
+        if (!layer_norm(p, &ln) || ln.x != x || !f32_vec(ln.w, D) || !f32_vec(ln.b, D)) break;
+        // a block starts with LayerNorm -> MatMul [D][3D]; otherwise this is the final LayerNorm
+        const size_t save = p;
+        p += 9;
+        int64_t n3 = 3 * D;
+        std::string qkv;
+        if (!linear(ln.out, D, &n3, &bk.qkv_w, &bk.qkv_b, &qkv)) {
+            p = save;
+            break;
+        }
+        bk.ln1_w = R(ln.w);
+        bk.ln1_b = R(ln.b);
+        bk.ln1_eps = ln.eps;
+        if (!at("Reshape") || R(ord[p]->in[0]) != qkv || ord[p]->in.size() != 2) return bad("qkv Reshape");
+        const StTensor* shp = weight(ord[p]->in[1]);
+        if (!shp || shp->dtype != "I64" || shp->bytes != 40) return bad("qkv Reshape shape");
+        int64_t sv[5];
+        std::memcpy(sv, shp->data, 40);
+        if (sv[2] != 3 || sv[3] <= 0 || sv[4] <= 0 || sv[3] * sv[4] != D) return bad("qkv Reshape [0,-1,3,H,D/H]");
+        if (out->heads && out->heads != sv[3]) return bad("blocks with different head counts");
+        out->heads = sv[3];
+        ++p;
+        // the attention, up to the next MatMul with a weight
+        int softmax = 0, act_mm = 0;
+        float scale = 0.0f;
+        bool have_scale = false;
+        for (; p < ord.size(); ++p) {
+            const GNode* n = ord[p];
+            if (n->op == "MatMul" && n->in.size() == 2 && weight(n->in[1])) break;
+            if (n->op == "MatMul") ++act_mm;
+            if (n->op == "Softmax") ++softmax;
+            if (n->op == "Mul" && n->in.size() == 2) {
+                float v;
+                if (scalar(n->in[1], &v) || scalar(n->in[0], &v)) {
+                    if (have_scale) return bad("two scale constants in one attention");
+                    scale = v;
+                    have_scale = true;
+                }
+            }
+        }
+        if (softmax != 1 || act_mm != 2 || !have_scale) return bad("attention (Mul scale, 2 MatMul, Softmax)");
+        if (out->scale != 0.0f && out->scale != scale) return bad("blocks with different attention scales");
+        out->scale = scale;
+        const std::string att = R(ord[p]->in[0]);
+        int64_t nd = D;
+        std::string proj;
+        if (!linear(att, D, &nd, &bk.proj_w, &bk.proj_b, &proj)) return bad("attention projection MatMul [D][D] + Add");
+        std::string res;
+        if (!at("Add") || !other(ord[p], R(proj), &res) || res != x) return bad("attention residual Add");
+        x = ord[p]->out[0];
+        ++p;
+        if (!layer_norm(p, &ln) || ln.x != R(x) || !f32_vec(ln.w, D) || !f32_vec(ln.b, D)) return bad("second LayerNorm");
+        bk.ln2_w = R(ln.w);
+        bk.ln2_b = R(ln.b);
+        bk.ln2_eps = ln.eps;
+        p += 9;
+        int64_t hdim = -1;
+        std::string h;
+        if (!linear(ln.out, D, &hdim, &bk.fc1_w, &bk.fc1_b, &h)) return bad("MLP MatMul [D][F] + Add");
+        if (out->hidden && out->hidden != hdim) return bad("blocks with different MLP widths");
+        out->hidden = hdim;
+        if (!at("Sigmoid") || R(ord[p]->in[0]) != R(h)) return bad("MLP Sigmoid");
+        const std::string sg = ord[p]->out[0];
+        ++p;
+        std::string o2;
+        if (!at("Mul") || !other(ord[p], R(h), &o2) || o2 != R(sg)) return bad("MLP swish Mul");
+        const std::string hs = ord[p]->out[0];
+        ++p;
+        nd = D;
+        std::string f2;
+        if (!linear(R(hs), hdim, &nd, &bk.fc2_w, &bk.fc2_b, &f2)) return bad("MLP MatMul [F][D] + Add");
+        if (!at("Add") || !other(ord[p], R(f2), &res) || res != R(x)) return bad("MLP residual Add");
+        x = ord[p]->out[0];
+        ++p;
+        x = R(x);
+        out->blocks.push_back(bk);
+    }
+    if (out->blocks.empty()) return bad("no transformer block");
+    if (!layer_norm(p, &ln) || ln.x != x || !f32_vec(ln.w, D) || !f32_vec(ln.b, D)) return bad("final LayerNorm");
+    out->lnf_w = R(ln.w);
+    out->lnf_b = R(ln.b);
+    out->lnf_eps = ln.eps;
+    p += 9;
+    // shape arithmetic of the Reshape (Unsqueeze, Concat, ...) may come first
+    for (int skip = 0; skip < 16 && p < ord.size() && !(ord[p]->op == "Reshape" && R(ord[p]->in[0]) == R(ln.out));
+         ++skip) {
+        for (const std::string& i : ord[p]->in)
+            if (R(i) == R(ln.out)) return bad("the final LayerNorm is read before its Reshape");
+        ++p;
+    }
+    if (!at("Reshape") || R(ord[p]->in[0]) != R(ln.out)) return bad("Reshape after the final LayerNorm");
+    const std::string rs = ord[p]->out[0];
+    ++p;
+    if (!at("Transpose") || R(ord[p]->in[0]) != R(rs) || !perm_is(ord[p], {0, 3, 1, 2}))
+        return bad("Transpose [0,3,1,2] after the final LayerNorm");
+    const std::string tr = ord[p]->out[0];
+    ++p;
+    if (!at("Add") || !other(ord[p], R(tr), &out->shortcut)) return bad("shortcut Add");
+    const std::string sum = ord[p]->out[0];
+    ++p;
+    if (!at("Squeeze") || R(ord[p]->in[0]) != R(sum)) return bad("Squeeze before the head");
+    const std::string sq = ord[p]->out[0];
+    ++p;
+    if (!at("Transpose") || R(ord[p]->in[0]) != R(sq) || !perm_is(ord[p], {0, 2, 1})) return bad("Transpose [0,2,1] before the head");
+    const std::string t8 = ord[p]->out[0];
+    ++p;
+    if (!at("MatMul") || R(ord[p]->in[0]) != R(t8) || R(ord[p]->in[1]) != head.weight)
+        return bad("the tail does not feed the head's MatMul");
+    return PPOCR_OK;
 }
 
 }  // namespace ppocr

@@ -1,0 +1,45 @@
+// The SVTR mixing tail before the recognition head (neck.hip): device weights and launcher.
+#pragma once
+#include "common.hpp"
+
+namespace ppocr {
+
+// The geometry the kernels are built for: PP-OCRv6_small_rec's tail, D = 120 channels,
+// 8 heads of 15, MLP hidden width 240.
+constexpr int kNeckDim = 120;
+constexpr int kNeckHeadDim = 15;
+constexpr int kNeckHidden = 240;
+constexpr int kNeckMaxBlocks = 8;
+
+// One transformer block, device pointers: LayerNorm (w, b, eps), qkv [D][3D] + [3D],
+// proj [D][D] + [D], LayerNorm, fc1 [D][H] + [H], fc2 [H][D] + [D] (MatMul weights as the
+// model stores them, row-major [K][N]).
+struct NeckBlockDev {
+    const float *ln1_w, *ln1_b;
+    float ln1_eps;
+    const float *qkv_w, *qkv_b, *proj_w, *proj_b;
+    const float *ln2_w, *ln2_b;
+    float ln2_eps;
+    const float *fc1_w, *fc1_b, *fc2_w, *fc2_b;
+};
+
+struct NeckDev {
+    int dim = 0, heads = 0, hidden = 0, blocks = 0;
+    float scale = 0.0f;  // the attention's Mul constant (head_dim^-1/2 in the model)
+    NeckBlockDev block[kNeckMaxBlocks];
+    const float *lnf_w = nullptr, *lnf_b = nullptr;
+    float lnf_eps = 0.0f;
+};
+
+// Floats of workspace per token row: the residual stream and the shortcut rows (D each),
+// qkv (3D), the attention output (D) and the MLP hidden layer (H).
+constexpr int64_t kNeckWsFloatsPerRow = 6 * kNeckDim + kNeckHidden;
+
+// The whole tail on token rows: x_in and shortcut_in in `layout` (PPOCR_NECK_ROWS: [m][D];
+// PPOCR_NECK_CHANNELS_FIRST: line b as [D][T_b] at D * (first row of b)), lines given by
+// device offsets line_off[0..lines] or, with line_off null, line_len rows each; out [m][D]
+// token rows (the input of the head's MatMul).  ws: kNeckWsFloatsPerRow * m floats.
+int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, int64_t m, const int64_t* line_off,
+                int64_t lines, int64_t line_len, int layout, float* out, float* ws, hipStream_t st);
+
+}  // namespace ppocr

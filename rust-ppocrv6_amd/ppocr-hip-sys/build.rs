@@ -20,11 +20,12 @@ const SOURCES: &[&str] = &[
     "head_cfg_rescue.hip",
     "head_fma.hip",
     "softmax_ctc.hip",
+    "neck.hip",
     "safetensors.cpp",
     "model_graph.cpp",
 ];
 const HEADERS: &[&str] =
-    &["common.hpp", "kernels.hpp", "head_mfma.hpp", "safetensors.hpp", "json.hpp", "model_graph.hpp"];
+    &["common.hpp", "kernels.hpp", "neck.hpp", "head_mfma.hpp", "safetensors.hpp", "json.hpp", "model_graph.hpp"];
 const FLAGS: &[&str] = &[
     "--offload-arch=gfx950",
     "-O3",

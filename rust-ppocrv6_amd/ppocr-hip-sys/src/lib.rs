@@ -30,10 +30,40 @@ pub const PPOCR_MODE_BF16X3: c_int = 3;
 pub const PPOCR_MODE_F16X2: c_int = 4;
 pub const PPOCR_MODE_AUTO: c_int = 5;
 
+pub const PPOCR_NECK_ROWS: c_int = 0;
+pub const PPOCR_NECK_CHANNELS_FIRST: c_int = 1;
+
 /// Opaque head handle (`ppocr_rh_t`).
 #[repr(C)]
 pub struct ppocr_rh_t {
     _private: [u8; 0],
+}
+
+/// Opaque neck handle (`ppocr_rn_t`).
+#[repr(C)]
+pub struct ppocr_rn_t {
+    _private: [u8; 0],
+}
+
+/// One transformer block's weights (`ppocr_rn_block_t`), host pointers; MatMul weights
+/// row-major [K][N] as the model stores them.
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct ppocr_rn_block_t {
+    pub ln1_w: *const f32,
+    pub ln1_b: *const f32,
+    pub ln1_eps: f32,
+    pub qkv_w: *const f32,
+    pub qkv_b: *const f32,
+    pub proj_w: *const f32,
+    pub proj_b: *const f32,
+    pub ln2_w: *const f32,
+    pub ln2_b: *const f32,
+    pub ln2_eps: f32,
+    pub fc1_w: *const f32,
+    pub fc1_b: *const f32,
+    pub fc2_w: *const f32,
+    pub fc2_b: *const f32,
 }
 
 extern "C" {
@@ -123,4 +153,20 @@ extern "C" {
                                    d_idx: *mut i32, d_maxprob: *mut f32, d_seq: *mut i32, d_seq_len: *mut i64,
                                    d_score: *mut f32, d_workspace: *mut c_void, workspace_bytes: usize,
                                    stream: *mut c_void) -> c_int;
+
+    // ---- the SVTR neck tail before the head (Model::forward's MatMul, LayerNorm, Softmax,
+    // Sigmoid, Mul and Add nodes between Transpose.0 and Transpose.8, src/engine/model.rs)
+    pub fn ppocr_rn_create(blocks: *const ppocr_rn_block_t, nblocks: c_int, lnf_w: *const f32, lnf_b: *const f32,
+                           lnf_eps: f32, dim: i64, heads: i64, hidden: i64, scale: f32, device: c_int,
+                           out: *mut *mut ppocr_rn_t) -> c_int;
+    pub fn ppocr_rn_create_from_model(path: *const c_char, device: c_int, out: *mut *mut ppocr_rn_t) -> c_int;
+    pub fn ppocr_rn_destroy(h: *mut ppocr_rn_t);
+    pub fn ppocr_rn_shape(h: *const ppocr_rn_t, dim: *mut i64, heads: *mut i64, hidden: *mut i64,
+                          blocks: *mut c_int) -> c_int;
+    pub fn ppocr_rn_workspace_bytes(h: *const ppocr_rn_t, m: i64) -> usize;
+    pub fn ppocr_rn_forward_dev(h: *const ppocr_rn_t, d_x: *const f32, d_shortcut: *const f32, m: i64,
+                                d_line_off: *const i64, lines: i64, layout: c_int, d_out: *mut f32,
+                                d_workspace: *mut c_void, workspace_bytes: usize, stream: *mut c_void) -> c_int;
+    pub fn ppocr_rn_forward(h: *const ppocr_rn_t, x: *const f32, shortcut: *const f32, line_off: *const i64,
+                            lines: i64, layout: c_int, out: *mut f32) -> c_int;
 }

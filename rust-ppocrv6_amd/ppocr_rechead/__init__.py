@@ -19,11 +19,11 @@ import os
 import numpy as np
 
 from . import _lib
-from ._lib import (MODE_AUTO, MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_F16X2, MODE_FP32_FMA, PPOCR_ERR_DEVICE,
-                   PPOCR_ERR_INVALID_ARG, PPOCR_ERR_MODEL, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
+from ._lib import (MODE_AUTO, MODE_BF16X1, MODE_BF16X2, MODE_BF16X3, MODE_F16X2, MODE_FP32_FMA, NECK_CHANNELS_FIRST,
+                   NECK_ROWS, PPOCR_ERR_DEVICE, PPOCR_ERR_INVALID_ARG, PPOCR_ERR_MODEL, PPOCR_ERR_NO_MEMORY, PPOCR_OK)
 
 __all__ = [
-    "OcrError", "QuantizedWeight", "RecHead", "CtcDecoder", "find_rec_head", "matmul_quantized_b", "matmul_transposed_b",
+    "OcrError", "QuantizedWeight", "RecHead", "RecNeck", "CtcDecoder", "find_rec_head", "matmul_quantized_b", "matmul_transposed_b",
     "softmax", "softmax_inplace", "MODE_FP32_FMA", "MODE_BF16X1", "MODE_BF16X2", "MODE_BF16X3", "MODE_F16X2", "MODE_AUTO",
 ]
 
@@ -282,6 +282,92 @@ class RecHead:
                                                   _ptr(seq), _ptr(seq_len), _ptr(score)))
         seqs = [seq[b * steps:b * steps + seq_len[b]].copy() for b in range(lines)]
         return {"idx": idx[:m], "maxprob": mp[:m], "seqs": seqs, "score": score[:lines]}
+
+
+class RecNeck:
+    """The recognition model's SVTR mixing tail before the head, resident in HBM: the
+    transformer blocks, final LayerNorm and shortcut Add between Transpose.0 and
+    Transpose.8 of PP-OCRv6_small_rec, which the reference's executor runs node by node
+    (Model::forward, src/engine/model.rs: MatMul 1245-1272, LayerNorm 1274-1284, Softmax
+    1286-1302, Sigmoid 953-963).
+
+    blocks: list of dicts with the fields of ppocr_rn_block_t (ln1_w, ln1_b, ln1_eps,
+    qkv_w [D][3D], qkv_b, proj_w [D][D], proj_b, ln2_w, ln2_b, ln2_eps, fc1_w [D][H], fc1_b,
+    fc2_w [H][D], fc2_b), MatMul weights row-major [K][N] as the model stores them."""
+
+    _FIELDS = ("ln1_w", "ln1_b", "qkv_w", "qkv_b", "proj_w", "proj_b", "ln2_w", "ln2_b", "fc1_w", "fc1_b",
+               "fc2_w", "fc2_b")
+
+    def __init__(self, blocks, lnf_w, lnf_b, lnf_eps, heads=8, scale=None, device=0):
+        self._h = ctypes.c_void_p()
+        keep = []
+
+        def arr(x):
+            a = _f32(x)
+            keep.append(a)
+            return a.ctypes.data_as(ctypes.c_void_p)
+
+        dim = int(np.asarray(blocks[0]["ln1_w"]).size)
+        hidden = int(np.asarray(blocks[0]["fc1_b"]).size)
+        if scale is None:
+            scale = float(np.float32((dim // heads) ** -0.5))
+        cb = (_lib.RnBlock * len(blocks))()
+        for i, b in enumerate(blocks):
+            for f in self._FIELDS:
+                setattr(cb[i], f, arr(b[f]))
+            cb[i].ln1_eps = float(b["ln1_eps"])
+            cb[i].ln2_eps = float(b["ln2_eps"])
+        _check(_lib.lib().ppocr_rn_create(cb, len(blocks), arr(lnf_w), arr(lnf_b), float(lnf_eps), dim, heads, hidden,
+                                          float(scale), device, ctypes.byref(self._h)))
+        self.dim, self.heads, self.hidden, self.blocks = dim, heads, hidden, len(blocks)
+
+    @classmethod
+    def from_model(cls, path, device=0):
+        """The tail of a recognition model file (its graph searched from the first
+        LayerNorm to the head's MatMul), weights uploaded from the file."""
+        self = cls.__new__(cls)
+        self._h = ctypes.c_void_p()
+        _check(_lib.lib().ppocr_rn_create_from_model(os.fsencode(path), device, ctypes.byref(self._h)))
+        d, h, f, b = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+        _check(_lib.lib().ppocr_rn_shape(self._h, ctypes.byref(d), ctypes.byref(h), ctypes.byref(f), ctypes.byref(b)))
+        self.dim, self.heads, self.hidden, self.blocks = d.value, h.value, f.value, b.value
+        return self
+
+    def close(self):
+        if self._h:
+            _lib.lib().ppocr_rn_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def workspace_bytes(self, m):
+        return int(_lib.lib().ppocr_rn_workspace_bytes(self._h, m))
+
+    def forward(self, x, shortcut, line_off, layout=_lib.NECK_ROWS):
+        """Token rows [m][D] (the head's input) from x and shortcut in `layout`: token rows
+        [m][D], or channels first (line b as [D][T_b] at D * line_off[b])."""
+        line_off = np.ascontiguousarray(line_off, dtype=np.int64)
+        lines = line_off.size - 1
+        if lines < 0:
+            raise OcrError("RecNeckHip", "line offsets must hold at least one entry")
+        m = int(line_off[-1])
+        x = _f32(x).reshape(-1)
+        shortcut = _f32(shortcut).reshape(-1)
+        if x.size != m * self.dim or shortcut.size != m * self.dim:
+            raise OcrError("RecNeckHip", f"expected {m} x {self.dim} values in x and shortcut")
+        out = np.empty((m, self.dim), np.float32)
+        if m:
+            _check(_lib.lib().ppocr_rn_forward(self._h, _ptr(x), _ptr(shortcut), _ptr(line_off), lines, layout,
+                                               _ptr(out)))
+        return out
 
 
 def find_rec_head(path):

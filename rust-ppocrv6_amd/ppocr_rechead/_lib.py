@@ -23,11 +23,23 @@ MODE_BF16X3 = 3
 MODE_F16X2 = 4
 MODE_AUTO = 5
 
+NECK_ROWS = 0
+NECK_CHANNELS_FIRST = 1
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _int = ctypes.c_int
 _sz = ctypes.c_size_t
+
+
+
+class RnBlock(ctypes.Structure):
+    """ppocr_rn_block_t: one transformer block's weights (host pointers)."""
+    _fields_ = [("ln1_w", _vp), ("ln1_b", _vp), ("ln1_eps", ctypes.c_float), ("qkv_w", _vp), ("qkv_b", _vp),
+                ("proj_w", _vp), ("proj_b", _vp), ("ln2_w", _vp), ("ln2_b", _vp), ("ln2_eps", ctypes.c_float),
+                ("fc1_w", _vp), ("fc1_b", _vp), ("fc2_w", _vp), ("fc2_b", _vp)]
+
 
 # name -> (restype, argtypes); every function declared in include/ppocr_rechead.h.
 SIGNATURES = {
@@ -64,6 +76,15 @@ SIGNATURES = {
     "ppocr_rh_decode_dev_noalloc": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppocr_rh_decode_nct": (_int, [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "ppocr_rh_decode_nct_dev": (_int, [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ppocr_rn_create": (_int, [ctypes.POINTER(RnBlock), _int, _vp, _vp, ctypes.c_float, _i64, _i64, _i64,
+                               ctypes.c_float, _int, ctypes.POINTER(_vp)]),
+    "ppocr_rn_create_from_model": (_int, [ctypes.c_char_p, _int, ctypes.POINTER(_vp)]),
+    "ppocr_rn_destroy": (None, [_vp]),
+    "ppocr_rn_shape": (_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                              ctypes.POINTER(_int)]),
+    "ppocr_rn_workspace_bytes": (_sz, [_vp, _i64]),
+    "ppocr_rn_forward_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _sz, _vp]),
+    "ppocr_rn_forward": (_int, [_vp, _vp, _vp, _vp, _i64, _int, _vp]),
 }
 
 _lib = None

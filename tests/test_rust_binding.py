@@ -20,7 +20,8 @@ C_TO_RUST = {
     "const float*": "*const f32", "float*": "*mut f32", "const int8_t*": "*const i8", "int8_t*": "*mut i8",
     "const int32_t*": "*const i32", "int32_t*": "*mut i32", "const int64_t*": "*const i64", "int64_t*": "*mut i64",
     "int*": "*mut c_int", "const ppocr_rh_t*": "*const ppocr_rh_t", "ppocr_rh_t*": "*mut ppocr_rh_t",
-    "ppocr_rh_t**": "*mut *mut ppocr_rh_t",
+    "ppocr_rh_t**": "*mut *mut ppocr_rh_t", "float": "f32", "const ppocr_rn_block_t*": "*const ppocr_rn_block_t",
+    "const ppocr_rn_t*": "*const ppocr_rn_t", "ppocr_rn_t*": "*mut ppocr_rn_t", "ppocr_rn_t**": "*mut *mut ppocr_rn_t",
 }
 
 
