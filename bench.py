@@ -36,12 +36,13 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="dense_256")
-    p.add_argument("--mode", type=int, default=5,
-                   help="0 fp32 FMA, 1/2/3 bf16 terms, 4 two fp16 terms, 5 auto (the library's default)")
+    p.add_argument("--mode", type=int, default=2,
+                   help="0 fp32 FMA, 1/2/3 bf16 terms (2: the headline), 4 two fp16 terms, 5 auto (the library's "
+                        "default)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-others", action="store_true", help="skip the other configurations")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", default="", help="fused|unfused|probs (profiling runs)")
+    p.add_argument("--only", default="", help="fused|unfused|probs|neck (profiling runs)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="also run one device copy of this many MiB (counter calibration)")
     return p.parse_args()
@@ -228,7 +229,6 @@ def other_config(name, modes, steps, warmup, samples=None):
     dlen, dscore = DeviceArray((lines,), np.int64), DeviceArray((lines,), np.float32)
     res = {"rows": m, "lines": lines, "head": "int8" if wk["quantized"] else "fp32",
            "auto_mode": MODE_NAMES[head.auto_mode()]}
-    amax = np.abs(a).max(axis=1)
     for mode in modes:
         ws = head.workspace_bytes(m, mode)
         dws = DeviceArray((max(ws, 1),), np.uint8)
@@ -241,10 +241,11 @@ def other_config(name, modes, steps, warmup, samples=None):
         flops = 2.0 * m * n * k
         r = {"ms_per_step": round(ms, 4), "rows_per_s": round(m / (ms / 1e3), 1),
              "TFLOPs": round(flops / (ms / 1e3) / 1e12, 2)}
-        lim, _ = head.guard_limits(mode)
-        if np.isfinite(lim):
-            r["guarded_rows"] = int((amax > lim).sum())
-            r["guard_limit"] = round(lim, 4)
+        prec, ra, rn = head.guard_limits(mode)
+        if np.isfinite(prec):
+            r["guarded_rows"] = int(head.guarded_rows(a, mode).sum())
+            r["guard_limits"] = {"precision_max_abs": round(prec, 4), "range_max_abs": round(ra, 4),
+                                 "range_norm": round(rn, 4)}
         if wk["quantized"] and m <= 8192:
             # the same step from host arrays (ppocr_rh_decode): what one call per page costs
             off = wk["line_off"]
@@ -357,6 +358,53 @@ def main():
                "logits_hbm_frac": round(logits_bytes / (ms_l / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
         dlog.free()
 
+    neck = None
+    if args.only in ("", "neck"):
+        # the SVTR tail before the head on the same lines (synthetic weights of the real
+        # model's statistics), alone and followed by the fused head: the head's input then
+        # never leaves the device
+        nw = wl.neck_weights()
+        nk = rh.RecNeck(nw["blocks"], nw["lnf_w"], nw["lnf_b"], nw["lnf_eps"])
+        rng = np.random.default_rng(wl.SEED_A + 0x77)
+        dfx = DeviceArray.from_numpy((rng.standard_normal((m, k)) * 1.5).astype(np.float32))
+        dsc = DeviceArray.from_numpy(rng.standard_normal((m, k)).astype(np.float32))
+        dfeat = DeviceArray((m, k), np.float32)
+        nws = nk.workspace_bytes(m)
+        dnws = DeviceArray((nws,), np.uint8)
+
+        def neck_step():
+            rh._check(L.ppocr_rn_forward_dev(nk.handle, dfx.p, dsc.p, m, doff.p, lines, rh.NECK_ROWS, dfeat.p,
+                                             dnws.p, nws, st))
+
+        ms_n, _ = timed(neck_step, stream, args.steps, args.warmup)
+        steps_of = np.diff(wk["line_off"])
+        nflops = float(sum(int(t) * wl.neck_flops_per_row(int(t)) for t in steps_of))
+        synchronize()
+        feats = dfeat.numpy()
+        neck = {"blocks": len(nw["blocks"]), "ms_per_step": round(ms_n, 4), "rows_per_s": round(m / (ms_n / 1e3), 1),
+                "TFLOPs": round(nflops / (ms_n / 1e3) / 1e12, 2),
+                "fp32_peak_frac": round(nflops / (ms_n / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+                "flops_per_step": nflops, "head_input_max_abs": round(float(np.abs(feats).max()), 2),
+                "neck_then_head": {}}
+        for hm in sorted({mode, 5}):
+            hws = head.workspace_bytes(m, hm)
+            dhws = DeviceArray((max(hws, 1),), np.uint8)
+
+            def neck_head_step():
+                neck_step()
+                rh._check(L.ppocr_rh_decode_dev(head.handle, dfeat.p, m, doff.p, lines, hm, didx.p, dmp.p, dseq.p,
+                                                dlen.p, dscore.p, dhws.p, hws, st))
+
+            ms_nh, _ = timed(neck_head_step, stream, args.steps, args.warmup)
+            rm = head.auto_mode() if hm == 5 else hm
+            neck["neck_then_head"][MODE_NAMES[hm] + (f" ({MODE_NAMES[rm]})" if hm == 5 else "")] = {
+                "ms_per_step": round(ms_nh, 4), "rows_per_s": round(m / (ms_nh / 1e3), 1),
+                "guarded_rows": int(head.guarded_rows(feats, rm).sum()) if rm in (2, 3, 4) else 0}
+            dhws.free()
+        for d in (dfx, dsc, dfeat, dnws):
+            d.free()
+        nk.close()
+
     probs = None
     if args.only in ("", "probs"):
         dprobs = DeviceArray((m, n), np.float32)
@@ -446,13 +494,14 @@ def main():
             "host_arrays": host,
             "unfused": unf,
             "probs_fused": probs,
+            "neck": neck,
             "cpu_baseline": cpu,
             "other_configs": others,
         }
         if copy:
             line["copy_probe"] = copy
     else:
-        line = {"metric": "profiling run", "unfused": unf, "probs_fused": probs, "copy_probe": copy}
+        line = {"metric": "profiling run", "unfused": unf, "probs_fused": probs, "neck": neck, "copy_probe": copy}
     print(json.dumps(line), flush=True)
     head.close()
 

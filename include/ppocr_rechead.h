@@ -50,11 +50,13 @@ typedef enum {
                                 it; int8 weights are exact in fp16); for an FP32 head,
                                 a_hi*w_hi + a_hi*w_lo + a_lo*w_hi with fp16 halves (weights
                                 below 32768 in magnitude) */
-    PPOCR_MODE_AUTO = 5      /* chosen per head from its weights: the bf16 split (BF16X2, or
-                                BF16X3 for an FP32 head) when its precision guard leaves rows
-                                of magnitude up to 8 on the split path, F16X2 otherwise (heads
-                                with large weight rows, whose bf16 guard would send ordinary
-                                rows to the rescue).  ppocr_rh_auto_mode tells which. */
+    PPOCR_MODE_AUTO = 5      /* chosen per head from its weights: F16X2, unless the bf16
+                                split's precision guard leaves rows of max|a| up to 32 on the
+                                split path (then BF16X2, or BF16X3 for an FP32 head; also when
+                                an FP32 head's weights do not fit fp16).  The recognition
+                                model's activations at the head reach |a| ~ 10-30, which the
+                                bf16 guard of typical heads sends to the rescue pass.
+                                ppocr_rh_auto_mode tells which. */
 } ppocr_mode_t;
 
 typedef struct ppocr_rh ppocr_rh_t;
@@ -123,11 +125,14 @@ int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized);
  * PPOCR_MODE_F16X2), -1 for a null handle.  No counterpart in the reference, whose CPU
  * kernels have one precision. */
 int ppocr_rh_auto_mode(const ppocr_rh_t* h);
-/* The precision guard of `mode` on this head: rows whose max |a| exceeds *stats_limit go to
- * the rescue pass in argmax / decode / probabilities, rows above *logits_limit in logits
- * (INFINITY: the mode has no guard).  No counterpart in the reference; for callers that
+/* The precision guard of `mode` on this head: a row a goes to the rescue pass of argmax,
+ * decode and probabilities when max|a| > *prec_limit, or when max|a| > *range_amax_limit
+ * and ||a||_2 > *range_norm_limit (its logits not proven to lie within the range the
+ * statistics pass's unshifted softmax sums allow); of logits when max|a| > *prec_limit.
+ * INFINITY: no such limit in this mode.  No counterpart in the reference; for callers that
  * want to know how many rows of a batch take the slower path. */
-int ppocr_rh_guard_limits(const ppocr_rh_t* h, int mode, float* stats_limit, float* logits_limit);
+int ppocr_rh_guard_limits(const ppocr_rh_t* h, int mode, float* prec_limit, float* range_amax_limit,
+                          float* range_norm_limit);
 
 /* Device workspace needed by the `_dev` entry points below for m rows (0 if none).  A
  * NULL workspace makes the call allocate one on its stream (stream-ordered) and free it

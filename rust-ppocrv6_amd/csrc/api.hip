@@ -54,6 +54,8 @@ struct ppocr_rh {
     // Rows with max|a| at most range_limit have every logit in [-kLogitBound, kLogitBound]:
     // |logit| <= max|a| * max_c sum_k |w_ck| + max_c |b_c| (range_ok: such a bound exists).
     float range_limit = 0.0f;
+    // ... or rows with ||a||_2^2 at most range_ss: |logit| <= ||a||_2 * max_c ||w_c||_2 + max_c |b_c|
+    float range_ss = 0.0f;
     bool range_ok = false;
 };
 
@@ -428,8 +430,12 @@ void set_limits(ppocr_rh* h, float wmax, double w1, double l2, double bmax) {
     // logit range bound: the largest L1 norm of a dequantised weight row and the largest
     // |bias|, rounded up by a small margin
     const double room = (double)kLogitBound - bmax * 1.001;
-    if (room > 0.0 && std::isfinite(w1) && std::isfinite(bmax)) {
+    if (room > 0.0 && std::isfinite(w1) && std::isfinite(bmax) && std::isfinite(l2)) {
         h->range_limit = (float)(w1 > 0.0 ? room / (w1 * 1.001) : INFINITY);
+        // the kernels sum the squares in fp32 (120 terms: relative error below 1e-5), so
+        // the limit on ||a||_2^2 keeps a further 0.1% margin
+        const double nl = l2 > 0.0 ? room / (l2 * 1.001) : INFINITY;
+        h->range_ss = (float)(nl * nl * 0.999);
         h->range_ok = true;
     }
 }
@@ -505,12 +511,14 @@ int check_head(const ppocr_rh* h, const char* op) {
     return PPOCR_OK;
 }
 
-// PPOCR_MODE_AUTO: the bf16 split while its guard leaves rows of max|a| up to
-// kAutoSplitRows on the split path (no rescue for activations of ordinary magnitude), the
-// fp16 split for heads with larger weight rows (whose bf16 guard would rescue most rows).
-// Measured on the dense 30720-row batch the bf16 split is ~3% faster than the fp16 one;
-// on the stress head (+-5 weight outliers) the fp16 split is 2.4x faster.
-constexpr float kAutoSplitRows = 8.0f;
+// PPOCR_MODE_AUTO: the fp16 split, unless the bf16 split's precision guard leaves rows of
+// max|a| up to kAutoSplitRows on the split path (then the bf16 split, ~3% faster).  The
+// activations the head sees in the recognition model (after the SVTR tail's final
+// LayerNorm, whose weights are ~3, plus the shortcut) reach |a| ~ 10-30: with the bf16
+// split most of those rows would go to the rescue pass (the synthetic 18710-class head's
+// bf16 limit is 11.7), with the fp16 split (limit 747) none.  Measured after the tail on
+// the 30720-row batch: head 0.225 ms in F16X2, 0.535 ms in BF16X2.
+constexpr float kAutoSplitRows = 32.0f;
 int auto_mode(const ppocr_rh* h) {
     if (h->amax_limit >= kAutoSplitRows || !h->f16_ok) return h->quantized ? PPOCR_MODE_BF16X2 : PPOCR_MODE_BF16X3;
     return PPOCR_MODE_F16X2;
@@ -602,7 +610,8 @@ Guard make_guard(const ppocr_rh* h, int cfg, const WsLayout& L, uint8_t* ws, int
                  reinterpret_cast<int*>(ws + L.guard_rows),
                  (int)std::min<int64_t>(m, INT32_MAX),
                  next_epoch(),
-                 h->range_ok ? std::min(prec, h->range_limit) : prec,
+                 h->range_ok ? h->range_limit : 0.0f,
+                 h->range_ok ? h->range_ss : 0.0f,
                  h->range_ok,
                  h->fma};
 }
@@ -861,18 +870,21 @@ int ppocr_rh_shape(const ppocr_rh_t* h, int64_t* n, int64_t* k, int* quantized) 
 
 int ppocr_rh_auto_mode(const ppocr_rh_t* h) { return h ? auto_mode(h) : -1; }
 
-int ppocr_rh_guard_limits(const ppocr_rh_t* h, int mode, float* stats_limit, float* logits_limit) {
-    if (!h || !stats_limit || !logits_limit) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
+int ppocr_rh_guard_limits(const ppocr_rh_t* h, int mode, float* prec_limit, float* range_amax_limit,
+                          float* range_norm_limit) {
+    if (!h || !prec_limit || !range_amax_limit || !range_norm_limit)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: null pointer");
     int cfg;
     if (int e = mode_cfg(h, mode, &cfg)) return e;
-    *stats_limit = *logits_limit = INFINITY;
+    *prec_limit = *range_amax_limit = *range_norm_limit = INFINITY;
     if (cfg == CFG_Q2 || cfg == CFG_H2 || cfg == CFG_F3 || cfg == CFG_HF3) {
-        const float prec = cfg_is_f16(cfg) ? h->amax_limit_h : h->amax_limit;
-        *logits_limit = prec;
+        *prec_limit = cfg_is_f16(cfg) ? h->amax_limit_h : h->amax_limit;
         // the two-term INT8 statistics pass skips the reference shift when the head has a
-        // logit range bound, and then also rescues the rows that could leave that range
-        const bool noref = h->range_ok && (cfg == CFG_Q2 || cfg == CFG_H2);
-        *stats_limit = noref ? std::min(prec, h->range_limit) : prec;
+        // logit range bound, and then also rescues the rows not proven to stay in range
+        if (h->range_ok && (cfg == CFG_Q2 || cfg == CFG_H2)) {
+            *range_amax_limit = h->range_limit;
+            *range_norm_limit = std::sqrt(h->range_ss);
+        }
     }
     return PPOCR_OK;
 }

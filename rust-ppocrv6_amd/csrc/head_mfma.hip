@@ -136,11 +136,12 @@ static int rescue_cfg(int cfg) {
 }
 
 // The statistics pass of the two-term INT8 mode skips the reference shift of the softmax
-// sum (NOREF) when the head allows it, flagging also the rows whose logits could leave
-// [-kLogitBound, kLogitBound]; its limit is then the lower stats_amax_limit.
+// sum (NOREF) when the head allows it, flagging also the rows whose logits are not proven
+// to lie in [-kLogitBound, kLogitBound] (the range limits of GuardLimits).
 static bool stats_noref_of(int cfg, const Guard& g) { return g.stats_noref && (cfg == CFG_Q2 || cfg == CFG_H2); }
-static float stats_limit_of(int cfg, const Guard& g) {
-    return stats_noref_of(cfg, g) ? g.stats_amax_limit : g.amax_limit;
+static GuardLimits stats_limit_of(int cfg, const Guard& g) {
+    if (stats_noref_of(cfg, g)) return GuardLimits{g.amax_limit, g.range_amax_limit, g.range_ss_limit};
+    return GuardLimits{g.amax_limit, INFINITY, INFINITY};
 }
 
 static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue,
@@ -162,7 +163,10 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     // statistics pass, so this pass must compute every t exactly as that pass did: the
     // same rows take the rescue (that pass's limit, the lower one when it skips the
     // reference shift).  Logits need only the precision limit.
-    const float limit = !guarded ? 0.0f : epi == 1 ? stats_limit_of(cfg, *guard) : guard->amax_limit;
+    const GuardLimits none{0.0f, 0.0f, 0.0f};
+    const GuardLimits limit = !guarded ? none
+                              : epi == 1 ? stats_limit_of(cfg, *guard)
+                                         : GuardLimits{guard->amax_limit, INFINITY, INFINITY};
     if (guarded) {
         // a replay of this call (same epoch) must start from an empty list too
         guard_reset_kernel<<<1, 1, 0, st>>>(guard->header, guard->epoch);
@@ -181,7 +185,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
                  row_max,
                  row_inv,
                  out,
-                 guarded ? limit : 0.0f,
+                 limit,
                  guarded ? guard->header : nullptr,
                  guarded ? guard->rows : nullptr,
                  guarded ? guard->epoch : 0u,
@@ -196,7 +200,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     const int rgrid = grid_blocks(slots, nsplit);
     x.rec = rec_rescue;
     x.mblocks = slots;
-    x.amax_limit = 0.0f;
+    x.lim = none;
     x.guard_header = guard->header;
     x.guard_rows = guard->rows;
     x.guard_epoch = guard->epoch;
@@ -255,7 +259,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
                   p_best,
                   p_sum,
                   p_idx,
-                  guarded ? stats_limit_of(cfg, *guard) : 0.0f,
+                  guarded ? stats_limit_of(cfg, *guard) : GuardLimits{0.0f, 0.0f, 0.0f},
                   guarded ? guard->header : nullptr,
                   guarded ? guard->rows : nullptr,
                   guarded ? guard->epoch : 0u,
@@ -274,7 +278,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
         const int rgrid = grid_blocks(slots, nsplit);
         x.rec = rec_rescue;
         x.mblocks = slots;
-        x.amax_limit = 0.0f;
+        x.lim = GuardLimits{0.0f, 0.0f, 0.0f};
         if (int e = call_stats_gather(rcfg, tg.G, x, (unsigned)rgrid, st)) return e;
     }
     const Guard* reset = guarded ? guard : nullptr;

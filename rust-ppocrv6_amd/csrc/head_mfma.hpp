@@ -218,13 +218,14 @@ __device__ __forceinline__ unsigned short split_term(float x, int t) {
 
 // Activation fragment of one lane for MFMA step s: row `row` of a (zero when the row
 // is not valid), the 8 k values of the lane's slot, as the bf16 term its product uses;
-// `amax` is raised to the largest |value| loaded.  `vec`: rows and groups are 16-byte
+// `amax` is raised to the largest |value| loaded, `ss` accumulates the squares of the
+// values loaded for product 0 (each k once).  `vec`: rows and groups are 16-byte
 // aligned, so each fragment is two float4 loads.  vec < 0 selects the channels-first
 // layout [lines][k][T] of the tensor before the neck's transpose, T = -vec: row r is step
 // r % T of line r / T, and its k values are T floats apart.
 template <int C, int G, int s>
 __device__ __forceinline__ u16x8 act_frag(const float* __restrict__ a, int64_t row, bool valid, int k, int vec,
-                                          int h, float& amax) {
+                                          int h, float& amax, float& ss) {
     u16x8 f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = 0;
@@ -258,6 +259,11 @@ __device__ __forceinline__ u16x8 act_frag(const float* __restrict__ a, int64_t r
         amax = fmaxf(amax, __builtin_fabsf(x[e]));
         f[e] = split_term<CfgT<C>::f16>(x[e], term);
     }
+    // every group g is loaded once for product 0, so the squares are counted once
+    if (p == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+    }
     return f;
 }
 
@@ -284,11 +290,12 @@ struct RowSource {
 // call's epoch with count 0 (a header with another epoch counts as empty; epochs have the
 // top bit set, so no index, count or non-negative float left in the workspace matches
 // one), then each append takes the next slot.  Slots past the capacity are dropped.
-__device__ __forceinline__ void guard_append(float amax, float amax_limit, bool valid, int64_t row, int h,
-                                             unsigned long long* guard_header, int* guard_rows, unsigned epoch,
+__device__ __forceinline__ void guard_append(float amax, float ss, const GuardLimits& lim, bool valid, int64_t row,
+                                             int h, unsigned long long* guard_header, int* guard_rows, unsigned epoch,
                                              int capacity) {
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    if (h == 0 && valid && amax > amax_limit) {
+    ss += __shfl_xor(ss, 32, 64);
+    if (h == 0 && valid && (amax > lim.prec || (amax > lim.range_amax && ss > lim.range_ss))) {
         unsigned long long cur = __hip_atomic_load(guard_header, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         while ((unsigned)(cur >> 32) != epoch) {
             const unsigned long long prev = atomicCAS(guard_header, cur, (unsigned long long)epoch << 32);
@@ -481,7 +488,7 @@ template <int C, int G, int MB, bool GATHER, bool NOREF, int OCC = 8 / kStatsWav
 __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, float amax_limit, unsigned long long* __restrict__ guard_header,
+    int* __restrict__ p_idx, GuardLimits lim, unsigned long long* __restrict__ guard_header,
     int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
@@ -513,12 +520,12 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
             arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
-            float amax = 0.0f;
+            float amax = 0.0f, ss = 0.0f;
             [&]<int... s>(std::integer_sequence<int, s...>) {
-                ((bf[b][s] = act_frag<C, G, s>(a, arow[b], valid[b], k, vec, h, amax)), ...);
+                ((bf[b][s] = act_frag<C, G, s>(a, arow[b], valid[b], k, vec, h, amax, ss)), ...);
             }(std::make_integer_sequence<int, S>{});
             if (!GATHER && guard_header && chunk == 0)
-                guard_append(amax, amax_limit, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch, guard_cap);
+                guard_append(amax, ss, lim, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch, guard_cap);
         }
 
         float best[MB], sum[MB], ref[MB];
@@ -707,7 +714,7 @@ template <int C, int G, int EPI, bool GATHER>
 __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles, int n,
     int nsplit, int tiles_per_chunk, int mblocks, const float* __restrict__ row_max,
-    const float* __restrict__ row_inv, float* __restrict__ out, float amax_limit,
+    const float* __restrict__ row_inv, float* __restrict__ out, GuardLimits lim,
     unsigned long long* __restrict__ guard_header, int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
@@ -766,13 +773,13 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
         const int64_t j0 = blk * ROWS + wave * 32;
         bool valid;
         const int64_t arow = src.row(j0 + i, m, valid);
-        float amax = 0.0f;
+        float amax = 0.0f, ss = 0.0f;
         u16x8 bf[S];
         [&]<int... s>(std::integer_sequence<int, s...>) {
-            ((bf[s] = act_frag<C, G, s>(a, arow, valid, k, vec, h, amax)), ...);
+            ((bf[s] = act_frag<C, G, s>(a, arow, valid, k, vec, h, amax, ss)), ...);
         }(std::make_integer_sequence<int, S>{});
         if (!GATHER && guard_header && chunk == 0)
-            guard_append(amax, amax_limit, valid, arow, h, guard_header, guard_rows, guard_epoch, guard_cap);
+            guard_append(amax, ss, lim, valid, arow, h, guard_header, guard_rows, guard_epoch, guard_cap);
         // rows of this lane's 16 accumulators (r -> row slot 8*(r/4) + 4*h + (r%4))
         int orow[16];  // rows are below 2^31 (the entry points check m)
         bool ovalid[16];
@@ -871,7 +878,7 @@ constexpr int main_lds_bytes() {
 template <int C, int G, int MB, bool GATHER, bool NOREF>
 static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
     stats_main_kernel<C, G, MB, GATHER, NOREF><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
-        x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.p_best, x.p_sum, x.p_idx, x.amax_limit,
+        x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.p_best, x.p_sum, x.p_idx, x.lim,
         x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap);
 }
 
@@ -910,7 +917,7 @@ int rows_cfg(const RowsLaunch& x, int epi, unsigned grid, hipStream_t st) {
     constexpr int LDS = writer_ring<Geo<C, G>::REC>() * Geo<C, G>::BUF;
     auto kern = epi == 0 ? rows_w_kernel<C, G, 0, GATHER> : rows_w_kernel<C, G, 1, GATHER>;
     kern<<<grid, 64 * (kWriterWaves + 1), LDS, st>>>(x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.n, x.nsplit, x.tpc,
-                                                      x.mblocks, x.row_max, x.row_inv, x.out, x.amax_limit,
+                                                      x.mblocks, x.row_max, x.row_inv, x.out, x.lim,
                                                       x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;

@@ -31,6 +31,15 @@ enum Cfg : int { CFG_Q1 = 0, CFG_Q2 = 1, CFG_Q3 = 2, CFG_F1 = 3, CFG_F3 = 4, CFG
 inline bool cfg_is_f16(int cfg) { return cfg == CFG_H2 || cfg == CFG_HF3; }
 inline bool cfg_is_fp32_head(int cfg) { return cfg == CFG_F1 || cfg == CFG_F3 || cfg == CFG_HF3; }
 
+// Which rows a pass of a split mode sends to the rescue: max|a| > prec (the precision
+// limit), or, when the pass skips the softmax's reference shift, rows whose logits are not
+// proven to lie in [-kLogitBound, kLogitBound]: max|a| > range_amax (the bound
+// max|a| * max_c ||w_c||_1) and ||a||_2^2 > range_ss (the bound ||a||_2 * max_c ||w_c||_2,
+// Cauchy-Schwarz).  Infinite limits send nothing.
+struct GuardLimits {
+    float prec, range_amax, range_ss;
+};
+
 // Arguments of one launch of the statistics kernels and of the writer (head_mfma.hpp).
 struct StatsLaunch {
     const float* a;
@@ -41,7 +50,7 @@ struct StatsLaunch {
     float* p_best;
     float* p_sum;
     int* p_idx;
-    float amax_limit;
+    GuardLimits lim;
     unsigned long long* guard_header;
     int* guard_rows;
     unsigned guard_epoch;
@@ -56,7 +65,7 @@ struct RowsLaunch {
     const float* row_max;
     const float* row_inv;
     float* out;
-    float amax_limit;
+    GuardLimits lim;
     unsigned long long* guard_header;
     int* guard_rows;
     unsigned guard_epoch;
@@ -79,10 +88,9 @@ int rows_cfg(const RowsLaunch& x, int epi, unsigned grid, hipStream_t st);
 // append of a call installs it (count 0), and a header with another epoch counts as empty,
 // so a fresh or stale workspace needs no reset.  Paths that end with a merge kernel reset
 // the header to (epoch, 0) there, so a replay of the same call (same epoch) starts empty.
-// The statistics pass may use a lower limit, stats_amax_limit, under which every logit of
-// the row lies in [-kLogitBound, kLogitBound]; its main pass then skips the reference
-// shift of the softmax sum (stats_noref), and the rescue pass, which keeps it, takes the
-// other rows.
+// The statistics pass may skip the reference shift of the softmax sum (stats_noref) when
+// the head bounds its logits: its rescue pass, which keeps the shift, then also takes the
+// rows whose logits are not proven to lie in [-kLogitBound, kLogitBound] (GuardLimits).
 constexpr float kLogitBound = 60.0f;
 struct FmaWeights;
 struct Guard {
@@ -91,7 +99,8 @@ struct Guard {
     int* rows;
     int capacity;  // entries of rows (the batch's row count)
     unsigned epoch;
-    float stats_amax_limit;
+    float range_amax_limit;  // rows up to it have every logit within kLogitBound (L1 bound)
+    float range_ss_limit;    // or rows with ||a||_2^2 up to it (L2 bound)
     bool stats_noref;
     const FmaWeights& fma;  // the head's fp32 weights, for a rescue in fp32 FMA
 };

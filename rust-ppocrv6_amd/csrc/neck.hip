@@ -12,8 +12,8 @@
 //   neck_gemm_kernel   rows x W[K][N] on fp32 MFMA (v_mfma_f32_32x32x2_f32: fp32 products,
 //                      fp32 sums), with the LayerNorm of the rows folded into the operand
 //                      load and bias, swish and the residual Add folded into the epilogue;
-//   neck_attn_kernel   one wave per 4 queries of one head: each 16-lane group streams its
-//                      line's keys with an online softmax, then merges across the group;
+//   neck_attn_kernel   one workgroup per (line, head), the line's keys and values in LDS,
+//                      a 16-lane group per query (two passes: maximum, then sums);
 //   neck_cf_rows_kernel  a line's channels-first [D][T] block to token rows;
 //   neck_final_kernel  the last LayerNorm plus the shortcut.
 #include <algorithm>
@@ -156,65 +156,127 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
 
 // ---------------------------------------------------------------- attention
 // qkv rows [m][3D] hold (q | k | v), each head h at columns h*HD .. h*HD + HD - 1 of its
-// third (the Reshape [0, -1, 3, H, HD] of the graph).  Wave = 4 queries (consecutive rows)
-// of head blockIdx.y; lane group g = lane / 16 owns query row r0 + g, lane j of the group
-// the keys t0 + j, t0 + j + 16, ...: per key s = (q * scale) . k, then a running maximum,
-// sum of exp(s - max) and sum of exp(s - max) * v, rescaled when the maximum rises; the 16
-// partial states merge with xor shuffles; o = (sum e v) / (sum e).  Any line length.
+// third (the Reshape [0, -1, 3, H, HD] of the graph).  One workgroup per (line, head): the
+// line's keys and values of that head are staged once in LDS (rows of kKvStride floats:
+// 16-byte aligned, and the 16 keys a lane group reads at once fall in distinct banks), then
+// each wave takes 4 queries at a time, lane group g = lane / 16 one query, lane j of the
+// group the keys j, j + 16, ...: pass 1 the scores s = (q * scale) . k and their maximum
+// (xor-shuffled over the group), pass 2 the same scores, p = exp(s - max), the sums of p and
+// of p * v, summed over the group; o = (sum p v) / (sum p).  Lines longer than
+// kAttnLdsSteps stream their keys from global memory with a running maximum instead.
+constexpr int kAttnLdsSteps = 256;
+constexpr int kKvStride = 20;
+
+template <int HD>
+__device__ __forceinline__ float score(const float (&q)[16], const float* kr) {
+    const f32x4* k4 = reinterpret_cast<const f32x4*>(kr);
+    float s = 0.0f;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        const f32x4 kv = k4[x];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * x + e < HD) s = fmaf(q[4 * x + e], kv[e], s);
+    }
+    return s;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void neck_attn_kernel(const float* __restrict__ qkv, int64_t m,
                                                         const int64_t* __restrict__ line_off, int64_t lines,
                                                         int64_t line_len, int dim, float scale,
                                                         float* __restrict__ o) {
-    const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+    static_assert(HD <= 16, "a lane group holds one head's query");
+    __shared__ __align__(16) float ks[kAttnLdsSteps * kKvStride];
+    __shared__ __align__(16) float vs[kAttnLdsSteps * kKvStride];
+    const int64_t line = blockIdx.x;
     const int h = blockIdx.y;
-    const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + g;
-    if (r >= m) return;  // a whole 16-lane group leaves together (shuffles stay within it)
-    int64_t t0, t1;
-    const bool in_line = line_of_row(line_off, lines, line_len, m, r, &t0, &t1) >= 0;
+    const int64_t t0 = line_off ? min(max(line_off[line], (int64_t)0), m) : min(line * line_len, m);
+    const int64_t t1 = line_off ? min(max(line_off[line + 1], t0), m) : min(t0 + line_len, m);
+    const int64_t T = t1 - t0;
+    if (T <= 0) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, j = lane & 15;
     const int64_t stride = 3 * (int64_t)dim;
-    float q[HD];
-#pragma unroll
-    for (int d = 0; d < HD; ++d) q[d] = qkv[r * stride + h * HD + d] * scale;
-    float mx = -INFINITY, l = 0.0f, acc[HD];
-#pragma unroll
-    for (int d = 0; d < HD; ++d) acc[d] = 0.0f;
-    if (in_line) {
-        for (int64_t t = t0 + j; t < t1; t += 16) {
-            const float* kr = qkv + t * stride + dim + h * HD;
-            const float* vr = qkv + t * stride + 2 * dim + h * HD;
-            float s = 0.0f;
-#pragma unroll
-            for (int d = 0; d < HD; ++d) s = fmaf(q[d], kr[d], s);
-            const float nm = fmaxf(mx, s);
-            const float corr = (mx == -INFINITY) ? 0.0f : expf(mx - nm);
-            const float p = expf(s - nm);
-            l = fmaf(l, corr, p);
-#pragma unroll
-            for (int d = 0; d < HD; ++d) acc[d] = fmaf(acc[d], corr, p * vr[d]);
-            mx = nm;
+    const bool in_lds = T <= kAttnLdsSteps;
+    if (in_lds) {
+        for (int e = tid; e < (int)T * 16; e += 256) {
+            const int t = e >> 4, d = e & 15;
+            const float* row = qkv + (t0 + t) * stride + h * HD;
+            ks[t * kKvStride + d] = d < HD ? row[dim + d] : 0.0f;
+            vs[t * kKvStride + d] = d < HD ? row[2 * dim + d] : 0.0f;
         }
+        __syncthreads();
     }
+    for (int64_t qi = (int64_t)wave * 4 + g; qi - g < T; qi += 16) {
+        const bool valid = qi < T;  // uniform over the lane group
+        const int64_t r = t0 + qi;
+        float q[16];
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-        const float om = __shfl_xor(mx, off, 64);
-        const float ol = __shfl_xor(l, off, 64);
-        const float nm = fmaxf(mx, om);
-        const float ca = (mx == -INFINITY) ? 0.0f : expf(mx - nm);
-        const float cb = (om == -INFINITY) ? 0.0f : expf(om - nm);
-        l = l * ca + ol * cb;
+        for (int d = 0; d < 16; ++d) q[d] = (valid && d < HD) ? qkv[r * stride + h * HD + d] * scale : 0.0f;
+        float l = 0.0f, acc[HD];
 #pragma unroll
-        for (int d = 0; d < HD; ++d) {
-            const float oa = __shfl_xor(acc[d], off, 64);
-            acc[d] = acc[d] * ca + oa * cb;
+        for (int d = 0; d < HD; ++d) acc[d] = 0.0f;
+        if (in_lds) {
+            float mx = -INFINITY;
+            for (int t = j; t < (int)T; t += 16) mx = fmaxf(mx, score<HD>(q, ks + t * kKvStride));
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            for (int t = j; t < (int)T; t += 16) {
+                const float p = __expf(score<HD>(q, ks + t * kKvStride) - mx);
+                l += p;
+                const f32x4* v4 = reinterpret_cast<const f32x4*>(vs + t * kKvStride);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    const f32x4 vv = v4[x];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * x + e < HD) acc[4 * x + e] = fmaf(p, vv[e], acc[4 * x + e]);
+                }
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                l += __shfl_xor(l, off, 64);
+#pragma unroll
+                for (int d = 0; d < HD; ++d) acc[d] += __shfl_xor(acc[d], off, 64);
+            }
+        } else {
+            float mx = -INFINITY;
+            for (int64_t t = t0 + j; t < t1; t += 16) {
+                const float* kr = qkv + t * stride + dim + h * HD;
+                const float* vr = qkv + t * stride + 2 * dim + h * HD;
+                float s = 0.0f;
+#pragma unroll
+                for (int d = 0; d < HD; ++d) s = fmaf(q[d], kr[d], s);
+                const float nm = fmaxf(mx, s);
+                const float corr = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
+                const float p = __expf(s - nm);
+                l = fmaf(l, corr, p);
+#pragma unroll
+                for (int d = 0; d < HD; ++d) acc[d] = fmaf(acc[d], corr, p * vr[d]);
+                mx = nm;
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                const float om = __shfl_xor(mx, off, 64);
+                const float ol = __shfl_xor(l, off, 64);
+                const float nm = fmaxf(mx, om);
+                const float ca = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
+                const float cb = (om == -INFINITY) ? 0.0f : __expf(om - nm);
+                l = l * ca + ol * cb;
+#pragma unroll
+                for (int d = 0; d < HD; ++d) {
+                    const float oa = __shfl_xor(acc[d], off, 64);
+                    acc[d] = acc[d] * ca + oa * cb;
+                }
+                mx = nm;
+            }
         }
-        mx = nm;
-    }
-    // lane j of the group writes dimension j
-    float mine = 0.0f;
+        // lane j of the group writes dimension j
+        float mine = 0.0f;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) mine = (j == d) ? acc[d] : mine;
-    if (j < HD) o[r * dim + h * HD + j] = (in_line && l > 0.0f) ? __fdiv_rn(mine, l) : 0.0f;
+        for (int d = 0; d < HD; ++d) mine = (j == d) ? acc[d] : mine;
+        if (valid && j < HD) o[r * dim + h * HD + j] = l > 0.0f ? __fdiv_rn(mine, l) : 0.0f;
+    }
 }
 
 // ---------------------------------------------------------------- layouts and the end
@@ -291,6 +353,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: unknown layout");
     if (m <= 0) return PPOCR_OK;
     if (lines <= 0 || (!line_off && line_len <= 0)) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: no lines");
+    if (lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many lines");
     float* x = ws;                       // residual stream [m][D]
     float* sc = x + m * D;               // shortcut rows [m][D]
     float* qkv = sc + m * D;             // [m][3D]
@@ -312,7 +375,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         if (int e = gemm_go<kNeckDim, true, false, false>(x, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b, k.ln1_eps,
                                                           nullptr, qkv, st))
             return e;
-        const dim3 ag((unsigned)((m + 15) / 16), (unsigned)nk.heads);
+        const dim3 ag((unsigned)lines, (unsigned)nk.heads);
         neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
         PPOCR_HIP(hipGetLastError());
         // x = x + proj(att)

@@ -92,9 +92,9 @@ extern "C" {
     pub fn ppocr_rh_shape(h: *const ppocr_rh_t, n: *mut i64, k: *mut i64, quantized: *mut c_int) -> c_int;
     /// The mode PPOCR_MODE_AUTO runs for this head (no counterpart in the reference).
     pub fn ppocr_rh_auto_mode(h: *const ppocr_rh_t) -> c_int;
-    /// Rows above these max |a| limits take the rescue pass (no counterpart in the reference).
-    pub fn ppocr_rh_guard_limits(h: *const ppocr_rh_t, mode: c_int, stats_limit: *mut f32,
-                                 logits_limit: *mut f32) -> c_int;
+    /// Which rows take the rescue pass (no counterpart in the reference).
+    pub fn ppocr_rh_guard_limits(h: *const ppocr_rh_t, mode: c_int, prec_limit: *mut f32,
+                                 range_amax_limit: *mut f32, range_norm_limit: *mut f32) -> c_int;
     pub fn ppocr_rh_workspace_bytes(h: *const ppocr_rh_t, m: i64, mode: c_int) -> usize;
 
     // ---- MatMul.12: matmul_quantized_b (src/ops/matmul.rs:1204-1336) / matmul_transposed_b

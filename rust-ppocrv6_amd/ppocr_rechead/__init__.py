@@ -192,12 +192,21 @@ class RecHead:
         return int(_lib.lib().ppocr_rh_auto_mode(self._h))
 
     def guard_limits(self, mode=None):
-        """(stats_limit, logits_limit): rows whose max |a| exceeds them take the rescue pass
-        of argmax / decode / probabilities, resp. of logits (inf: no guard in this mode)."""
-        st, lg = ctypes.c_float(), ctypes.c_float()
+        """(prec, range_amax, range_norm): a row a takes the rescue pass of argmax / decode /
+        probabilities when max|a| > prec or (max|a| > range_amax and ||a||_2 > range_norm),
+        of logits when max|a| > prec (inf: no such limit in this mode)."""
+        p, ra, rn = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
         _check(_lib.lib().ppocr_rh_guard_limits(self._h, self.default_mode if mode is None else mode,
-                                                ctypes.byref(st), ctypes.byref(lg)))
-        return float(st.value), float(lg.value)
+                                                ctypes.byref(p), ctypes.byref(ra), ctypes.byref(rn)))
+        return float(p.value), float(ra.value), float(rn.value)
+
+    def guarded_rows(self, a, mode=None):
+        """Which rows of a [rows][k] the statistics pass of `mode` sends to the rescue."""
+        prec, ra, rn = self.guard_limits(mode)
+        a = _f32(a).reshape(-1, self.k)
+        amax = np.abs(a).max(axis=1) if a.size else np.zeros(0, np.float32)
+        norm = np.sqrt((a.astype(np.float64) ** 2).sum(axis=1))
+        return (amax > prec) | ((amax > ra) & (norm > rn))
 
     def workspace_bytes(self, m, mode=None):
         return int(_lib.lib().ppocr_rh_workspace_bytes(self._h, m, self.default_mode if mode is None else mode))

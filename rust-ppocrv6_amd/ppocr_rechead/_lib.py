@@ -57,7 +57,8 @@ SIGNATURES = {
     "ppocr_rh_device_bytes": (_sz, [_vp]),
     "ppocr_rh_shape": (_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_int)]),
     "ppocr_rh_auto_mode": (_int, [_vp]),
-    "ppocr_rh_guard_limits": (_int, [_vp, _int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]),
+    "ppocr_rh_guard_limits": (_int, [_vp, _int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float),
+                                     ctypes.POINTER(ctypes.c_float)]),
     "ppocr_rh_workspace_bytes": (_sz, [_vp, _i64, _int]),
     "ppocr_rh_logits": (_int, [_vp, _vp, _i64, _int, _vp]),
     "ppocr_rh_logits_dev": (_int, [_vp, _vp, _i64, _int, _vp, _vp, _sz, _vp]),

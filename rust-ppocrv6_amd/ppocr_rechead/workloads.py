@@ -125,3 +125,38 @@ def make_near_ties(a, rows, q, scales, bias, rng, target_gap=(1e-7, 1e-5), chunk
         a[rr[keep]] = xn[keep]
         ok.extend(rr[keep].tolist())
     return np.asarray(sorted(ok), dtype=np.int64)
+
+
+NECK_DIM, NECK_HEADS, NECK_HIDDEN = 120, 8, 240
+SEED_NECK = 0x5EED0300
+
+
+def neck_weights(seed=SEED_NECK, blocks=2):
+    """Weights of the SVTR tail before the head (ppocr_rn_block_t fields per block, plus the
+    final LayerNorm), seeded normals with the statistics of PP-OCRv6_small_rec's tail:
+    LayerNorm weights ~1 +- 0.2 (final ~3 +- 1.7), MatMul weights 0.045-0.1, biases
+    0.03-0.17."""
+    rng = np.random.default_rng(seed)
+    d, hd = NECK_DIM, NECK_HIDDEN
+
+    def f(*shape, s=1.0, mu=0.0):
+        return (mu + s * rng.standard_normal(shape)).astype(np.float32)
+
+    bl = []
+    for _ in range(blocks):
+        bl.append({"ln1_w": f(d, s=0.2, mu=1.0), "ln1_b": f(d, s=0.3), "ln1_eps": 1e-5,
+                   "qkv_w": f(d, 3 * d, s=0.08), "qkv_b": f(3 * d, s=0.16),
+                   "proj_w": f(d, d, s=0.05), "proj_b": f(d, s=0.03),
+                   "ln2_w": f(d, s=0.2, mu=1.0), "ln2_b": f(d, s=0.3), "ln2_eps": 1e-5,
+                   "fc1_w": f(d, hd, s=0.1), "fc1_b": f(hd, s=0.07),
+                   "fc2_w": f(hd, d, s=0.045), "fc2_b": f(d, s=0.08)})
+    return {"blocks": bl, "lnf_w": f(d, s=1.7, mu=3.0), "lnf_b": f(d, s=0.6, mu=-0.5), "lnf_eps": 1e-6}
+
+
+def neck_flops_per_row(steps, blocks=2):
+    """Algorithmic FLOPs of the tail per token row of a line of `steps` tokens: the four
+    MatMuls of each block (2 D 3D + 2 D D + 2 D H + 2 H D) and its attention (2 steps D for
+    the scores, 2 steps D for the weighted values)."""
+    d, h = NECK_DIM, NECK_HIDDEN
+    return blocks * (2 * d * 3 * d + 2 * d * d + 2 * d * h + 2 * h * d + 4 * steps * d)
+

@@ -12,20 +12,9 @@ SCALE = np.float32(15 ** -0.5)
 
 
 def neck_weights(seed=7, blocks=2):
-    """Blocks as dicts with the fields of ppocr_rn_block_t, plus the final LayerNorm; the
-    scales follow the real model's (LayerNorm weights ~1 +- 0.2, final ~3 +- 1.7, MatMul
-    weights 0.04-0.1, biases 0.03-0.17)."""
-    rng = np.random.default_rng(seed)
-    f = lambda *shape, s=1.0, mu=0.0: (mu + s * rng.standard_normal(shape)).astype(np.float32)
-    bl = []
-    for _ in range(blocks):
-        bl.append({"ln1_w": f(DIM, s=0.2, mu=1.0), "ln1_b": f(DIM, s=0.3), "ln1_eps": 1e-5,
-                   "qkv_w": f(DIM, 3 * DIM, s=0.08), "qkv_b": f(3 * DIM, s=0.16),
-                   "proj_w": f(DIM, DIM, s=0.05), "proj_b": f(DIM, s=0.03),
-                   "ln2_w": f(DIM, s=0.2, mu=1.0), "ln2_b": f(DIM, s=0.3), "ln2_eps": 1e-5,
-                   "fc1_w": f(DIM, HIDDEN, s=0.1), "fc1_b": f(HIDDEN, s=0.07),
-                   "fc2_w": f(HIDDEN, DIM, s=0.045), "fc2_b": f(DIM, s=0.08)})
-    return {"blocks": bl, "lnf_w": f(DIM, s=1.7, mu=3.0), "lnf_b": f(DIM, s=0.6, mu=-0.5), "lnf_eps": 1e-6}
+    """Seeded synthetic tail weights (ppocr_rechead.workloads.neck_weights)."""
+    from ppocr_rechead import workloads as wl
+    return wl.neck_weights(seed=seed, blocks=blocks)
 
 
 def lines_of(lengths):

@@ -61,7 +61,7 @@ def test_argument_errors_do_not_need_a_device(rh):
     assert L.ppocr_softmax_rows(None, -1, 5) == rh.PPOCR_ERR_INVALID_ARG
     assert L.ppocr_rh_footprint_bytes(None) == 0
     assert L.ppocr_rh_auto_mode(None) == -1
-    assert L.ppocr_rh_guard_limits(None, 2, None, None) == rh.PPOCR_ERR_INVALID_ARG
+    assert L.ppocr_rh_guard_limits(None, 2, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
     assert L.ppocr_rh_logits(None, None, 1, 2, None) == rh.PPOCR_ERR_INVALID_ARG
     assert rh._lib.last_error() == "MatMulQuantizedB: null head handle"
 

@@ -264,22 +264,53 @@ def test_tiny_activations(orc, rh, head, mode):
 
 def test_guard_limits_query(orc, rh):
     """ppocr_rh_guard_limits reports the limits the kernels apply: for the INT8 head the
-    precision limits of the bf16 and fp16 splits (logits) and, for the statistics pass,
-    the lower of those and the logit range bound (60 - 1.001 max|bias|) / (1.001 max_c
-    ||w_c||_1); no guard (inf) in the one- and three-term modes and in fp32 FMA."""
+    precision limits of the bf16 and fp16 splits and, for the statistics pass, the logit
+    range bounds (60 - 1.001 max|bias|) / (1.001 max_c ||w_c||_1) on max|a| and
+    (60 - 1.001 max|bias|) / (1.001 max_c ||w_c||_2) on ||a||_2 (the latter squared with a
+    0.1% margin); no guard (inf) in the one- and three-term modes and in fp32 FMA."""
     from ppocr_rechead import workloads as wl
     w_t, bias = wl.weights(stress=True)
     q, s = orc.pack_int8(w_t)
     h = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
     wd = np.abs(q.astype(np.float64)) * s.astype(np.float64)[:, None]
-    rng_lim = (60.0 - 1.001 * float(np.abs(bias).max())) / (1.001 * float(wd.sum(axis=1).max()))
+    room = 60.0 - 1.001 * float(np.abs(bias).max())
+    rng_amax = room / (1.001 * float(wd.sum(axis=1).max()))
+    rng_norm = room / (1.001 * float(np.sqrt((wd * wd).sum(axis=1)).max())) * np.sqrt(0.999)
     for mode, prec in ((2, _int8_limit(q, s)), (4, _f16_limit_int8(q, s))):
-        st, lg = h.guard_limits(mode)
-        print(f"mode {mode}: stats limit {st:.4f}, logits limit {lg:.4f} (precision {prec:.4f}, range {rng_lim:.4f})")
-        assert abs(lg - prec) <= 1e-5 * prec
-        assert abs(st - min(prec, rng_lim)) <= 1e-5 * min(prec, rng_lim)
+        p, ra, rn = h.guard_limits(mode)
+        print(f"mode {mode}: precision {p:.4f} ({prec:.4f}), range max|a| {ra:.4f} ({rng_amax:.4f}), "
+              f"range ||a|| {rn:.4f} ({rng_norm:.4f})")
+        assert abs(p - prec) <= 1e-5 * prec
+        assert abs(ra - rng_amax) <= 1e-5 * rng_amax and abs(rn - rng_norm) <= 1e-5 * rng_norm
     for mode in (0, 1, 3):
-        assert h.guard_limits(mode) == (np.inf, np.inf)
+        assert h.guard_limits(mode) == (np.inf, np.inf, np.inf)
+    h.close()
+
+
+def test_rows_over_the_range_bound_but_within_the_norm_bound(orc, rh, head):
+    """Rows whose max|a| exceeds the logit range bound on max|a| but whose ||a||_2 proves
+    the range (a few large entries, or many moderate ones, as the activations after the
+    SVTR tail's final LayerNorm have) stay on the split path of decode and probabilities
+    and meet the bars there."""
+    h = rh.RecHead(qw=rh.QuantizedWeight(head["q"], head["s"]), bias=head["bias"])
+    prec, ra, rn = h.guard_limits(4)
+    rng = np.random.default_rng(43)
+    a = rng.standard_normal((512, 120)).astype(np.float32)
+    # moderate entries everywhere, scaled so max|a| lies between the two range bounds
+    a *= (np.float32(ra * 1.3) / np.abs(a).max(axis=1))[:, None]
+    keep = np.sqrt((a.astype(np.float64) ** 2).sum(1)) < rn * 0.98
+    a = a[keep][:256]
+    assert a.shape[0] >= 64 and not h.guarded_rows(a, 4).any() and (np.abs(a).max(1) > ra).all()
+    off = np.array([0, 100, a.shape[0]], np.int64)
+    for mode in (4, 2):
+        got = h.decode(a, off, mode=mode)
+        ref = orc.rechead_lines(a, off, head["q"], head["s"], head["bias"])
+        lg = f64_logits_q(a, head["q"], head["s"], head["bias"])
+        check_argmax(got["idx"], ref["idx"], top2_gap(lg), label=f"range by norm, mode {mode}")
+        assert_close_rel(got["maxprob"], ref["maxprob"], f"range by norm maxprob mode {mode}", row_scale=rel_scale(lg))
+        probs = h.probs(a[:64], mode)
+        refp = orc.softmax_rows(orc.matmul_quantized_b(a[:64], head["q"], head["s"], head["bias"]))
+        assert_close_rel(probs, refp, f"range by norm probs mode {mode}", row_scale=rel_scale(lg[:64]))
     h.close()
 
 
@@ -308,10 +339,11 @@ def test_f16x2_outlier_head_needs_no_rescue_for_ordinary_rows(orc, rh):
 
 
 def test_auto_mode_picks_per_head_and_matches_the_explicit_mode(orc, rh):
-    """MODE_AUTO, the default: the bf16 split for a head whose bf16 limit is at least 8 (the
-    synthetic INT8 head, ~11.7), the fp16 split for one whose large weight rows pull it
-    below (the stress head, ~1.6; the synthetic FP32 head, ~5.8).  Its results are those of
-    the explicit mode, bit for bit, on logits and on the decode."""
+    """MODE_AUTO, the default: the fp16 split unless the bf16 limit is at least 32 (then the
+    bf16 split): the synthetic INT8 head (~11.7), the stress head (~1.6) and the synthetic
+    FP32 head (~5.8) all take the fp16 split, a head with weights 1/8 as large (limit ~94)
+    the bf16 one.  Its results are those of the explicit mode, bit for bit, on logits and
+    on the decode."""
     from ppocr_rechead import workloads as wl
     rng = np.random.default_rng(41)
     a = rng.standard_normal((512, 120)).astype(np.float32)
@@ -324,15 +356,18 @@ def test_auto_mode_picks_per_head_and_matches_the_explicit_mode(orc, rh):
     q2, s2 = orc.pack_int8(w_t2)
     cases.append(("int8 stress", rh.RecHead(qw=rh.QuantizedWeight(q2, s2), bias=bias2), _int8_limit(q2, s2)))
     cases.append(("fp32", rh.RecHead(w_t=w_t, bias=bias), _f32_limit(w_t)))
+    w_s = (w_t / np.float32(8.0)).astype(np.float32)
+    q3, s3 = orc.pack_int8(w_s)
+    cases.append(("int8 small weights", rh.RecHead(qw=rh.QuantizedWeight(q3, s3), bias=bias), _int8_limit(q3, s3)))
     for name, h, lim in cases:
-        want = (rh.MODE_BF16X2 if h.quantized else rh.MODE_BF16X3) if lim >= 8.0 else rh.MODE_F16X2
+        want = (rh.MODE_BF16X2 if h.quantized else rh.MODE_BF16X3) if lim >= 32.0 else rh.MODE_F16X2
         print(f"{name}: bf16 limit {lim:.2f} -> auto mode {h.auto_mode()}", flush=True)
         assert h.auto_mode() == want
         assert h.default_mode == rh.MODE_AUTO
-        st, lg = h.guard_limits(want)
-        assert st <= lg and (st == lg or h.quantized)
+        prec, ra, rn = h.guard_limits(want)
+        assert h.quantized or (ra == np.inf and rn == np.inf)
         if want != rh.MODE_F16X2:
-            assert abs(lg - lim) <= 1e-5 * lim, (lg, lim)
+            assert abs(prec - lim) <= 1e-5 * lim, (prec, lim)
         np.testing.assert_array_equal(h.logits(a), h.logits(a, want))
         d_auto, d_want = h.decode(a, off), h.decode(a, off, mode=want)
         for key in ("idx", "maxprob", "score"):
