@@ -315,7 +315,8 @@ int ppocr_rn_shape(const ppocr_rn_t* h, int64_t* dim, int64_t* heads, int64_t* h
 size_t ppocr_rn_workspace_bytes(const ppocr_rn_t* h, int64_t m);
 /* out [m][dim] token rows = the tail applied to x and shortcut (both in `layout`), lines
  * by d_line_off[0..lines] (read on the device, clamped into [0, m]; attention never mixes
- * tokens of different lines). */
+ * tokens of different lines).  d_workspace: ppocr_rn_workspace_bytes(h, m) bytes, 16-byte
+ * aligned, or NULL (stream-ordered scratch). */
 int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_shortcut, int64_t m,
                          const int64_t* d_line_off, int64_t lines, int layout, float* d_out, void* d_workspace,
                          size_t workspace_bytes, void* stream);

@@ -1428,6 +1428,8 @@ int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_s
     if (!d_x || !d_shortcut || !d_out || !d_line_off || lines == 0)
         return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null pointer or no lines");
     const size_t need = ppocr_rn_workspace_bytes(h, m);
+    if (reinterpret_cast<uintptr_t>(d_workspace) & 15)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: the workspace must be 16-byte aligned");
     DeviceGuard dg(h->device);
     if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecNeckHip: hipSetDevice failed");
     hipStream_t st = static_cast<hipStream_t>(stream);

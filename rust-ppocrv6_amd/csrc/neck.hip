@@ -12,8 +12,8 @@
 //   neck_gemm_kernel   rows x W[K][N] on fp32 MFMA (v_mfma_f32_32x32x2_f32: fp32 products,
 //                      fp32 sums), with the LayerNorm of the rows folded into the operand
 //                      load and bias, swish and the residual Add folded into the epilogue;
-//   neck_attn_kernel   one workgroup per (line, head), the line's keys and values in LDS,
-//                      a 16-lane group per query (two passes: maximum, then sums);
+//   neck_attn_kernel   one workgroup per (line, head): the line's K, Q and V of the head in
+//                      LDS, scores and weighted sums on fp32 MFMA, the softmax between;
 //   neck_cf_rows_kernel  a line's channels-first [D][T] block to token rows;
 //   neck_final_kernel  the last LayerNorm plus the shortcut.
 #include <algorithm>
@@ -57,7 +57,7 @@ __device__ __forceinline__ int64_t line_of_row(const int64_t* line_off, int64_t 
 // ---------------------------------------------------------------- GEMM
 // out[r][n] = EPI(LN?(a[r])[.] . W[.][n] + bias[n]) (+ res[r][n]), W row-major [K][N] as the
 // model stores a MatMul weight.  A workgroup owns 128 rows x 128 columns; each wave 32 rows x
-// 4 tiles of 32 columns.  The contraction index is split in halves: lanes 0-31 take
+// 4 tiles of 32 columns, interleaved (tile t holds columns n0 + 4 i + t).  The contraction index is split in halves: lanes 0-31 take
 // k = s, lanes 32-63 take k = K/2 + s at MFMA step s, so each lane holds one contiguous half
 // of its row in registers (and can normalise it: the row's two halves meet in one xor-32
 // shuffle).  The workgroup's W columns are staged once in LDS.
@@ -75,19 +75,21 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
     extern __shared__ __align__(16) float wl[];  // [K][kGemmCols]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, half = lane >> 5;
     const int n0 = blockIdx.y * kGemmCols;
-    // stage W[:, n0 .. n0 + 128) (columns past n as zeros)
-    for (int e = tid; e < K * (kGemmCols / 4); e += 256) {
-        const int kk = e / (kGemmCols / 4), c4 = (e % (kGemmCols / 4)) * 4;
-        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        const float* src = w + (size_t)kk * n + n0 + c4;
-        if (n0 + c4 + 3 < n) {
-            v = f32x4{src[0], src[1], src[2], src[3]};
-        } else {
-#pragma unroll
-            for (int x = 0; x < 4; ++x)
-                if (n0 + c4 + x < n) v[x] = src[x];
-        }
-        *reinterpret_cast<f32x4*>(wl + kk * kGemmCols + c4) = v;
+    // stage W[:, n0 .. n0 + 128) straight from global memory into LDS, all loads in flight
+    // at once: one instruction of a wave fills two rows of the stage (64 lanes x 16 bytes),
+    // lane L row 2x + L / 32, columns 4 (L % 32) .. + 3.  n is a multiple of 4 and W 16-byte
+    // aligned, so a 16-byte chunk lies wholly inside or outside the columns; a chunk past n
+    // reloads the row's first chunk instead (it lands in columns whose results are never
+    // stored, and each output column depends only on its own W column).
+    static_assert(K % 2 == 0, "two stage rows per instruction");
+    for (int x = wave; x < K / 2; x += 4) {
+        const int kk = 2 * x + (lane >> 5), c4 = n0 + 4 * (lane & 31);
+        const float* src = w + (size_t)kk * n + (c4 < n ? c4 : 0);
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void*>(src),
+            reinterpret_cast<__attribute__((address_space(3))) void*>(
+                reinterpret_cast<uintptr_t>(wl + (size_t)x * 2 * kGemmCols)),
+            16, 0, 0);
     }
     // this lane's half row
     const int64_t row = (int64_t)blockIdx.x * kGemmRows + wave * 32 + i;
@@ -123,62 +125,134 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
 #pragma unroll
         for (int x = 0; x < KH; ++x) av[x] = fmaf((av[x] - mean) * inv, ln_w[half * KH + x], ln_b[half * KH + x]);
     }
+    // the direct loads count in this wave's vmcnt: wait for them, then for the other waves'
+    __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
     __syncthreads();
 
+    // MFMA column i of tile t is W column n0 + 4 i + t: a lane's four B operands of a step are
+    // one 16-byte LDS read, issued kWPrefetch steps ahead of its MFMAs
+    constexpr int kWPrefetch = 4;
     f32x16 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
+    const float* wbase = wl + half * KH * kGemmCols + 4 * i;
+    f32x4 wq[kWPrefetch];
 #pragma unroll
-    for (int s = 0; s < KH; ++s) {
-        const float* wr = wl + (half * KH + s) * kGemmCols + i;
+    for (int p = 0; p < kWPrefetch; ++p) wq[p] = *reinterpret_cast<const f32x4*>(wbase + p * kGemmCols);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], wr[32 * t], acc[t], 0, 0, 0);
+    for (int st = 0; st < KH; ++st) {
+        const f32x4 cur = wq[st % kWPrefetch];
+        if (st + kWPrefetch < KH)
+            wq[st % kWPrefetch] = *reinterpret_cast<const f32x4*>(wbase + (st + kWPrefetch) * kGemmCols);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[st], cur[t], acc[t], 0, 0, 0);
     }
 
-    // epilogue: lane (i, half) holds column n0 + 32t + i of rows 8(r/4) + 4 half + r%4
+    // epilogue: lane (i, half) holds columns n0 + 4i .. + 3 (tile t: + t) of rows
+    // 8(r/4) + 4 half + r%4; the four columns are one 16-byte chunk, wholly inside or
+    // outside [0, n).  The residual Add reads the rows it overwrites (res == out in place),
+    // so every residual is loaded before the first store: with the stores in between, each
+    // load would wait for the one before it.
     const int64_t rbase = (int64_t)blockIdx.x * kGemmRows + wave * 32;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int col = n0 + 32 * t + i;
-        if (col >= n) continue;
-        const float bc = bias[col];
+    const int col = n0 + 4 * i;
+    if (col >= n) return;
+    const f32x4 bc = *reinterpret_cast<const f32x4*>(bias + col);
+    f32x4 rv[16];
+    if constexpr (RES) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (rr >= m) continue;
-            float v = acc[t][r] + bc;
-            if constexpr (SWISH) v = swish_of(v);
-            if constexpr (RES) v = res[rr * n + col] + v;
-            out[rr * n + col] = v;
+            rv[r] = rr < m ? *reinterpret_cast<const f32x4*>(res + rr * n + col) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (rr >= m) continue;
+        f32x4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float x = acc[t][r] + bc[t];
+            if constexpr (SWISH) x = swish_of(x);
+            if constexpr (RES) x = rv[r][t] + x;
+            v[t] = x;
+        }
+        *reinterpret_cast<f32x4*>(out + rr * n + col) = v;
     }
 }
 
 // ---------------------------------------------------------------- attention
-// qkv rows [m][3D] hold (q | k | v), each head h at columns h*HD .. h*HD + HD - 1 of its
-// third (the Reshape [0, -1, 3, H, HD] of the graph).  One workgroup per (line, head): the
-// line's keys and values of that head are staged once in LDS (rows of kKvStride floats:
-// 16-byte aligned, and the 16 keys a lane group reads at once fall in distinct banks), then
-// each wave takes 4 queries at a time, lane group g = lane / 16 one query, lane j of the
-// group the keys j, j + 16, ...: pass 1 the scores s = (q * scale) . k and their maximum
-// (xor-shuffled over the group), pass 2 the same scores, p = exp(s - max), the sums of p and
-// of p * v, summed over the group; o = (sum p v) / (sum p).  Lines longer than
-// kAttnLdsSteps stream their keys from global memory with a running maximum instead.
-constexpr int kAttnLdsSteps = 256;
-constexpr int kKvStride = 20;
+// One workgroup per (line, head).  Lines of up to kAttnMfmaSteps steps run on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32: fp32 products and sums, the reference's arithmetic class): the
+// head's K, Q * scale and V of the line are staged once in LDS, then each wave takes blocks
+// of 16 queries and computes
+//   S^T = K Q^T   (key tiles of 16 x 16, contraction over the head's dims, 15 padded to 16);
+//   the softmax over the keys, per query (column) of S^T: its maximum and sum meet in two
+//   xor shuffles across the lane groups;
+//   O^T = V^T P^T (contraction over the keys).
+// In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + j, j < 4;
+// A and B operands: lane l holds row (A) or column (B) l % 16 at contraction index l / 16.
+// So lane l's scores are query l % 16 at keys 16 t + 4 g + j (g = l / 16), and the second
+// product takes, at MFMA step s of key tile t, key 16 t + 4 g + s for lane group g on both
+// operands: P^T's operand is then the lane's own score j = s, with no data movement.  Dims
+// are stored permuted (dim 4 s + g at position 4 g + s) so that one 16-byte LDS read gives a
+// lane its four contraction steps.  Lines longer than kAttnMfmaSteps stream their keys from
+// global memory with a running maximum (a 16-lane group per query) instead.
+constexpr int kAttnMfmaSteps = 256;
+constexpr int kVtStride = kAttnMfmaSteps + 4;
+
+__device__ __forceinline__ int perm_dim(int d) { return 4 * (d & 3) + (d >> 2); }
 
 template <int HD>
-__device__ __forceinline__ float score(const float (&q)[16], const float* kr) {
-    const f32x4* k4 = reinterpret_cast<const f32x4*>(kr);
-    float s = 0.0f;
+__device__ __forceinline__ void attn_stream(const float* __restrict__ qkv, int64_t t0, int64_t t1, int h, int dim,
+                                            float scale, int tid, float* __restrict__ o) {
+    const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, j = lane & 15;
+    const int64_t T = t1 - t0;
+    const int64_t stride = 3 * (int64_t)dim;
+    for (int64_t qi = (int64_t)wave * 4 + g; qi - g < T; qi += 16) {
+        const bool valid = qi < T;  // uniform over the lane group
+        const int64_t r = t0 + qi;
+        float q[HD];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-        const f32x4 kv = k4[x];
+        for (int d = 0; d < HD; ++d) q[d] = valid ? qkv[r * stride + h * HD + d] * scale : 0.0f;
+        float l = 0.0f, acc[HD], mx = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (4 * x + e < HD) s = fmaf(q[4 * x + e], kv[e], s);
+        for (int d = 0; d < HD; ++d) acc[d] = 0.0f;
+        for (int64_t t = t0 + j; t < t1; t += 16) {
+            const float* kr = qkv + t * stride + dim + h * HD;
+            const float* vr = qkv + t * stride + 2 * dim + h * HD;
+            float sc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < HD; ++d) sc = fmaf(q[d], kr[d], sc);
+            const float nm = fmaxf(mx, sc);
+            const float corr = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
+            const float p = __expf(sc - nm);
+            l = fmaf(l, corr, p);
+#pragma unroll
+            for (int d = 0; d < HD; ++d) acc[d] = fmaf(acc[d], corr, p * vr[d]);
+            mx = nm;
+        }
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const float om = __shfl_xor(mx, off, 64);
+            const float ol = __shfl_xor(l, off, 64);
+            const float nm = fmaxf(mx, om);
+            const float ca = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
+            const float cb = (om == -INFINITY) ? 0.0f : __expf(om - nm);
+            l = l * ca + ol * cb;
+#pragma unroll
+            for (int d = 0; d < HD; ++d) {
+                const float oa = __shfl_xor(acc[d], off, 64);
+                acc[d] = acc[d] * ca + oa * cb;
+            }
+            mx = nm;
+        }
+        // lane j of the group writes dimension j
+        float mine = 0.0f;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) mine = (j == d) ? acc[d] : mine;
+        if (valid && j < HD) o[r * dim + h * HD + j] = l > 0.0f ? __fdiv_rn(mine, l) : 0.0f;
     }
-    return s;
 }
 
 template <int HD>
@@ -186,96 +260,101 @@ __global__ __launch_bounds__(256) void neck_attn_kernel(const float* __restrict_
                                                         const int64_t* __restrict__ line_off, int64_t lines,
                                                         int64_t line_len, int dim, float scale,
                                                         float* __restrict__ o) {
-    static_assert(HD <= 16, "a lane group holds one head's query");
-    __shared__ __align__(16) float ks[kAttnLdsSteps * kKvStride];
-    __shared__ __align__(16) float vs[kAttnLdsSteps * kKvStride];
+    static_assert(HD <= 16, "one 16-wide MFMA tile holds a head's dims");
+    constexpr int NT = kAttnMfmaSteps / 16;  // key tiles at most
+    __shared__ __align__(16) float ks[kAttnMfmaSteps * 16];  // K [t][dim permuted]
+    __shared__ __align__(16) float qs[kAttnMfmaSteps * 16];  // Q * scale [t][dim permuted]
+    __shared__ __align__(16) float vt[16 * kVtStride];       // V^T [dim][t]
     const int64_t line = blockIdx.x;
     const int h = blockIdx.y;
     const int64_t t0 = line_off ? min(max(line_off[line], (int64_t)0), m) : min(line * line_len, m);
     const int64_t t1 = line_off ? min(max(line_off[line + 1], t0), m) : min(t0 + line_len, m);
-    const int64_t T = t1 - t0;
-    if (T <= 0) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, j = lane & 15;
-    const int64_t stride = 3 * (int64_t)dim;
-    const bool in_lds = T <= kAttnLdsSteps;
-    if (in_lds) {
-        for (int e = tid; e < (int)T * 16; e += 256) {
-            const int t = e >> 4, d = e & 15;
-            const float* row = qkv + (t0 + t) * stride + h * HD;
-            ks[t * kKvStride + d] = d < HD ? row[dim + d] : 0.0f;
-            vs[t * kKvStride + d] = d < HD ? row[2 * dim + d] : 0.0f;
-        }
-        __syncthreads();
+    const int64_t T64 = t1 - t0;
+    if (T64 <= 0) return;
+    const int tid = threadIdx.x;
+    if (T64 > kAttnMfmaSteps) {
+        attn_stream<HD>(qkv, t0, t1, h, dim, scale, tid, o);
+        return;
     }
-    for (int64_t qi = (int64_t)wave * 4 + g; qi - g < T; qi += 16) {
-        const bool valid = qi < T;  // uniform over the lane group
-        const int64_t r = t0 + qi;
-        float q[16];
+    const int T = (int)T64, nt = (T + 15) >> 4;
+    const int64_t stride = 3 * (int64_t)dim;
+    // stage 16 * nt rows (zeros past the line's end and past the head's dims)
+    for (int e = tid; e < nt * 256; e += 256) {
+        const int t = e >> 4, d = e & 15;
+        float kv = 0.0f, qv = 0.0f, vv = 0.0f;
+        if (t < T && d < HD) {
+            const float* row = qkv + (t0 + t) * stride + h * HD + d;
+            qv = row[0] * scale;
+            kv = row[dim];
+            vv = row[2 * dim];
+        }
+        ks[t * 16 + perm_dim(d)] = kv;
+        qs[t * 16 + perm_dim(d)] = qv;
+        vt[d * kVtStride + t] = vv;
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
+    for (int qb = wave; qb < nt; qb += 4) {
+        const int q0 = 16 * qb;
+        const f32x4 qf = *reinterpret_cast<const f32x4*>(qs + (q0 + c) * 16 + 4 * g);
+        f32x4 sc[NT];
 #pragma unroll
-        for (int d = 0; d < 16; ++d) q[d] = (valid && d < HD) ? qkv[r * stride + h * HD + d] * scale : 0.0f;
-        float l = 0.0f, acc[HD];
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+                const f32x4 kf = *reinterpret_cast<const f32x4*>(ks + (16 * t + c) * 16 + 4 * g);
+                f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int d = 0; d < HD; ++d) acc[d] = 0.0f;
-        if (in_lds) {
-            float mx = -INFINITY;
-            for (int t = j; t < (int)T; t += 16) mx = fmaxf(mx, score<HD>(q, ks + t * kKvStride));
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            for (int t = j; t < (int)T; t += 16) {
-                const float p = __expf(score<HD>(q, ks + t * kKvStride) - mx);
-                l += p;
-                const f32x4* v4 = reinterpret_cast<const f32x4*>(vs + t * kKvStride);
-#pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                    const f32x4 vv = v4[x];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (4 * x + e < HD) acc[4 * x + e] = fmaf(p, vv[e], acc[4 * x + e]);
-                }
-            }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-                l += __shfl_xor(l, off, 64);
-#pragma unroll
-                for (int d = 0; d < HD; ++d) acc[d] += __shfl_xor(acc[d], off, 64);
-            }
-        } else {
-            float mx = -INFINITY;
-            for (int64_t t = t0 + j; t < t1; t += 16) {
-                const float* kr = qkv + t * stride + dim + h * HD;
-                const float* vr = qkv + t * stride + 2 * dim + h * HD;
-                float s = 0.0f;
-#pragma unroll
-                for (int d = 0; d < HD; ++d) s = fmaf(q[d], kr[d], s);
-                const float nm = fmaxf(mx, s);
-                const float corr = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
-                const float p = __expf(s - nm);
-                l = fmaf(l, corr, p);
-#pragma unroll
-                for (int d = 0; d < HD; ++d) acc[d] = fmaf(acc[d], corr, p * vr[d]);
-                mx = nm;
-            }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-                const float om = __shfl_xor(mx, off, 64);
-                const float ol = __shfl_xor(l, off, 64);
-                const float nm = fmaxf(mx, om);
-                const float ca = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
-                const float cb = (om == -INFINITY) ? 0.0f : __expf(om - nm);
-                l = l * ca + ol * cb;
-#pragma unroll
-                for (int d = 0; d < HD; ++d) {
-                    const float oa = __shfl_xor(acc[d], off, 64);
-                    acc[d] = acc[d] * ca + oa * cb;
-                }
-                mx = nm;
+                for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[s], acc, 0, 0, 0);
+                sc[t] = acc;
             }
         }
-        // lane j of the group writes dimension j
-        float mine = 0.0f;
+        // the maximum over the line's keys of query q0 + c: this lane's keys, then the four
+        // lane groups
+        float mx = -INFINITY;
 #pragma unroll
-        for (int d = 0; d < HD; ++d) mine = (j == d) ? acc[d] : mine;
-        if (valid && j < HD) o[r * dim + h * HD + j] = l > 0.0f ? __fdiv_rn(mine, l) : 0.0f;
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    if (16 * t + 4 * g + jj < T) mx = fmaxf(mx, sc[t][jj]);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float l = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float p = (16 * t + 4 * g + jj < T) ? __expf(sc[t][jj] - mx) : 0.0f;
+                    sc[t][jj] = p;
+                    l += p;
+                }
+            }
+        }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        // O^T = V^T P^T, even and odd key tiles on two accumulators
+        f32x4 oa = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, ob = oa;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+                const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + c * kVtStride + 16 * t + 4 * g);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    if (t & 1) ob = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[s], sc[t][s], ob, 0, 0, 0);
+                    else oa = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[s], sc[t][s], oa, 0, 0, 0);
+                }
+            }
+        }
+        // lane l: query q0 + c, dims 4 g + j
+        if (q0 + c < T) {
+            float* orow = o + (t0 + q0 + c) * dim + h * HD;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                if (4 * g + jj < HD) orow[4 * g + jj] = __fdiv_rn(oa[jj] + ob[jj], l);
+        }
     }
 }
 

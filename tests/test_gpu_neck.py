@@ -36,7 +36,8 @@ def _check(got, ref, label):
     assert np.all(err <= bar), label
 
 
-@pytest.mark.parametrize("lengths", [[1], [7, 40, 1, 120, 3], [240, 240, 97]])
+@pytest.mark.parametrize("lengths", [[1], [7, 40, 1, 120, 3], [240, 240, 97], [16, 17, 255, 256, 31],
+                                     [300, 257, 5]])
 def test_neck_matches_the_oracle(orc, rh, lengths):
     w = neck_weights()
     neck = _make(rh, w)
