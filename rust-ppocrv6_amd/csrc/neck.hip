@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
                                                         const float* res, float* out) {
     constexpr int KH = K / 2;
     static_assert(K % 8 == 0, "rows are loaded 4 floats at a time per half");
-    extern __shared__ __align__(16) float wl[];  // [K][kGemmCols]
+    extern __shared__ __align__(16) float wl[];  // [K][kGemmCols], then (LN) [2][K]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, half = lane >> 5;
     const int n0 = blockIdx.y * kGemmCols;
     // stage W[:, n0 .. n0 + 128) straight from global memory into LDS, all loads in flight
@@ -91,6 +91,19 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
                 reinterpret_cast<uintptr_t>(wl + (size_t)x * 2 * kGemmCols)),
             16, 0, 0);
     }
+    // the LayerNorm weights and biases after the stage ([K] then [K]), by wave 0: lane L the
+    // 16-byte chunk L of the two
+    float* lnl = wl + K * kGemmCols;
+    if constexpr (LN) {
+        static_assert(K % 4 == 0 && K / 2 <= 64, "LayerNorm parameters in one instruction");
+        if (wave == 0 && lane < K / 2) {
+            const float* src = lane < K / 4 ? ln_w + 4 * lane : ln_b + 4 * (lane - K / 4);
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(lnl)), 16, 0,
+                0);
+        }
+    }
     // this lane's half row
     const int64_t row = (int64_t)blockIdx.x * kGemmRows + wave * 32 + i;
     float av[KH];
@@ -108,12 +121,13 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
 #pragma unroll
         for (int x = 0; x < KH; ++x) av[x] = 0.0f;
     }
+    float mean = 0.0f, inv = 0.0f;
     if constexpr (LN) {
         float s = 0.0f;
 #pragma unroll
         for (int x = 0; x < KH; ++x) s += av[x];
         s += __shfl_xor(s, 32, 64);
-        const float mean = __fdiv_rn(s, (float)K);
+        mean = __fdiv_rn(s, (float)K);
         float v = 0.0f;
 #pragma unroll
         for (int x = 0; x < KH; ++x) {
@@ -121,13 +135,15 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
             v = fmaf(d, d, v);
         }
         v += __shfl_xor(v, 32, 64);
-        const float inv = inv_std_of(__fdiv_rn(v, (float)K), eps);
-#pragma unroll
-        for (int x = 0; x < KH; ++x) av[x] = fmaf((av[x] - mean) * inv, ln_w[half * KH + x], ln_b[half * KH + x]);
+        inv = inv_std_of(__fdiv_rn(v, (float)K), eps);
     }
     // the direct loads count in this wave's vmcnt: wait for them, then for the other waves'
     __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
     __syncthreads();
+    if constexpr (LN) {
+#pragma unroll
+        for (int x = 0; x < KH; ++x) av[x] = fmaf((av[x] - mean) * inv, lnl[half * KH + x], lnl[K + half * KH + x]);
+    }
 
     // MFMA column i of tile t is W column n0 + 4 i + t: a lane's four B operands of a step are
     // one 16-byte LDS read, issued kWPrefetch steps ahead of its MFMAs
@@ -165,10 +181,7 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
             rv[r] = rr < m ? *reinterpret_cast<const f32x4*>(res + rr * n + col) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (rr >= m) continue;
+    auto value = [&](int r) {
         f32x4 v;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -177,7 +190,22 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
             if constexpr (RES) x = rv[r][t] + x;
             v[t] = x;
         }
-        *reinterpret_cast<f32x4*>(out + rr * n + col) = v;
+        return v;
+    };
+    // a block wholly inside the batch stores without a branch per row: at a branch the
+    // compiler waits for every access in flight (stores included), once per row
+    if (rbase + 32 <= m) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+            *reinterpret_cast<f32x4*>(out + rr * n + col) = value(r);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (rr < m) *reinterpret_cast<f32x4*>(out + rr * n + col) = value(r);
+        }
     }
 }
 
@@ -278,19 +306,30 @@ __global__ __launch_bounds__(256) void neck_attn_kernel(const float* __restrict_
     }
     const int T = (int)T64, nt = (T + 15) >> 4;
     const int64_t stride = 3 * (int64_t)dim;
-    // stage 16 * nt rows (zeros past the line's end and past the head's dims)
-    for (int e = tid; e < nt * 256; e += 256) {
-        const int t = e >> 4, d = e & 15;
-        float kv = 0.0f, qv = 0.0f, vv = 0.0f;
-        if (t < T && d < HD) {
-            const float* row = qkv + (t0 + t) * stride + h * HD + d;
-            qv = row[0] * scale;
-            kv = row[dim];
-            vv = row[2 * dim];
+    // stage 16 * nt rows (zeros past the line's end and past the head's dims): thread tid
+    // takes dim tid % 16 of rows tid / 16 + 16 x, every load issued before the first LDS
+    // store (a loop of load, wait, store would wait once per row group)
+    const int sd = tid & 15, st0 = tid >> 4;
+    float kv[NT], qv[NT], vv[NT];
+#pragma unroll
+    for (int x = 0; x < NT; ++x) {
+        const int t = st0 + 16 * x;
+        kv[x] = qv[x] = vv[x] = 0.0f;
+        if (x < nt && t < T && sd < HD) {
+            const float* row = qkv + (t0 + t) * stride + h * HD + sd;
+            qv[x] = row[0];  // scaled at the store: a use here would wait for the load
+            kv[x] = row[dim];
+            vv[x] = row[2 * dim];
         }
-        ks[t * 16 + perm_dim(d)] = kv;
-        qs[t * 16 + perm_dim(d)] = qv;
-        vt[d * kVtStride + t] = vv;
+    }
+#pragma unroll
+    for (int x = 0; x < NT; ++x) {
+        if (x < nt) {
+            const int t = st0 + 16 * x;
+            ks[t * 16 + perm_dim(sd)] = kv[x];
+            qs[t * 16 + perm_dim(sd)] = qv[x] * scale;
+            vt[sd * kVtStride + t] = vv[x];
+        }
     }
     __syncthreads();
     const int lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
@@ -415,7 +454,8 @@ int gemm_go(const float* a, int64_t m, const float* w, int n, const float* bias,
     const int64_t gx = (m + kGemmRows - 1) / kGemmRows;
     const int gy = (n + kGemmCols - 1) / kGemmCols;
     if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
-    neck_gemm_kernel<K, LN, SWISH, RES><<<dim3((unsigned)gx, (unsigned)gy), 256, K * kGemmCols * 4, st>>>(
+    const size_t lds = (size_t)K * kGemmCols * 4 + (LN ? 2 * K * 4 : 0);
+    neck_gemm_kernel<K, LN, SWISH, RES><<<dim3((unsigned)gx, (unsigned)gy), 256, lds, st>>>(
         a, m, w, n, bias, ln_w, ln_b, eps, res, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
