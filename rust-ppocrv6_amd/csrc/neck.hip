@@ -210,77 +210,36 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------- attention
-// One workgroup per (line, head).  Lines of up to kAttnMfmaSteps steps run on fp32 MFMA
-// (v_mfma_f32_16x16x4_f32: fp32 products and sums, the reference's arithmetic class): the
-// head's K, Q * scale and V of the line are staged once in LDS, then each wave takes blocks
-// of 16 queries and computes
-//   S^T = K Q^T   (key tiles of 16 x 16, contraction over the head's dims, 15 padded to 16);
-//   the softmax over the keys, per query (column) of S^T: its maximum and sum meet in two
-//   xor shuffles across the lane groups;
-//   O^T = V^T P^T (contraction over the keys).
+// One workgroup per (line, head), on fp32 MFMA (v_mfma_f32_16x16x4_f32: fp32 products and
+// sums, the reference's arithmetic class).  Each wave takes blocks of 16 queries (up to
+// kAttnQBlocks of them per pass over the keys, 4 * 16 * kAttnQBlocks queries per pass) and,
+// for every block of kAttnKeys keys staged in LDS (K with its dims permuted, V transposed):
+//   S^T = K Q^T      key tiles of 16 x 16, contraction over the head's dims (15 padded to 16);
+//   the block's maximum per query (column of S^T), meeting across the lane groups in two
+//   xor shuffles; the running maximum, and the rescaling of the running sums by
+//   exp(old - new) (an online softmax: the first block of a line needs no rescaling);
+//   O^T += V^T P^T   contraction over the block's keys.
 // In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + j, j < 4;
 // A and B operands: lane l holds row (A) or column (B) l % 16 at contraction index l / 16.
 // So lane l's scores are query l % 16 at keys 16 t + 4 g + j (g = l / 16), and the second
 // product takes, at MFMA step s of key tile t, key 16 t + 4 g + s for lane group g on both
 // operands: P^T's operand is then the lane's own score j = s, with no data movement.  Dims
 // are stored permuted (dim 4 s + g at position 4 g + s) so that one 16-byte LDS read gives a
-// lane its four contraction steps.  Lines longer than kAttnMfmaSteps stream their keys from
-// global memory with a running maximum (a 16-lane group per query) instead.
-constexpr int kAttnMfmaSteps = 256;
-constexpr int kVtStride = kAttnMfmaSteps + 4;
+// lane its four contraction steps.  o = (sum p v) / (sum p) per query.
+constexpr int kAttnKeys = 128;                 // keys per LDS block
+constexpr int kAttnKeyTiles = kAttnKeys / 16;  // 16-key tiles per block
+constexpr int kAttnQBlocks = 2;                // 16-query blocks per wave and pass
+constexpr int kVtStride = kAttnKeys + 4;
 
 __device__ __forceinline__ int perm_dim(int d) { return 4 * (d & 3) + (d >> 2); }
 
-template <int HD>
-__device__ __forceinline__ void attn_stream(const float* __restrict__ qkv, int64_t t0, int64_t t1, int h, int dim,
-                                            float scale, int tid, float* __restrict__ o) {
-    const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, j = lane & 15;
-    const int64_t T = t1 - t0;
-    const int64_t stride = 3 * (int64_t)dim;
-    for (int64_t qi = (int64_t)wave * 4 + g; qi - g < T; qi += 16) {
-        const bool valid = qi < T;  // uniform over the lane group
-        const int64_t r = t0 + qi;
-        float q[HD];
-#pragma unroll
-        for (int d = 0; d < HD; ++d) q[d] = valid ? qkv[r * stride + h * HD + d] * scale : 0.0f;
-        float l = 0.0f, acc[HD], mx = -INFINITY;
-#pragma unroll
-        for (int d = 0; d < HD; ++d) acc[d] = 0.0f;
-        for (int64_t t = t0 + j; t < t1; t += 16) {
-            const float* kr = qkv + t * stride + dim + h * HD;
-            const float* vr = qkv + t * stride + 2 * dim + h * HD;
-            float sc = 0.0f;
-#pragma unroll
-            for (int d = 0; d < HD; ++d) sc = fmaf(q[d], kr[d], sc);
-            const float nm = fmaxf(mx, sc);
-            const float corr = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
-            const float p = __expf(sc - nm);
-            l = fmaf(l, corr, p);
-#pragma unroll
-            for (int d = 0; d < HD; ++d) acc[d] = fmaf(acc[d], corr, p * vr[d]);
-            mx = nm;
-        }
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) {
-            const float om = __shfl_xor(mx, off, 64);
-            const float ol = __shfl_xor(l, off, 64);
-            const float nm = fmaxf(mx, om);
-            const float ca = (mx == -INFINITY) ? 0.0f : __expf(mx - nm);
-            const float cb = (om == -INFINITY) ? 0.0f : __expf(om - nm);
-            l = l * ca + ol * cb;
-#pragma unroll
-            for (int d = 0; d < HD; ++d) {
-                const float oa = __shfl_xor(acc[d], off, 64);
-                acc[d] = acc[d] * ca + oa * cb;
-            }
-            mx = nm;
-        }
-        // lane j of the group writes dimension j
-        float mine = 0.0f;
-#pragma unroll
-        for (int d = 0; d < HD; ++d) mine = (j == d) ? acc[d] : mine;
-        if (valid && j < HD) o[r * dim + h * HD + j] = l > 0.0f ? __fdiv_rn(mine, l) : 0.0f;
-    }
+// max(a, b) as one v_max_f32 (fmaxf on values the compiler cannot prove canonical, MFMA
+// results and shuffles, costs a v_max_f32 x, x, x per operand first).  Operands here are
+// scores, never NaN unless the inputs are.
+__device__ __forceinline__ float max_f32(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 
 template <int HD>
@@ -289,110 +248,135 @@ __global__ __launch_bounds__(256) void neck_attn_kernel(const float* __restrict_
                                                         int64_t line_len, int dim, float scale,
                                                         float* __restrict__ o) {
     static_assert(HD <= 16, "one 16-wide MFMA tile holds a head's dims");
-    constexpr int NT = kAttnMfmaSteps / 16;  // key tiles at most
-    __shared__ __align__(16) float ks[kAttnMfmaSteps * 16];  // K [t][dim permuted]
-    __shared__ __align__(16) float qs[kAttnMfmaSteps * 16];  // Q * scale [t][dim permuted]
-    __shared__ __align__(16) float vt[16 * kVtStride];       // V^T [dim][t]
+    constexpr int KT = kAttnKeyTiles, QB = kAttnQBlocks;
+    __shared__ __align__(16) float ks[kAttnKeys * 16];  // K block [t][dim permuted]
+    __shared__ __align__(16) float vt[16 * kVtStride];  // V block transposed [dim][t]
     const int64_t line = blockIdx.x;
     const int h = blockIdx.y;
     const int64_t t0 = line_off ? min(max(line_off[line], (int64_t)0), m) : min(line * line_len, m);
     const int64_t t1 = line_off ? min(max(line_off[line + 1], t0), m) : min(t0 + line_len, m);
-    const int64_t T64 = t1 - t0;
-    if (T64 <= 0) return;
-    const int tid = threadIdx.x;
-    if (T64 > kAttnMfmaSteps) {
-        attn_stream<HD>(qkv, t0, t1, h, dim, scale, tid, o);
-        return;
-    }
-    const int T = (int)T64, nt = (T + 15) >> 4;
+    if (t1 - t0 <= 0) return;
+    const int T = (int)(t1 - t0);  // the launcher bounds m by INT32_MAX
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
     const int64_t stride = 3 * (int64_t)dim;
-    // stage 16 * nt rows (zeros past the line's end and past the head's dims): thread tid
-    // takes dim tid % 16 of rows tid / 16 + 16 x, every load issued before the first LDS
-    // store (a loop of load, wait, store would wait once per row group)
-    const int sd = tid & 15, st0 = tid >> 4;
-    float kv[NT], qv[NT], vv[NT];
+    const float* base = qkv + t0 * stride + h * HD;  // the line's first row, this head
+    const int sd = tid & 15, st0 = tid >> 4;  // staging: dim tid % 16 of rows tid / 16 + 16 x
+    for (int qpass = 0; qpass < T; qpass += 4 * 16 * QB) {
+        // this wave's query blocks: queries qpass + 16 (wave + 4 x) + c
+        f32x4 qf[QB], oa[QB], ob[QB];
+        float mx[QB], ls[QB];
 #pragma unroll
-    for (int x = 0; x < NT; ++x) {
-        const int t = st0 + 16 * x;
-        kv[x] = qv[x] = vv[x] = 0.0f;
-        if (x < nt && t < T && sd < HD) {
-            const float* row = qkv + (t0 + t) * stride + h * HD + sd;
-            qv[x] = row[0];  // scaled at the store: a use here would wait for the load
-            kv[x] = row[dim];
-            vv[x] = row[2 * dim];
+        for (int x = 0; x < QB; ++x) {
+            const int q = qpass + 16 * (wave + 4 * x) + c;
+            const float* row = base + (int64_t)q * stride;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int d = 4 * s + g;
+                qf[x][s] = (q < T && d < HD) ? row[d] : 0.0f;
+            }
+            oa[x] = ob[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mx[x] = -INFINITY;
+            ls[x] = 0.0f;
         }
-    }
 #pragma unroll
-    for (int x = 0; x < NT; ++x) {
-        if (x < nt) {
-            const int t = st0 + 16 * x;
-            ks[t * 16 + perm_dim(sd)] = kv[x];
-            qs[t * 16 + perm_dim(sd)] = qv[x] * scale;
-            vt[sd * kVtStride + t] = vv[x];
-        }
-    }
-    __syncthreads();
-    const int lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
-    for (int qb = wave; qb < nt; qb += 4) {
-        const int q0 = 16 * qb;
-        const f32x4 qf = *reinterpret_cast<const f32x4*>(qs + (q0 + c) * 16 + 4 * g);
-        f32x4 sc[NT];
+        for (int x = 0; x < QB; ++x) qf[x] = qf[x] * scale;  // the Mul(scale) node, rounded as it
+        for (int kb = 0; kb < T; kb += kAttnKeys) {
+            const int rem = T - kb;  // keys of the line from this block on
+            // stage keys kb .. kb + 127 (zeros past the line's end and past the head's dims),
+            // every load issued before the first LDS store
+            float kv[KT], vv[KT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
-                const f32x4 kf = *reinterpret_cast<const f32x4*>(ks + (16 * t + c) * 16 + 4 * g);
-                f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int x = 0; x < KT; ++x) {
+                const int t = st0 + 16 * x;
+                kv[x] = vv[x] = 0.0f;
+                if (t < rem && sd < HD) {
+                    const float* row = base + (int64_t)(kb + t) * stride + sd;
+                    kv[x] = row[dim];
+                    vv[x] = row[2 * dim];
+                }
+            }
+            __syncthreads();  // the previous block's readers are done
 #pragma unroll
-                for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[s], acc, 0, 0, 0);
-                sc[t] = acc;
+            for (int x = 0; x < KT; ++x) {
+                const int tl = st0 + 16 * x;
+                ks[tl * 16 + perm_dim(sd)] = kv[x];
+                vt[sd * kVtStride + tl] = vv[x];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int x = 0; x < QB; ++x) {
+                const int q0 = qpass + 16 * (wave + 4 * x);
+                if (q0 >= T) continue;  // uniform over the wave
+                // one query block at a time: interleaved, their scores would all be live
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 sc[KT];
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+                    const f32x4 kf = *reinterpret_cast<const f32x4*>(ks + (16 * t + c) * 16 + 4 * g);
+                    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[x][s], acc, 0, 0, 0);
+                    sc[t] = acc;
+                }
+                // keys past the line's end score -inf (their p is then exactly 0); the block's
+                // maximum for query q0 + c: this lane's keys, then the lane groups
+                float bm = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        sc[t][jj] = (16 * t + 4 * g + jj < rem) ? sc[t][jj] : -INFINITY;
+                        bm = max_f32(bm, sc[t][jj]);
+                    }
+                }
+                bm = max_f32(bm, __shfl_xor(bm, 16, 64));
+                bm = max_f32(bm, __shfl_xor(bm, 32, 64));
+                const float nm = max_f32(mx[x], bm);
+                if (kb > 0) {
+                    // rescale the sums so far (every block of a pass after the first follows one
+                    // that set a finite maximum)
+                    const float corr = __expf(mx[x] - nm);
+                    ls[x] *= corr;
+                    oa[x] = oa[x] * corr;
+                    ob[x] = ob[x] * corr;
+                }
+                mx[x] = nm;
+                float l = 0.0f;
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const float p = __expf(sc[t][jj] - nm);
+                        sc[t][jj] = p;
+                        l += p;
+                    }
+                }
+                ls[x] += l;
+                // O^T += V^T P^T, even and odd key tiles on two accumulators
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+                    const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + c * kVtStride + 16 * t + 4 * g);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        if (t & 1) ob[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[s], sc[t][s], ob[x], 0, 0, 0);
+                        else oa[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[s], sc[t][s], oa[x], 0, 0, 0);
+                    }
+                }
             }
         }
-        // the maximum over the line's keys of query q0 + c: this lane's keys, then the four
-        // lane groups
-        float mx = -INFINITY;
+        // per query: the sums of the four lane groups; lane l writes query q0 + c, dims 4 g + j
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
+        for (int x = 0; x < QB; ++x) {
+            const int q = qpass + 16 * (wave + 4 * x) + c;
+            float l = ls[x];
+            l += __shfl_xor(l, 16, 64);
+            l += __shfl_xor(l, 32, 64);
+            if (q < T) {
+                float* orow = o + (t0 + q) * (int64_t)dim + h * HD;
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
-                    if (16 * t + 4 * g + jj < T) mx = fmaxf(mx, sc[t][jj]);
+                    if (4 * g + jj < HD) orow[4 * g + jj] = __fdiv_rn(oa[x][jj] + ob[x][jj], l);
             }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        float l = 0.0f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const float p = (16 * t + 4 * g + jj < T) ? __expf(sc[t][jj] - mx) : 0.0f;
-                    sc[t][jj] = p;
-                    l += p;
-                }
-            }
-        }
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
-        // O^T = V^T P^T, even and odd key tiles on two accumulators
-        f32x4 oa = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, ob = oa;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
-                const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + c * kVtStride + 16 * t + 4 * g);
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    if (t & 1) ob = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[s], sc[t][s], ob, 0, 0, 0);
-                    else oa = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[s], sc[t][s], oa, 0, 0, 0);
-                }
-            }
-        }
-        // lane l: query q0 + c, dims 4 g + j
-        if (q0 + c < T) {
-            float* orow = o + (t0 + q0 + c) * dim + h * HD;
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-                if (4 * g + jj < HD) orow[4 * g + jj] = __fdiv_rn(oa[jj] + ob[jj], l);
         }
     }
 }
