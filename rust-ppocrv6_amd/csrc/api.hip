@@ -553,7 +553,7 @@ int mode_cfg(const ppocr_rh* h, int mode, int* cfg) {
 
 int fma_nsplit(int64_t m, int64_t n) {
     const int64_t mblocks = (m + kFmaRowsPerBlock - 1) / kFmaRowsPerBlock;
-    const int64_t ntiles = (n + 63) / 64;
+    const int64_t ntiles = (n + kFmaCols - 1) / kFmaCols;
     int64_t ns = (1024 + mblocks - 1) / std::max<int64_t>(mblocks, 1);
     ns = std::min<int64_t>(std::max<int64_t>(ns, 1), std::min<int64_t>(ntiles, 1024));
     return (int)ns;

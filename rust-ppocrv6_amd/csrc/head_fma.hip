@@ -2,8 +2,9 @@
 // Same contraction as compute_quantized_b_cols_avx2 (src/ops/matmul.rs:1338-1443) and
 // transposed_b_tile_fma (src/ops/matmul.rs:1025-1087): fp32 products of the activation
 // and the (exactly dequantised) weight, fp32 accumulation, then (sum * scale) + bias.
-// Register tile: every thread owns 8 rows x 4 classes of a 128 x 64 block; k is staged
-// through LDS in chunks of 40.
+// Register tile: every thread owns 8 rows x 8 classes of a 128 x 128 block (classes
+// 4 tn .. + 3 and 64 + 4 tn .. + 3, so each k step is four 16-byte LDS reads for 64 FMAs); k
+// is staged through LDS in chunks of 32.
 #include <algorithm>
 
 #include "kernels.hpp"
@@ -11,10 +12,11 @@
 namespace ppocr {
 
 namespace {
-constexpr int BM = 128, BN = 64, KC = 40;
+constexpr int BM = kFmaRowsPerBlock, BN = kFmaCols, KC = 32;
 constexpr int64_t kFmaRescueSlots = 128;  // row-block slots of a gather-mode (rescue) launch
 constexpr int AST = BM + 4;  // LDS row strides (floats); +4 keeps 16-byte alignment
-constexpr int WST = BN + 1;
+constexpr int WST = BN + 4;
+static_assert(BM == 128 && BN == 128 && KC == 32, "the thread mappings below");
 
 
 // Rows of a block: contiguous rows m0 .. m0 + BM - 1, or (GATHER) entries of the precision
@@ -42,8 +44,9 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
     float* __restrict__ p_best, float* __restrict__ p_sum, int* __restrict__ p_idx, int64_t line_len,
     const unsigned long long* __restrict__ guard_header, const int* __restrict__ guard_rows, unsigned guard_epoch,
     int guard_cap) {
-    __shared__ __align__(16) float As[KC * AST];
-    __shared__ float Ws[KC * WST];
+    __shared__ __align__(16) float As[KC * AST];  // [k][row]
+    __shared__ __align__(16) float Ws[KC * WST];  // [k][class]
+    __shared__ int64_t s_row[BM];                 // the block's rows (-1: none), read by the staging
 
     const int tid = threadIdx.x, tm = tid >> 4, tn = tid & 15;
     const int chunk = blockIdx.x;
@@ -56,6 +59,9 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
         src = FmaRows{guard_rows, c < (unsigned)guard_cap ? (int)c : guard_cap};
     }
     const int64_t nrows = GATHER ? (int64_t)src.count : m;
+    // class j of this thread within a tile: 4 tn + j (j < 4), 64 + 4 tn + j - 4 (j >= 4), in
+    // increasing class order
+    auto cls = [&](int j) { return (j < 4 ? 0 : 64 - 4) + 4 * tn + j; };
 
     for (int64_t m0 = (int64_t)blockIdx.y * BM; m0 < nrows; m0 += (int64_t)gridDim.y * BM) {
         // this thread's 8 rows (local slots 8 * tm .. 8 * tm + 7 of the block)
@@ -63,6 +69,12 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
         bool rvalid[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) rows[r] = src.row(m0 + 8 * tm + r, m, rvalid[r]);
+        __syncthreads();  // the previous block's staging is done with the table
+        if (tid < BM) {
+            bool v;
+            const int64_t r = src.row(m0 + tid, m, v);
+            s_row[tid] = v ? r : -1;
+        }
 
         RowStat st[8];
 #pragma unroll
@@ -78,38 +90,51 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
         }
 
         for (int n0 = c0; n0 < c1; n0 += BN) {
-            float acc[8][4];
+            float acc[8][8];
 #pragma unroll
             for (int r = 0; r < 8; ++r)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[r][j] = 0.0f;
+                for (int j = 0; j < 8; ++j) acc[r][j] = 0.0f;
+            // this thread's eight columns' constants, loaded once per tile of classes
+            float csc[8], cbi[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int col = n0 + cls(j);
+                csc[j] = col < c1 ? scale[col] : 0.0f;
+                cbi[j] = col < c1 ? bias[col] : 0.0f;
+            }
 
             for (int k0 = 0; k0 < k; k0 += KC) {
-                __syncthreads();
-                if (line_len > 0) {
-                    // channels-first [lines][k][line_len]: neighbouring threads take neighbouring steps
-                    for (int idx = tid; idx < BM * KC; idx += 256) {
-                        const int mm = idx % BM, kk = idx / BM;
-                        bool v;
-                        const int64_t row = src.row(m0 + mm, m, v), line = row / line_len;
-                        As[kk * AST + mm] = (v && k0 + kk < k)
-                                                ? a[(line * k + k0 + kk) * line_len + (row - line * line_len)]
-                                                : 0.0f;
-                    }
-                } else {
-                    for (int idx = tid; idx < BM * KC; idx += 256) {
-                        const int mm = idx / KC, kk = idx % KC;
-                        bool v;
-                        const int64_t row = src.row(m0 + mm, m, v);
-                        As[kk * AST + mm] = (v && k0 + kk < k) ? a[row * k + k0 + kk] : 0.0f;
-                    }
-                }
-                for (int idx = tid; idx < BN * KC; idx += 256) {
-                    const int nn = idx / KC, kk = idx % KC;
-                    const int col = n0 + nn;
+                // stage the chunk.  Rows layout: thread tid takes k0 + tid % 32 of rows
+                // tid / 32 + 8 it (classes likewise); channels-first [lines][k][line_len]:
+                // neighbouring threads take neighbouring steps (row tid % 128 at k0 + tid / 128
+                // + 2 it).  Past the rows, classes or k: zeros.
+                constexpr int IT = BM * KC / 256;
+                __syncthreads();  // the previous chunk's readers are done
+#pragma unroll 4
+                for (int it = 0; it < IT; ++it) {
+                    const int mm = line_len > 0 ? (tid & (BM - 1)) : (tid >> 5) + 8 * it;
+                    const int kk = line_len > 0 ? (tid >> 7) + 2 * it : (tid & 31);
+                    const int64_t row = s_row[mm];
                     float v = 0.0f;
-                    if (col < c1 && k0 + kk < k)
-                        v = q ? (float)q[(int64_t)col * k + k0 + kk] : w[(int64_t)col * k + k0 + kk];
+                    if (row >= 0 && k0 + kk < k) {
+                        if (line_len > 0) {
+                            const int64_t line = row / line_len;
+                            v = a[(line * k + k0 + kk) * line_len + (row - line * line_len)];
+                        } else {
+                            v = a[row * k + k0 + kk];
+                        }
+                    }
+                    As[kk * AST + mm] = v;
+                }
+#pragma unroll 4
+                for (int it = 0; it < IT; ++it) {
+                    const int nn = (tid >> 5) + 8 * it, kk = tid & 31;
+                    float v = 0.0f;
+                    if (n0 + nn < c1 && k0 + kk < k) {
+                        const int64_t e = (int64_t)(n0 + nn) * k + k0 + kk;
+                        v = q ? (float)q[e] : w[e];
+                    }
                     Ws[kk * WST + nn] = v;
                 }
                 __syncthreads();
@@ -117,15 +142,16 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
                 for (int kk = 0; kk < kend; ++kk) {
                     const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm]);
                     const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[kk * AST + 8 * tm + 4]);
-                    float wv[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) wv[j] = Ws[kk * WST + tn + 16 * j];
+                    const f32x4 w0 = *reinterpret_cast<const f32x4*>(&Ws[kk * WST + 4 * tn]);
+                    const f32x4 w1 = *reinterpret_cast<const f32x4*>(&Ws[kk * WST + 64 + 4 * tn]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            acc[r][j] = fmaf(a0[r], wv[j], acc[r][j]);
-                            acc[r + 4][j] = fmaf(a1[r], wv[j], acc[r + 4][j]);
+                            acc[r][j] = fmaf(a0[r], w0[j], acc[r][j]);
+                            acc[r + 4][j] = fmaf(a1[r], w0[j], acc[r + 4][j]);
+                            acc[r][j + 4] = fmaf(a0[r], w1[j], acc[r][j + 4]);
+                            acc[r + 4][j + 4] = fmaf(a1[r], w1[j], acc[r + 4][j + 4]);
                         }
                     }
                 }
@@ -134,20 +160,20 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
             if (EPI == EPI_STATS) {
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
-                    float tv[4];
+                    float tv[8];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int col = n0 + tn + 16 * j;
-                        tv[j] = col < c1 ? fmaf(acc[r][j], scale[col] * kLog2e, bias[col] * kLog2e) : -INFINITY;
-                    }
-                    float tmax = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
+                    for (int j = 0; j < 8; ++j)
+                        tv[j] = n0 + cls(j) < c1 ? fmaf(acc[r][j], csc[j] * kLog2e, cbi[j] * kLog2e) : -INFINITY;
+                    const float tmax = fmaxf(fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3])),
+                                             fmaxf(fmaxf(tv[4], tv[5]), fmaxf(tv[6], tv[7])));
                     const bool better = tmax > st[r].best;
                     if (better) {
-                        int jj = 3;
+                        // the first of this thread's columns (in class order) holding the maximum
+                        int jj = 7;
 #pragma unroll
-                        for (int j = 2; j >= 0; --j) jj = (tv[j] == tmax) ? j : jj;
+                        for (int j = 6; j >= 0; --j) jj = (tv[j] == tmax) ? j : jj;
                         st[r].best = tmax;
-                        st[r].idx = n0 + tn + 16 * jj;
+                        st[r].idx = n0 + cls(jj);
                     }
                     const bool shift = st[r].best != -INFINITY &&
                                        (st[r].best > st[r].ref + 64.0f || st[r].best < st[r].ref - 64.0f);
@@ -161,31 +187,40 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
                     }
                     float e = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) e += __builtin_amdgcn_exp2f(refzero ? tv[j] : tv[j] - st[r].ref);
+                    for (int j = 0; j < 8; ++j) e += __builtin_amdgcn_exp2f(refzero ? tv[j] : tv[j] - st[r].ref);
                     st[r].sum += e;
                 }
             } else {
+                auto value = [&](int r, int j) {
+                    if (EPI == EPI_LOGITS) return __fadd_rn(__fmul_rn(acc[r][j], csc[j]), cbi[j]);
+                    return __builtin_amdgcn_exp2f(fmaf(acc[r][j], csc[j] * kLog2e, cbi[j] * kLog2e) - rmax[r]) *
+                           rinv[r];
+                };
+                bool all = n0 + BN <= c1;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int col = n0 + tn + 16 * j;
-                    if (col >= c1) continue;
-                    const float sc = scale[col], bi = bias[col];
+                for (int r = 0; r < 8; ++r) all = all && rvalid[r];
+                if (all) {
+                    // no branch per value: at a branch the compiler waits for every store in
+                    // flight
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) out[rows[r] * n + n0 + cls(j)] = value(r, j);
+                } else {
 #pragma unroll
                     for (int r = 0; r < 8; ++r) {
                         if (!rvalid[r]) continue;
-                        float v;
-                        if (EPI == EPI_LOGITS)
-                            v = __fadd_rn(__fmul_rn(acc[r][j], sc), bi);
-                        else
-                            v = __builtin_amdgcn_exp2f(fmaf(acc[r][j], sc * kLog2e, bi * kLog2e) - rmax[r]) * rinv[r];
-                        out[rows[r] * n + col] = v;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (n0 + cls(j) < c1) out[rows[r] * n + n0 + cls(j)] = value(r, j);
                     }
                 }
             }
         }
 
         if (EPI == EPI_STATS) {
-            // the 16 threads of one tm are 16 consecutive lanes: butterfly over them.
+            // the 16 threads of one tm are 16 consecutive lanes: butterfly over them (ties keep
+            // the lower class).
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 RowStat s = st[r];

@@ -172,7 +172,7 @@ enum Epi : int { EPI_LOGITS = 0, EPI_PROBS = 1, EPI_STATS = 2 };
 // fp32 vector FMA path over the packed int8 weights (q != null) or fp32 weights (w != null).
 int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                       const float* a, int64_t m, int64_t n, int64_t k, float* out, hipStream_t st);
-constexpr int kFmaRowsPerBlock = 128;
+constexpr int kFmaRowsPerBlock = 128, kFmaCols = 128;  // rows and classes of a workgroup's tile
 int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                      const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
                      float* p_sum, int* p_idx, hipStream_t st, int64_t line_len = 0);
