@@ -561,7 +561,7 @@ int fma_nsplit(int64_t m, int64_t n) {
 
 int nsplit_for(const ppocr_rh* h, int64_t m, int cfg) {
     if (cfg < 0) return fma_nsplit(m, h->n);
-    return stats_nsplit(m, stats_rows_per_block_mfma(cfg, m), h->geom.tiles);
+    return stats_nsplit(m, stats_rows_per_block_mfma(cfg, m), h->geom.tiles, stats_per_cu_mfma(cfg, m));
 }
 
 constexpr size_t kAlign = 256;

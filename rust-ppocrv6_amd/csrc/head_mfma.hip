@@ -40,22 +40,28 @@ static int main_blocks(int cfg, int64_t m) {
 // pass (4 waves).
 int stats_rows_per_block_mfma(int cfg, int64_t m) { return 32 * kStatsWaves * main_blocks(cfg, m); }
 
-// Vocabulary chunks per row block.  The grid runs in rounds of kStatsSlots workgroups
-// (2 per CU on the 256 CUs of an MI355X), and a workgroup costs a fixed start and finish
-// (its rows' activations, the pipeline fill, the partials) worth about kChunkFixedTiles
-// tiles of the main loop (measured on the MI355X: 30720 rows run 5% faster in 4 chunks of
-// 147 tiles, one round, than in 8 chunks of 74, two rounds).  The chunk count from 4 to
-// 64 minimising rounds x (fixed + tiles per chunk) is taken.  At least 4 chunks keep each
-// XCD's slice of the weight records (the chunks of workgroup id mod 8) within its L2.
-constexpr int64_t kStatsSlots = 256 * 8 / kStatsWaves;
-constexpr int64_t kChunkFixedTiles = 8;
-int stats_nsplit(int64_t m, int rows_per_block, int tiles) {
+// Vocabulary chunks per row block.  The grid runs in rounds of `slots` workgroups (those
+// that fit on the 256 CUs of an MI355X at once), and a workgroup costs a fixed start and
+// finish (its rows' activations, the pipeline fill, the partials) worth about `fixed`
+// tiles of the main loop.  The chunk count from 4 to 64 minimising rounds x (fixed + tiles
+// per chunk) is taken.  At least 4 chunks keep each XCD's slice of the weight records (the
+// chunks of workgroup id mod 8) within its L2.  Most kernels run 2 workgroups per CU with
+// a fixed cost of 8 tiles (measured: 30720 rows run 5% faster in 4 chunks of 147 tiles,
+// one round, than in 8 chunks of 74, two rounds).  The two-term modes' one-block-per-wave
+// kernel (small batches: 128-row workgroups, 51 KB of LDS, 148 VGPRs) runs 3 per CU, fixed
+// 10 tiles (measured against 2 per CU and 8 tiles: 2280 rows 43.8 -> 40.5 us per step in 32
+// chunks instead of 16, 4800 rows 63.5 -> 61.6 in 16 instead of 8; 8160 rows keep 8
+// chunks, which the 8-tile estimate would have traded for 32 in three rounds, 84 -> 95 us).
+int stats_per_cu_mfma(int cfg, int64_t m) { return main_blocks(cfg, m) == 1 && (cfg == CFG_Q2 || cfg == CFG_H2) ? 3 : 2; }
+int stats_nsplit(int64_t m, int rows_per_block, int tiles, int per_cu) {
     const int64_t mblocks = (m + rows_per_block - 1) / rows_per_block;
+    const int64_t slots = 256 * (int64_t)per_cu;
+    const int64_t fixed = per_cu == 3 ? 10 : 8;
     int best = 4;
     int64_t best_cost = -1;
     for (int ns = 4; ns <= 64; ns *= 2) {
-        const int64_t rounds = (mblocks * ns + kStatsSlots - 1) / kStatsSlots;
-        const int64_t cost = rounds * (kChunkFixedTiles + (tiles + ns - 1) / ns);
+        const int64_t rounds = (mblocks * ns + slots - 1) / slots;
+        const int64_t cost = rounds * (fixed + (tiles + ns - 1) / ns);
         if (best_cost < 0 || cost < best_cost) {
             best = ns;
             best_cost = cost;

@@ -138,7 +138,8 @@ int launch_guard_clear(unsigned long long* guard_header, hipStream_t st);
 int launch_logits_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a,
                        int64_t m, int64_t n, int64_t k, float* out, const Guard* guard, hipStream_t st);
 // Fused projection + online softmax statistics: per (row, vocabulary chunk) partials.
-int stats_nsplit(int64_t m, int rows_per_block, int tiles);
+int stats_per_cu_mfma(int cfg, int64_t m);  // workgroups of the main statistics pass per CU
+int stats_nsplit(int64_t m, int rows_per_block, int tiles, int per_cu);
 int stats_rows_per_block_mfma(int cfg, int64_t m);
 // Main pass, rescue of the guarded rows, then one wave per row merges the partials and
 // resolves the argmax: idx, maxprob (1/sum) and, when non-null, row_max (log2-domain
