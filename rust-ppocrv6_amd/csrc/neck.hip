@@ -469,20 +469,30 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         neck_cf_rows_kernel<<<grid, 256, 0, st>>>(shortcut_in, m, D, line_off, lines, line_len, sc);
         PPOCR_HIP(hipGetLastError());
         scr = sc;
-    } else {
-        PPOCR_HIP(hipMemcpyAsync(x, x_in, (size_t)m * D * 4, hipMemcpyDeviceToDevice, st));
+    }
+    // the residual stream: the first block reads it from the input rows (row layout; the
+    // GEMMs load rows 16 bytes at a time, so an input that is not 16-byte aligned is copied
+    // into the workspace first) and writes it to the workspace with its first residual Add;
+    // later blocks work in place
+    const float* xin = x;
+    if (layout == PPOCR_NECK_ROWS) {
+        if (reinterpret_cast<uintptr_t>(x_in) & 15)
+            PPOCR_HIP(hipMemcpyAsync(x, x_in, (size_t)m * D * 4, hipMemcpyDeviceToDevice, st));
+        else
+            xin = x_in;
     }
     for (int b = 0; b < nk.blocks; ++b) {
         const NeckBlockDev& k = nk.block[b];
+        const float* xr = b == 0 ? xin : x;
         // LN1 -> qkv
-        if (int e = gemm_go<kNeckDim, true, false, false>(x, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b, k.ln1_eps,
+        if (int e = gemm_go<kNeckDim, true, false, false>(xr, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b, k.ln1_eps,
                                                           nullptr, qkv, st))
             return e;
         const dim3 ag((unsigned)lines, (unsigned)nk.heads);
         neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
         PPOCR_HIP(hipGetLastError());
         // x = x + proj(att)
-        if (int e = gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr, 0.0f, x, x,
+        if (int e = gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr, 0.0f, xr, x,
                                                           st))
             return e;
         // LN2 -> fc1 -> swish
