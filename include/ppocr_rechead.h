@@ -311,6 +311,11 @@ int ppocr_rn_create_from_model(const char* path, int device, ppocr_rn_t** out);
 void ppocr_rn_destroy(ppocr_rn_t* h);
 /* dim, heads, hidden and the number of blocks. */
 int ppocr_rn_shape(const ppocr_rn_t* h, int64_t* dim, int64_t* heads, int64_t* hidden, int* blocks);
+/* No counterpart in the reference: the arithmetic of the tail's MatMuls, 1 when they run on
+ * fp16 halves of both operands (three exact products summed in fp32, 22 bits of each
+ * operand; chosen at creation when the weights bound every MatMul operand inside fp16's
+ * range), 0 when on fp32 products; a negative status for a null handle. */
+int ppocr_rn_gemm_halves(const ppocr_rn_t* h);
 /* Device workspace of ppocr_rn_forward_dev for m token rows. */
 size_t ppocr_rn_workspace_bytes(const ppocr_rn_t* h, int64_t m);
 /* out [m][dim] token rows = the tail applied to x and shortcut (both in `layout`), lines

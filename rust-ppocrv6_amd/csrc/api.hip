@@ -1238,6 +1238,58 @@ struct NeckHost {
     const float *lnf_w = nullptr, *lnf_b = nullptr;
 };
 
+// fp16 planes of W^T for the tail's fp16-halves GEMMs: [2][N][kp], the nearest half of each
+// weight, then the nearest half of what it leaves, k padded with zeros.
+std::vector<uint16_t> neck_half_planes(const float* w, int64_t K, int64_t N) {
+    const int64_t kp = neck_f16_kp((int)K);
+    std::vector<uint16_t> out((size_t)(2 * N * kp), 0);
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t c = 0; c < N; ++c) {
+            const float x = w[k * N + c];
+            const _Float16 hi = (_Float16)x;
+            const _Float16 lo = (_Float16)(x - (float)hi);
+            out[(size_t)(c * kp + k)] = __builtin_bit_cast(uint16_t, hi);
+            out[(size_t)((N + c) * kp + k)] = __builtin_bit_cast(uint16_t, lo);
+        }
+    return out;
+}
+
+// Whether the weights keep every operand of the tail's GEMMs inside fp16's range, with room:
+// each operand is a LayerNorm output (|z_k| <= sqrt(D - 1) for the normalised row, so
+// |y_k| <= sqrt(D - 1) |w_k| + |b_k|), the attention's output (a convex combination of the
+// value rows, so no larger than them) or the swish of fc1's output (|x sigmoid(x)| <= |x|);
+// a product's bound is max_c sum_k |W[k][c]| times its input's bound plus max |bias|.
+bool neck_f16_bounds_ok(const NeckHost& nh) {
+    const int64_t D = nh.dim, H = nh.hidden;
+    constexpr double kLimit = 16384.0;  // a quarter of fp16's largest finite value
+    auto amax = [](const float* v, int64_t n) {
+        double r = 0.0;
+        for (int64_t i = 0; i < n; ++i) r = std::max(r, (double)std::fabs(v[i]));
+        return r;
+    };
+    // max over columns c0 .. c0 + nc - 1 of sum_k |W[k][c]| (W [K][N])
+    auto col_l1 = [](const float* w, int64_t K, int64_t N, int64_t c0, int64_t nc) {
+        double r = 0.0;
+        for (int64_t c = c0; c < c0 + nc; ++c) {
+            double s = 0.0;
+            for (int64_t k = 0; k < K; ++k) s += std::fabs(w[k * N + c]);
+            r = std::max(r, s);
+        }
+        return r;
+    };
+    const double zmax = std::sqrt((double)(D - 1)) * 1.001;
+    for (const ppocr_rn_block_t& b : nh.blocks) {
+        const double y1 = zmax * amax(b.ln1_w, D) + amax(b.ln1_b, D);  // qkv's input
+        const double y2 = zmax * amax(b.ln2_w, D) + amax(b.ln2_b, D);  // fc1's input
+        const double v = y1 * col_l1(b.qkv_w, D, 3 * D, 2 * D, D) + amax(b.qkv_b + 2 * D, D);  // proj's input
+        const double hs = y2 * col_l1(b.fc1_w, D, H, 0, H) + amax(b.fc1_b, H);               // fc2's input
+        const double wmax = std::max(std::max(amax(b.qkv_w, D * 3 * D), amax(b.proj_w, D * D)),
+                                     std::max(amax(b.fc1_w, D * H), amax(b.fc2_w, H * D)));
+        if (!(y1 <= kLimit && y2 <= kLimit && v <= kLimit && hs <= kLimit && wmax <= kLimit)) return false;
+    }
+    return true;
+}
+
 int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
     const char* op = "RecNeckHip";
     if (!out) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null output handle");
@@ -1266,6 +1318,19 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
     }
     parts.push_back({nh.lnf_w, D});
     parts.push_back({nh.lnf_b, D});
+    // the fp16 planes of each block's four weights, as float-sized parts after the rest
+    const bool f16 = neck_f16_bounds_ok(nh);
+    std::vector<std::vector<uint16_t>> planes;
+    if (f16) {
+        for (const ppocr_rn_block_t& b : nh.blocks) {
+            planes.push_back(neck_half_planes(b.qkv_w, D, 3 * D));
+            planes.push_back(neck_half_planes(b.proj_w, D, D));
+            planes.push_back(neck_half_planes(b.fc1_w, D, H));
+            planes.push_back(neck_half_planes(b.fc2_w, H, D));
+        }
+        for (const auto& pl : planes)
+            parts.push_back({reinterpret_cast<const float*>(pl.data()), (int64_t)(pl.size() / 2)});
+    }
     int64_t total = 0;
     for (const auto& pt : parts) total += (pt.second + 3) / 4 * 4;  // each part 16-byte aligned
     if (device < 0) return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": negative device");
@@ -1317,6 +1382,14 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
     nd.lnf_w = dev_ptr[q++];
     nd.lnf_b = dev_ptr[q++];
     nd.lnf_eps = nh.lnf_eps;
+    nd.f16 = f16;
+    for (size_t i = 0; f16 && i < nh.blocks.size(); ++i) {
+        NeckBlockDev& b = nd.block[i];
+        b.qkv_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
+        b.proj_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
+        b.fc1_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
+        b.fc2_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
+    }
     *out = h.release();
     return PPOCR_OK;
 }
@@ -1409,6 +1482,11 @@ int ppocr_rn_shape(const ppocr_rn_t* h, int64_t* dim, int64_t* heads, int64_t* h
     if (hidden) *hidden = h->dev.hidden;
     if (blocks) *blocks = h->dev.blocks;
     return PPOCR_OK;
+}
+
+int ppocr_rn_gemm_halves(const ppocr_rn_t* h) {
+    if (int e = check_neck(h)) return e;
+    return h->dev.f16 ? 1 : 0;
 }
 
 size_t ppocr_rn_workspace_bytes(const ppocr_rn_t* h, int64_t m) {

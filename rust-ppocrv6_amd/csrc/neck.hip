@@ -56,24 +56,91 @@ __device__ __forceinline__ int64_t line_of_row(const int64_t* line_off, int64_t 
 
 // ---------------------------------------------------------------- GEMM
 // out[r][n] = EPI(LN?(a[r])[.] . W[.][n] + bias[n]) (+ res[r][n]), W row-major [K][N] as the
-// model stores a MatMul weight.  A workgroup owns 128 rows x 128 columns; each wave 32 rows x
-// 4 tiles of 32 columns, interleaved (tile t holds columns n0 + 4 i + t).  The contraction index is split in halves: lanes 0-31 take
-// k = s, lanes 32-63 take k = K/2 + s at MFMA step s, so each lane holds one contiguous half
-// of its row in registers (and can normalise it: the row's two halves meet in one xor-32
-// shuffle).  The workgroup's W columns are staged once in LDS.
+// model stores a MatMul weight.  A workgroup owns 128 rows x 128 columns, staged once in
+// LDS; it has 4 row groups of 32 rows times 4 / TPW column groups, a wave each, and a wave
+// owns TPW tiles of 32 columns, interleaved (tile t holds the group's columns TPW i + t, so
+// a lane's TPW B operands of an MFMA step are one LDS read).  With TPW = 2 a workgroup has 8
+// waves: two per SIMD, so one wave's loads and stores overlap another's MFMAs.  The
+// contraction index is split in halves: lanes 0-31 take k = s, lanes 32-63 take
+// k = K/2 + s at MFMA step s, so each lane holds one contiguous half of its row in
+// registers (and can normalise it: the row's two halves meet in one xor-32 shuffle).
 constexpr int kGemmRows = 128, kGemmCols = 128;
 
-template <int K, bool LN, bool SWISH, bool RES>
-__global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict__ a, int64_t m,
-                                                        const float* __restrict__ w, int n,
-                                                        const float* __restrict__ bias,
-                                                        const float* __restrict__ ln_w,
-                                                        const float* __restrict__ ln_b, float eps,
-                                                        const float* res, float* out) {
-    constexpr int KH = K / 2;
+template <int N>
+struct FVec;
+template <>
+struct FVec<2> {
+    typedef float type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct FVec<4> {
+    typedef float type __attribute__((ext_vector_type(4)));
+};
+
+// Epilogue of the tail's GEMMs: lane (i, half) holds columns col .. col + TPW - 1 (tile t:
+// col + t) of rows rbase + 8(r/4) + 4 half + r%4; the columns are one chunk wholly inside or
+// outside [0, n).  Bias, then the swish (fc1) or the residual Add (proj, fc2).  The residual
+// Add reads the rows it overwrites (res == out in place), so every residual is loaded
+// before the first store: with the stores in between, each load would wait for the one
+// before it.
+template <bool SWISH, bool RES, int TPW>
+__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TPW], int64_t rbase, int half, int col, int64_t m,
+                                              int n, const float* __restrict__ bias, const float* res, float* out) {
+    using VT = typename FVec<TPW>::type;
+    if (col >= n) return;
+    const VT bc = *reinterpret_cast<const VT*>(bias + col);
+    VT rv[16];
+    if constexpr (RES) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+            rv[r] = rr < m ? *reinterpret_cast<const VT*>(res + rr * n + col) : VT{};
+        }
+    }
+    auto value = [&](int r) {
+        VT v;
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            float x = acc[t][r] + bc[t];
+            if constexpr (SWISH) x = swish_of(x);
+            if constexpr (RES) x = rv[r][t] + x;
+            v[t] = x;
+        }
+        return v;
+    };
+    // a block wholly inside the batch stores without a branch per row: at a branch the
+    // compiler waits for every access in flight (stores included), once per row
+    if (rbase + 32 <= m) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+            *reinterpret_cast<VT*>(out + rr * n + col) = value(r);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (rr < m) *reinterpret_cast<VT*>(out + rr * n + col) = value(r);
+        }
+    }
+}
+
+template <int TPW>
+constexpr int gemm_threads() {
+    return 64 * 4 * (4 / TPW);
+}
+
+template <int K, bool LN, bool SWISH, bool RES, int TPW>
+__global__ __launch_bounds__(gemm_threads<TPW>()) void neck_gemm_kernel(
+    const float* __restrict__ a, int64_t m, const float* __restrict__ w, int n, const float* __restrict__ bias,
+    const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps, const float* res, float* out) {
+    static_assert(TPW == 2 || TPW == 4, "tiles per wave");
+    using VT = typename FVec<TPW>::type;
+    constexpr int KH = K / 2, NW = gemm_threads<TPW>() / 64, GC = 32 * TPW;  // waves, a group's columns
     static_assert(K % 8 == 0, "rows are loaded 4 floats at a time per half");
     extern __shared__ __align__(16) float wl[];  // [K][kGemmCols], then (LN) [2][K]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, half = lane >> 5;
+    const int rg = wave & 3, cg = wave >> 2;  // row group, column group
     const int n0 = blockIdx.y * kGemmCols;
     // stage W[:, n0 .. n0 + 128) straight from global memory into LDS, all loads in flight
     // at once: one instruction of a wave fills two rows of the stage (64 lanes x 16 bytes),
@@ -82,7 +149,7 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
     // reloads the row's first chunk instead (it lands in columns whose results are never
     // stored, and each output column depends only on its own W column).
     static_assert(K % 2 == 0, "two stage rows per instruction");
-    for (int x = wave; x < K / 2; x += 4) {
+    for (int x = wave; x < K / 2; x += NW) {
         const int kk = 2 * x + (lane >> 5), c4 = n0 + 4 * (lane & 31);
         const float* src = w + (size_t)kk * n + (c4 < n ? c4 : 0);
         __builtin_amdgcn_global_load_lds(
@@ -105,7 +172,7 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
         }
     }
     // this lane's half row
-    const int64_t row = (int64_t)blockIdx.x * kGemmRows + wave * 32 + i;
+    const int64_t row = (int64_t)blockIdx.x * kGemmRows + rg * 32 + i;
     float av[KH];
     if (row < m) {
         const f32x4* src = reinterpret_cast<const f32x4*>(a + row * K + half * KH);
@@ -145,68 +212,170 @@ __global__ __launch_bounds__(256) void neck_gemm_kernel(const float* __restrict_
         for (int x = 0; x < KH; ++x) av[x] = fmaf((av[x] - mean) * inv, lnl[half * KH + x], lnl[K + half * KH + x]);
     }
 
-    // MFMA column i of tile t is W column n0 + 4 i + t: a lane's four B operands of a step are
-    // one 16-byte LDS read, issued kWPrefetch steps ahead of its MFMAs
+    // MFMA column i of tile t is W column n0 + GC cg + TPW i + t: a lane's B operands of a
+    // step are one LDS read, issued kWPrefetch steps ahead of its MFMAs
     constexpr int kWPrefetch = 4;
+    f32x16 acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) acc[t] = f32x16{};
+    const float* wbase = wl + half * KH * kGemmCols + GC * cg + TPW * i;
+    VT wq[kWPrefetch];
+#pragma unroll
+    for (int p = 0; p < kWPrefetch; ++p) wq[p] = *reinterpret_cast<const VT*>(wbase + p * kGemmCols);
+#pragma unroll
+    for (int st = 0; st < KH; ++st) {
+        const VT cur = wq[st % kWPrefetch];
+        if (st + kWPrefetch < KH) wq[st % kWPrefetch] = *reinterpret_cast<const VT*>(wbase + (st + kWPrefetch) * kGemmCols);
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[st], cur[t], acc[t], 0, 0, 0);
+    }
+
+    gemm_epilogue<SWISH, RES, TPW>(acc, (int64_t)blockIdx.x * kGemmRows + rg * 32, half, n0 + GC * cg + TPW * i, m,
+                                   n, bias, res, out);
+}
+
+// ---------------------------------------------------------------- GEMM, fp16 halves
+// The same products with both operands split into fp16 halves, x = x_hi + x_lo (x_hi the
+// nearest half, x_lo the nearest half of what it leaves: 22 bits of x), as three products
+// a_hi w_hi + a_hi w_lo + a_lo w_hi on v_mfma_f32_32x32x16_f16 (exact products, fp32 sums);
+// the dropped a_lo w_lo is below 2^-22 of each product.  Used when the weights bound every
+// operand inside fp16's range (neck creation checks it).  The weights come as fp16 planes of
+// W^T, [2][N][KP] (hi, then lo; k padded with zeros to KP); a workgroup stages its 128
+// columns of both planes in LDS, the 16-byte chunk q of column c at slot q ^ ((c / 4) % 8),
+// so that the lanes reading chunk q of columns 4 i + t (i = 0..7) hit 8 different bank
+// groups.  Lane (i, h) holds k = 16 s + 8 h + e (e < 8) of its row at MFMA step s, for the
+// activation (A, row i) and the weights (B, column i) alike; the row's LayerNorm meets its
+// two halves in xor-32 shuffles as in the fp32 kernel, and the epilogue is the same.
+template <int K>
+constexpr int gemm16_kp() {
+    return K <= 128 ? 128 : 256;
+}
+template <int K, bool LN>
+constexpr size_t gemm16_lds_bytes() {
+    return (size_t)2 * kGemmCols * gemm16_kp<K>() * 2 + (LN ? 2 * K * 4 : 0);
+}
+
+template <int K, bool LN, bool SWISH, bool RES>
+__global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __restrict__ a, int64_t m,
+                                                          const uint16_t* __restrict__ wt, int n,
+                                                          const float* __restrict__ bias,
+                                                          const float* __restrict__ ln_w,
+                                                          const float* __restrict__ ln_b, float eps,
+                                                          const float* res, float* out) {
+    constexpr int KP = gemm16_kp<K>(), S = KP / 16, NCH = KP / 8;
+    static_assert(K % 8 == 0 && K <= KP, "8-element chunks of k");
+    extern __shared__ __align__(16) uint8_t ls16[];  // [2][128][NCH] chunks of 16 bytes, then (LN) [2][K] floats
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.y * kGemmCols;
+    // stage both planes: chunk e of the stage = plane e / (128 NCH), column (e / NCH) % 128,
+    // slot e % NCH, holding the column's chunk slot ^ ((column / 4) % 8); a column past n
+    // reloads column 0 (its results are never stored, and each output column depends only
+    // on its own weights)
+    constexpr int CH = 2 * kGemmCols * NCH;
+    static_assert(CH % 64 == 0 && NCH % 8 == 0, "whole instructions; slots permuted within groups of 8");
+    for (int x = wave; x < CH / 64; x += 4) {
+        const int e = 64 * x + lane;
+        const int p = e / (kGemmCols * NCH), c = (e / NCH) % kGemmCols, sl = e % NCH;
+        const int col = n0 + c < n ? n0 + c : 0;
+        const uint16_t* src = wt + ((size_t)p * n + col) * KP + 8 * (sl ^ ((c >> 2) & 7));
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void*>(src),
+            reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(ls16 + 1024 * x)),
+            16, 0, 0);
+    }
+    const float* lnl = reinterpret_cast<const float*>(ls16 + (size_t)CH * 16);
+    if constexpr (LN) {
+        static_assert(K % 4 == 0 && K / 2 <= 64, "LayerNorm parameters in one instruction");
+        if (wave == 0 && lane < K / 2) {
+            const float* src = lane < K / 4 ? ln_w + 4 * lane : ln_b + 4 * (lane - K / 4);
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(lnl)), 16, 0,
+                0);
+        }
+    }
+    // this lane's chunks of its row: k = 16 s + 8 h .. + 7 (zeros past K)
+    const int64_t row = (int64_t)blockIdx.x * kGemmRows + wave * 32 + i;
+    float av[S][8];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int k0 = 16 * s + 8 * h;
+        if (row < m && k0 < K) {
+            const f32x4* src = reinterpret_cast<const f32x4*>(a + row * K + k0);
+            const f32x4 v0 = src[0], v1 = src[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                av[s][e] = v0[e];
+                av[s][4 + e] = v1[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) av[s][e] = 0.0f;
+        }
+    }
+    float mean = 0.0f, inv = 0.0f;
+    if constexpr (LN) {
+        float sm = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sm += av[s][e];
+        sm += __shfl_xor(sm, 32, 64);
+        mean = __fdiv_rn(sm, (float)K);
+        float v = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (16 * s + 8 * h < K) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = av[s][e] - mean;
+                    v = fmaf(d, d, v);
+                }
+            }
+        }
+        v += __shfl_xor(v, 32, 64);
+        inv = inv_std_of(__fdiv_rn(v, (float)K), eps);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0): this wave's direct loads
+    __syncthreads();
+    // the operand halves
+    u16x8 ahi[S], alo[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int k0 = 16 * s + 8 * h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float x = av[s][e];
+            if constexpr (LN) x = k0 < K ? fmaf((x - mean) * inv, lnl[k0 + e], lnl[K + k0 + e]) : 0.0f;
+            const _Float16 xh = (_Float16)x;
+            const _Float16 xl = (_Float16)(x - (float)xh);
+            ahi[s][e] = __builtin_bit_cast(unsigned short, xh);
+            alo[s][e] = __builtin_bit_cast(unsigned short, xl);
+        }
+    }
     f32x16 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
-    const float* wbase = wl + half * KH * kGemmCols + 4 * i;
-    f32x4 wq[kWPrefetch];
+    // column 4 i + t, chunk 2 s + h: slot (2 s + h) ^ (i % 8)
+    const uint8_t* whi = ls16 + (size_t)(4 * i) * NCH * 16;
+    const uint8_t* wlo = whi + (size_t)kGemmCols * NCH * 16;
 #pragma unroll
-    for (int p = 0; p < kWPrefetch; ++p) wq[p] = *reinterpret_cast<const f32x4*>(wbase + p * kGemmCols);
-#pragma unroll
-    for (int st = 0; st < KH; ++st) {
-        const f32x4 cur = wq[st % kWPrefetch];
-        if (st + kWPrefetch < KH)
-            wq[st % kWPrefetch] = *reinterpret_cast<const f32x4*>(wbase + (st + kWPrefetch) * kGemmCols);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[st], cur[t], acc[t], 0, 0, 0);
-    }
-
-    // epilogue: lane (i, half) holds columns n0 + 4i .. + 3 (tile t: + t) of rows
-    // 8(r/4) + 4 half + r%4; the four columns are one 16-byte chunk, wholly inside or
-    // outside [0, n).  The residual Add reads the rows it overwrites (res == out in place),
-    // so every residual is loaded before the first store: with the stores in between, each
-    // load would wait for the one before it.
-    const int64_t rbase = (int64_t)blockIdx.x * kGemmRows + wave * 32;
-    const int col = n0 + 4 * i;
-    if (col >= n) return;
-    const f32x4 bc = *reinterpret_cast<const f32x4*>(bias + col);
-    f32x4 rv[16];
-    if constexpr (RES) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
-            rv[r] = rr < m ? *reinterpret_cast<const f32x4*>(res + rr * n + col) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    }
-    auto value = [&](int r) {
-        f32x4 v;
+    for (int s = 0; s < S; ++s) {
+        const int sl = (2 * s + h) ^ (i & 7);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            float x = acc[t][r] + bc[t];
-            if constexpr (SWISH) x = swish_of(x);
-            if constexpr (RES) x = rv[r][t] + x;
-            v[t] = x;
-        }
-        return v;
-    };
-    // a block wholly inside the batch stores without a branch per row: at a branch the
-    // compiler waits for every access in flight (stores included), once per row
-    if (rbase + 32 <= m) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
-            *reinterpret_cast<f32x4*>(out + rr * n + col) = value(r);
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (rr < m) *reinterpret_cast<f32x4*>(out + rr * n + col) = value(r);
+            const u16x8 bh = *reinterpret_cast<const u16x8*>(whi + ((size_t)t * NCH + sl) * 16);
+            const u16x8 bl = *reinterpret_cast<const u16x8*>(wlo + ((size_t)t * NCH + sl) * 16);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
+                                                            __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
+                                                            __builtin_bit_cast(f16x8, bl), acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, alo[s]),
+                                                            __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
         }
     }
+    gemm_epilogue<SWISH, RES, 4>(acc, (int64_t)blockIdx.x * kGemmRows + wave * 32, h, n0 + 4 * i, m, n, bias, res,
+                                 out);
 }
 
 // ---------------------------------------------------------------- attention
@@ -433,13 +602,31 @@ __global__ __launch_bounds__(256) void neck_final_kernel(const float* __restrict
 }
 
 template <int K, bool LN, bool SWISH, bool RES>
+int gemm16_go(const float* a, int64_t m, const uint16_t* wt, int n, const float* bias, const float* ln_w,
+              const float* ln_b, float eps, const float* res, float* out, hipStream_t st) {
+    static_assert(gemm16_kp<K>() == neck_f16_kp(K), "the planes' padding");
+    const int64_t gx = (m + kGemmRows - 1) / kGemmRows;
+    const int gy = (n + kGemmCols - 1) / kGemmCols;
+    if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
+    neck_gemm16_kernel<K, LN, SWISH, RES><<<dim3((unsigned)gx, (unsigned)gy), 256, gemm16_lds_bytes<K, LN>(), st>>>(
+        a, m, wt, n, bias, ln_w, ln_b, eps, res, out);
+    PPOCR_HIP(hipGetLastError());
+    return PPOCR_OK;
+}
+
+// Tiles of 32 columns per wave of the tail's GEMMs (4: 4-wave workgroups; 2, 8-wave
+// workgroups with two waves per SIMD, measured 2% slower).
+constexpr int kGemmTilesPerWave = 4;
+
+template <int K, bool LN, bool SWISH, bool RES>
 int gemm_go(const float* a, int64_t m, const float* w, int n, const float* bias, const float* ln_w,
             const float* ln_b, float eps, const float* res, float* out, hipStream_t st) {
     const int64_t gx = (m + kGemmRows - 1) / kGemmRows;
     const int gy = (n + kGemmCols - 1) / kGemmCols;
     if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
     const size_t lds = (size_t)K * kGemmCols * 4 + (LN ? 2 * K * 4 : 0);
-    neck_gemm_kernel<K, LN, SWISH, RES><<<dim3((unsigned)gx, (unsigned)gy), 256, lds, st>>>(
+    constexpr int TPW = kGemmTilesPerWave;
+    neck_gemm_kernel<K, LN, SWISH, RES, TPW><<<dim3((unsigned)gx, (unsigned)gy), gemm_threads<TPW>(), lds, st>>>(
         a, m, w, n, bias, ln_w, ln_b, eps, res, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
@@ -485,23 +672,31 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         const NeckBlockDev& k = nk.block[b];
         const float* xr = b == 0 ? xin : x;
         // LN1 -> qkv
-        if (int e = gemm_go<kNeckDim, true, false, false>(xr, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b, k.ln1_eps,
-                                                          nullptr, qkv, st))
+        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, false, false>(xr, m, k.qkv_h, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b,
+                                                                    k.ln1_eps, nullptr, qkv, st)
+                           : gemm_go<kNeckDim, true, false, false>(xr, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b,
+                                                                   k.ln1_eps, nullptr, qkv, st))
             return e;
         const dim3 ag((unsigned)lines, (unsigned)nk.heads);
         neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
         PPOCR_HIP(hipGetLastError());
         // x = x + proj(att)
-        if (int e = gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr, 0.0f, xr, x,
-                                                          st))
+        if (int e = nk.f16 ? gemm16_go<kNeckDim, false, false, true>(att, m, k.proj_h, D, k.proj_b, nullptr, nullptr,
+                                                                    0.0f, xr, x, st)
+                           : gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr,
+                                                                   0.0f, xr, x, st))
             return e;
         // LN2 -> fc1 -> swish
-        if (int e = gemm_go<kNeckDim, true, true, false>(x, m, k.fc1_w, H, k.fc1_b, k.ln2_w, k.ln2_b, k.ln2_eps,
-                                                         nullptr, hid, st))
+        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, true, false>(x, m, k.fc1_h, H, k.fc1_b, k.ln2_w, k.ln2_b,
+                                                                   k.ln2_eps, nullptr, hid, st)
+                           : gemm_go<kNeckDim, true, true, false>(x, m, k.fc1_w, H, k.fc1_b, k.ln2_w, k.ln2_b,
+                                                                  k.ln2_eps, nullptr, hid, st))
             return e;
         // x = x + fc2(hid)
-        if (int e = gemm_go<kNeckHidden, false, false, true>(hid, m, k.fc2_w, D, k.fc2_b, nullptr, nullptr, 0.0f, x,
-                                                             x, st))
+        if (int e = nk.f16 ? gemm16_go<kNeckHidden, false, false, true>(hid, m, k.fc2_h, D, k.fc2_b, nullptr, nullptr,
+                                                                       0.0f, x, x, st)
+                           : gemm_go<kNeckHidden, false, false, true>(hid, m, k.fc2_w, D, k.fc2_b, nullptr, nullptr,
+                                                                      0.0f, x, x, st))
             return e;
     }
     neck_final_kernel<<<(unsigned)((m + 3) / 4), 256, 0, st>>>(x, m, D, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);

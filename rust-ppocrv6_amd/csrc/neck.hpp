@@ -21,6 +21,10 @@ struct NeckBlockDev {
     const float *ln2_w, *ln2_b;
     float ln2_eps;
     const float *fc1_w, *fc1_b, *fc2_w, *fc2_b;
+    // fp16 planes of each W^T, [2][N][kp] (the nearest half of each weight, then the nearest
+    // half of what it leaves; k padded with zeros to kp = 128 for K <= 128, else 256), used
+    // when NeckDev::f16 is set
+    const uint16_t *qkv_h, *proj_h, *fc1_h, *fc2_h;
 };
 
 struct NeckDev {
@@ -29,7 +33,13 @@ struct NeckDev {
     NeckBlockDev block[kNeckMaxBlocks];
     const float *lnf_w = nullptr, *lnf_b = nullptr;
     float lnf_eps = 0.0f;
+    // the GEMMs run on fp16 halves (three products): set when the weights bound every GEMM
+    // operand inside fp16's range (neck_f16_bounds_ok)
+    bool f16 = false;
 };
+
+// k of a weight's fp16 planes, padded: 128 for K <= 128, else 256.
+constexpr int neck_f16_kp(int k) { return k <= 128 ? 128 : 256; }
 
 // Floats of workspace per token row: the residual stream and the shortcut rows (D each),
 // qkv (3D), the attention output (D) and the MLP hidden layer (H).

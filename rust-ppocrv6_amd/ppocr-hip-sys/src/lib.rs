@@ -163,6 +163,8 @@ extern "C" {
     pub fn ppocr_rn_destroy(h: *mut ppocr_rn_t);
     pub fn ppocr_rn_shape(h: *const ppocr_rn_t, dim: *mut i64, heads: *mut i64, hidden: *mut i64,
                           blocks: *mut c_int) -> c_int;
+    /// The tail's MatMul arithmetic: 1 fp16 halves, 0 fp32 (no counterpart in the reference).
+    pub fn ppocr_rn_gemm_halves(h: *const ppocr_rn_t) -> c_int;
     pub fn ppocr_rn_workspace_bytes(h: *const ppocr_rn_t, m: i64) -> usize;
     pub fn ppocr_rn_forward_dev(h: *const ppocr_rn_t, d_x: *const f32, d_shortcut: *const f32, m: i64,
                                 d_line_off: *const i64, lines: i64, layout: c_int, d_out: *mut f32,

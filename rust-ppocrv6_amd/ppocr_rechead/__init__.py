@@ -357,6 +357,15 @@ class RecNeck:
     def handle(self):
         return self._h
 
+    @property
+    def gemm_halves(self):
+        """True when the tail's MatMuls run on fp16 halves of both operands (three exact
+        products summed in fp32), False on fp32 products."""
+        r = _lib.lib().ppocr_rn_gemm_halves(self._h)
+        if r < 0:
+            _check(r)
+        return r == 1
+
     def workspace_bytes(self, m):
         return int(_lib.lib().ppocr_rn_workspace_bytes(self._h, m))
 

@@ -83,6 +83,7 @@ SIGNATURES = {
     "ppocr_rn_destroy": (None, [_vp]),
     "ppocr_rn_shape": (_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                               ctypes.POINTER(_int)]),
+    "ppocr_rn_gemm_halves": (_int, [_vp]),
     "ppocr_rn_workspace_bytes": (_sz, [_vp, _i64]),
     "ppocr_rn_forward_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _sz, _vp]),
     "ppocr_rn_forward": (_int, [_vp, _vp, _vp, _vp, _i64, _int, _vp]),

@@ -62,6 +62,8 @@ def test_argument_errors_do_not_need_a_device(rh):
     assert L.ppocr_rh_footprint_bytes(None) == 0
     assert L.ppocr_rh_auto_mode(None) == -1
     assert L.ppocr_rh_guard_limits(None, 2, None, None, None) == rh.PPOCR_ERR_INVALID_ARG
+    assert L.ppocr_rn_gemm_halves(None) == rh.PPOCR_ERR_INVALID_ARG
+    assert rh._lib.last_error() == "RecNeckHip: null neck handle"
     assert L.ppocr_rh_logits(None, None, 1, 2, None) == rh.PPOCR_ERR_INVALID_ARG
     assert rh._lib.last_error() == "MatMulQuantizedB: null head handle"
 

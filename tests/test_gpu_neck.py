@@ -5,9 +5,9 @@ constructor and the device entry point against each other bit for bit; and the n
 feeding the head against the oracle's neck feeding the oracle's head.
 
 The bar: the kernels sum the MatMuls and the attention in another order than the oracle
-(fp32 MFMA, an online softmax), so the tail's outputs (magnitude up to ~15 with the final
-LayerNorm's weights) may differ by a few fp32 roundings of the sums they pass through;
-they are held to 1e-4 absolute + 1e-5 relative."""
+(MFMA on fp16 halves of both operands or on fp32, an online softmax), so the tail's outputs
+(magnitude up to ~30 with the final LayerNorm's weights) may differ by a few fp32 roundings
+of the sums they pass through; they are held to 1e-4 absolute + 1e-5 relative."""
 import numpy as np
 import pytest
 
@@ -63,6 +63,26 @@ def test_neck_large_batch_against_the_oracle_on_sampled_lines(orc, rh):
         t0, t1 = off[b], off[b + 1]
         ref = oracle_neck(orc, w, x[t0:t1], sc[t0:t1], np.array([0, t1 - t0]))
         _check(got[t0:t1], ref, f"large batch line {b}")
+    neck.close()
+
+
+def test_neck_matmul_arithmetic_follows_the_weight_bounds(orc, rh):
+    """The model's weights bound every MatMul operand far inside fp16's range (LayerNorm
+    outputs, attention outputs no larger than the value rows, swish no larger than its
+    input), so the MatMuls run on fp16 halves; an fc1 weight 2000 times larger bounds fc2's
+    input beyond the limit (16384) and the tail keeps fp32 products.  Both against the
+    oracle at the same bar."""
+    w = neck_weights(seed=41)
+    neck = _make(rh, w)
+    assert neck.gemm_halves
+    x, sc, off = _inputs([37, 120, 5], seed=16)
+    _check(neck.forward(x, sc, off), oracle_neck(orc, w, x, sc, off), "fp16 halves")
+    neck.close()
+    big = {**w, "blocks": [dict(b) for b in w["blocks"]]}
+    big["blocks"][1]["fc1_w"] = (big["blocks"][1]["fc1_w"] * np.float32(2000.0)).astype(np.float32)
+    neck = _make(rh, big)
+    assert not neck.gemm_halves
+    _check(neck.forward(x, sc, off), oracle_neck(orc, big, x, sc, off), "fp32 products")
     neck.close()
 
 
