@@ -1254,12 +1254,20 @@ std::vector<uint16_t> neck_half_planes(const float* w, int64_t K, int64_t N) {
     return out;
 }
 
-// Whether the weights keep every operand of the tail's GEMMs inside fp16's range, with room:
-// each operand is a LayerNorm output (|z_k| <= sqrt(D - 1) for the normalised row, so
+// Whether the weights keep every operand of the tail's GEMMs and attention inside fp16's range,
+// with room: each operand is a LayerNorm output (|z_k| <= sqrt(D - 1) for the normalised row, so
 // |y_k| <= sqrt(D - 1) |w_k| + |b_k|), the attention's output (a convex combination of the
-// value rows, so no larger than them) or the swish of fc1's output (|x sigmoid(x)| <= |x|);
+// value rows, so no larger than them), q, k or v (products of LN1's output), or the swish of
+// fc1's output (|x sigmoid(x)| <= |x|); the attention's probabilities lie in [0, 1];
 // a product's bound is max_c sum_k |W[k][c]| times its input's bound plus max |bias|.
-bool neck_f16_bounds_ok(const NeckHost& nh) {
+// The largest e <= 15 with bound * 2^e <= 32768 (half of fp16's largest finite value).
+int neck_f16_exponent(double bound) {
+    int e = 0;
+    while (e < 15 && bound * std::ldexp(1.0, e + 1) <= 32768.0) ++e;
+    return e;
+}
+
+bool neck_f16_bounds_ok(const NeckHost& nh, int (*exps)[3]) {
     const int64_t D = nh.dim, H = nh.hidden;
     constexpr double kLimit = 16384.0;  // a quarter of fp16's largest finite value
     auto amax = [](const float* v, int64_t n) {
@@ -1281,11 +1289,17 @@ bool neck_f16_bounds_ok(const NeckHost& nh) {
     for (const ppocr_rn_block_t& b : nh.blocks) {
         const double y1 = zmax * amax(b.ln1_w, D) + amax(b.ln1_b, D);  // qkv's input
         const double y2 = zmax * amax(b.ln2_w, D) + amax(b.ln2_b, D);  // fc1's input
-        const double v = y1 * col_l1(b.qkv_w, D, 3 * D, 2 * D, D) + amax(b.qkv_b + 2 * D, D);  // proj's input
+        const double qk = y1 * col_l1(b.qkv_w, D, 3 * D, 0, 2 * D) + amax(b.qkv_b, 2 * D);     // the attention's q, k
+        const double v = y1 * col_l1(b.qkv_w, D, 3 * D, 2 * D, D) + amax(b.qkv_b + 2 * D, D);  // its v, proj's input
         const double hs = y2 * col_l1(b.fc1_w, D, H, 0, H) + amax(b.fc1_b, H);               // fc2's input
         const double wmax = std::max(std::max(amax(b.qkv_w, D * 3 * D), amax(b.proj_w, D * D)),
                                      std::max(amax(b.fc1_w, D * H), amax(b.fc2_w, H * D)));
-        if (!(y1 <= kLimit && y2 <= kLimit && v <= kLimit && hs <= kLimit && wmax <= kLimit)) return false;
+        if (!(y1 <= kLimit && y2 <= kLimit && qk <= kLimit && v <= kLimit && hs <= kLimit && wmax <= kLimit))
+            return false;
+        const size_t i = (size_t)(&b - nh.blocks.data());
+        exps[i][0] = neck_f16_exponent(qk * (double)std::fabs(nh.scale));  // q * scale
+        exps[i][1] = neck_f16_exponent(qk);                                // k
+        exps[i][2] = neck_f16_exponent(v);                                 // v
     }
     return true;
 }
@@ -1319,7 +1333,8 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
     parts.push_back({nh.lnf_w, D});
     parts.push_back({nh.lnf_b, D});
     // the fp16 planes of each block's four weights, as float-sized parts after the rest
-    const bool f16 = neck_f16_bounds_ok(nh);
+    int exps[kNeckMaxBlocks][3] = {};
+    const bool f16 = neck_f16_bounds_ok(nh, exps);
     std::vector<std::vector<uint16_t>> planes;
     if (f16) {
         for (const ppocr_rn_block_t& b : nh.blocks) {
@@ -1389,6 +1404,9 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
         b.proj_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
         b.fc1_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
         b.fc2_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
+        b.attn_eq = exps[i][0];
+        b.attn_ek = exps[i][1];
+        b.attn_ev = exps[i][2];
     }
     *out = h.release();
     return PPOCR_OK;

@@ -550,6 +550,181 @@ __global__ __launch_bounds__(256) void neck_attn_kernel(const float* __restrict_
     }
 }
 
+// The same attention on fp16 halves (when the weights bound q, k and v inside fp16's range,
+// as for the MatMuls): x = x_hi + x_lo for q * scale, k, v and the probabilities p, three
+// products per MFMA step (hi hi, hi lo, lo hi; exact, summed in fp32) on
+// v_mfma_f32_16x16x16_f16, which takes a head's 16 dims (or 16 keys) in one step.  The
+// operand layouts of the 16x16x16 form: lane l holds row (A) or column (B) l % 16 at
+// contraction indices 4 (l / 16) .. + 3; so K rows and V^T rows are read 4 halves at a
+// time in their natural order, and P^T's operand of key tile t is again the lane's own
+// scores (keys 16 t + 4 g + j), split in place.  Every operand is split after an exact
+// scaling by a power of two, undone on the scores and the output: the MFMA takes fp16
+// subnormal inputs as zeros (measured: the halves of values below 0.25 would vanish), so
+// the scalings lift the low halves above fp16's smallest normal (6.1e-5).  q, k and v use
+// exponents from their bounds (neck creation); the probabilities, in (0, 1], 2^15.
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+constexpr int kKhStride = 20;  // halves per K row in LDS: 16 dims + 4, so the 16 rows a
+                               // lane group reads at once fall in distinct banks
+
+__device__ __forceinline__ void split_half(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restrict__ qkv, int64_t m,
+                                                          const int64_t* __restrict__ line_off, int64_t lines,
+                                                          int64_t line_len, int dim, float scale, int eq, int ek,
+                                                          int ev, float* __restrict__ o) {
+    // powers of two: exact scalings of the operands before the split, undone on the scores
+    // and the output
+    const float qmul = ldexpf(1.0f, eq), kmul = ldexpf(1.0f, ek), vmul = ldexpf(1.0f, ev);
+    const float sdiv = ldexpf(1.0f, -(eq + ek)), vdiv = ldexpf(1.0f, -ev);
+    static_assert(HD <= 16, "one 16-wide MFMA tile holds a head's dims");
+    constexpr int KT = kAttnKeyTiles, QB = kAttnQBlocks;
+    __shared__ __align__(16) _Float16 ks[2][kAttnKeys * kKhStride];  // K block [hi, lo][t][dim]
+    __shared__ __align__(16) _Float16 vt[2][16 * kVtStride];         // V block transposed [hi, lo][dim][t]
+    const int64_t line = blockIdx.x;
+    const int h = blockIdx.y;
+    const int64_t t0 = line_off ? min(max(line_off[line], (int64_t)0), m) : min(line * line_len, m);
+    const int64_t t1 = line_off ? min(max(line_off[line + 1], t0), m) : min(t0 + line_len, m);
+    if (t1 - t0 <= 0) return;
+    const int T = (int)(t1 - t0);  // the launcher bounds m by INT32_MAX
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
+    const int64_t stride = 3 * (int64_t)dim;
+    const float* base = qkv + t0 * stride + h * HD;  // the line's first row, this head
+    const int sd = tid & 15, st0 = tid >> 4;  // staging: dim tid % 16 of rows tid / 16 + 16 x
+    for (int qpass = 0; qpass < T; qpass += 4 * 16 * QB) {
+        // this wave's query blocks: queries qpass + 16 (wave + 4 x) + c, dims 4 g .. + 3
+        f16x4 qh[QB], ql[QB];
+        f32x4 oa[QB];
+        float mx[QB], ls[QB];
+#pragma unroll
+        for (int x = 0; x < QB; ++x) {
+            const int q = qpass + 16 * (wave + 4 * x) + c;
+            const float* row = base + (int64_t)q * stride;
+            float qv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = 4 * g + e;
+                qv[e] = (q < T && d < HD) ? row[d] : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                _Float16 hi, lo;
+                split_half((qv[e] * scale) * qmul, hi, lo);  // the Mul(scale) node, rounded as it
+                qh[x][e] = hi;
+                ql[x][e] = lo;
+            }
+            oa[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mx[x] = -INFINITY;
+            ls[x] = 0.0f;
+        }
+        for (int kb = 0; kb < T; kb += kAttnKeys) {
+            const int rem = T - kb;  // keys of the line from this block on
+            // stage keys kb .. kb + 127 (zeros past the line's end and past the head's dims),
+            // every load issued before the first LDS store
+            float kv[KT], vv[KT];
+#pragma unroll
+            for (int x = 0; x < KT; ++x) {
+                const int t = st0 + 16 * x;
+                kv[x] = vv[x] = 0.0f;
+                if (t < rem && sd < HD) {
+                    const float* row = base + (int64_t)(kb + t) * stride + sd;
+                    kv[x] = row[dim];
+                    vv[x] = row[2 * dim];
+                }
+            }
+            __syncthreads();  // the previous block's readers are done
+#pragma unroll
+            for (int x = 0; x < KT; ++x) {
+                const int tl = st0 + 16 * x;
+                split_half(kv[x] * kmul, ks[0][tl * kKhStride + sd], ks[1][tl * kKhStride + sd]);
+                split_half(vv[x] * vmul, vt[0][sd * kVtStride + tl], vt[1][sd * kVtStride + tl]);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int x = 0; x < QB; ++x) {
+                const int q0 = qpass + 16 * (wave + 4 * x);
+                if (q0 >= T) continue;  // uniform over the wave
+                // one query block at a time: interleaved, their scores would all be live
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 sc[KT];
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+                    const f16x4 kh = *reinterpret_cast<const f16x4*>(&ks[0][(16 * t + c) * kKhStride + 4 * g]);
+                    const f16x4 kl = *reinterpret_cast<const f16x4*>(&ks[1][(16 * t + c) * kKhStride + 4 * g]);
+                    f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, qh[x], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, ql[x], acc, 0, 0, 0);
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh[x], acc, 0, 0, 0) * sdiv;
+                }
+                // keys past the line's end score -inf (their p is then exactly 0); the block's
+                // maximum for query q0 + c: this lane's keys, then the lane groups
+                float bm = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        sc[t][jj] = (16 * t + 4 * g + jj < rem) ? sc[t][jj] : -INFINITY;
+                        bm = max_f32(bm, sc[t][jj]);
+                    }
+                }
+                bm = max_f32(bm, __shfl_xor(bm, 16, 64));
+                bm = max_f32(bm, __shfl_xor(bm, 32, 64));
+                const float nm = max_f32(mx[x], bm);
+                if (kb > 0) {
+                    // rescale the sums so far (every block of a pass after the first follows one
+                    // that set a finite maximum)
+                    const float corr = __expf(mx[x] - nm);
+                    ls[x] *= corr;
+                    oa[x] = oa[x] * corr;
+                }
+                mx[x] = nm;
+                float l = 0.0f;
+                f32x4 ob = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int t = 0; t < KT; ++t) {
+                    f16x4 ph, pl;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        // p scaled by 2^15 (exact; it cancels in sum(p v) / sum(p)), so the halves
+                        // of small probabilities stay above fp16's subnormals
+                        const float p = __expf(sc[t][jj] - nm) * 32768.0f;
+                        l += p;
+                        _Float16 hi, lo;
+                        split_half(p, hi, lo);
+                        ph[jj] = hi;
+                        pl[jj] = lo;
+                    }
+                    // O^T += V^T P^T: even and odd key tiles on two accumulators
+                    const f16x4 vh = *reinterpret_cast<const f16x4*>(&vt[0][c * kVtStride + 16 * t + 4 * g]);
+                    const f16x4 vl = *reinterpret_cast<const f16x4*>(&vt[1][c * kVtStride + 16 * t + 4 * g]);
+                    f32x4& acc = (t & 1) ? ob : oa[x];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph, acc, 0, 0, 0);
+                }
+                oa[x] += ob;
+                ls[x] += l;
+            }
+        }
+        // per query: the sums of the four lane groups; lane l writes query q0 + c, dims 4 g + j
+#pragma unroll
+        for (int x = 0; x < QB; ++x) {
+            const int q = qpass + 16 * (wave + 4 * x) + c;
+            float l = ls[x];
+            l += __shfl_xor(l, 16, 64);
+            l += __shfl_xor(l, 32, 64);
+            if (q < T) {
+                float* orow = o + (t0 + q) * (int64_t)dim + h * HD;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    if (4 * g + jj < HD) orow[4 * g + jj] = __fdiv_rn(oa[x][jj] * vdiv, l);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- layouts and the end
 // Channels-first lines (line b: [D][T_b] at D * t0_b, the graph's [1, D, T] per line) to
 // token rows [m][D]: a 32-row x 32-channel tile per workgroup through LDS (reads along the
@@ -678,7 +853,11 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
                                                                    k.ln1_eps, nullptr, qkv, st))
             return e;
         const dim3 ag((unsigned)lines, (unsigned)nk.heads);
-        neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
+        if (nk.f16)
+            neck_attn16_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale,
+                                                                k.attn_eq, k.attn_ek, k.attn_ev, att);
+        else
+            neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
         PPOCR_HIP(hipGetLastError());
         // x = x + proj(att)
         if (int e = nk.f16 ? gemm16_go<kNeckDim, false, false, true>(att, m, k.proj_h, D, k.proj_b, nullptr, nullptr,

@@ -25,6 +25,10 @@ struct NeckBlockDev {
     // half of what it leaves; k padded with zeros to kp = 128 for K <= 128, else 256), used
     // when NeckDev::f16 is set
     const uint16_t *qkv_h, *proj_h, *fc1_h, *fc2_h;
+    // the attention's operands scaled by powers of two before the fp16 split (q * scale by
+    // 2^attn_eq, k by 2^attn_ek, v by 2^attn_ev), chosen from their bounds so that the halves
+    // of all but negligible values stay above fp16's subnormals
+    int attn_eq, attn_ek, attn_ev;
 };
 
 struct NeckDev {
