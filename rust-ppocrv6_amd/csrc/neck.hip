@@ -9,11 +9,14 @@
 //
 // gfx950 layout: the token rows of all lines packed back to back, channels contiguous
 // ([m][D], D = 120).  Four kinds of kernels:
-//   neck_gemm_kernel   rows x W[K][N] on fp32 MFMA (v_mfma_f32_32x32x2_f32: fp32 products,
-//                      fp32 sums), with the LayerNorm of the rows folded into the operand
-//                      load and bias, swish and the residual Add folded into the epilogue;
-//   neck_attn_kernel   one workgroup per (line, head): the line's K, Q and V of the head in
-//                      LDS, scores and weighted sums on fp32 MFMA, the softmax between;
+//   neck_gemm16_kernel rows x W[K][N] on fp16 halves of both operands (three exact products
+//                      per f16 MFMA step, fp32 sums), with the LayerNorm of the rows folded
+//                      into the operand load and bias, swish and the residual Add folded into
+//                      the epilogue; neck_gemm_kernel the same on fp32 MFMA, for weights that
+//                      do not bound the operands inside fp16's range;
+//   neck_attn16_kernel one workgroup per (line, head): the line's K and V of the head in LDS,
+//                      scores and weighted sums on MFMA (fp16 halves; neck_attn_kernel on
+//                      fp32), an online softmax between;
 //   neck_cf_rows_kernel  a line's channels-first [D][T] block to token rows;
 //   neck_final_kernel  the last LayerNorm plus the shortcut.
 #include <algorithm>
