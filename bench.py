@@ -385,6 +385,7 @@ def main():
                 "TFLOPs": round(nflops / (ms_n / 1e3) / 1e12, 2),
                 "fp32_peak_frac": round(nflops / (ms_n / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4),
                 "flops_per_step": nflops, "head_input_max_abs": round(float(np.abs(feats).max()), 2),
+                "matmul_arithmetic": "fp16 halves (3 products)" if nk.gemm_halves else "fp32",
                 "neck_then_head": {}}
         for hm in sorted({mode, 5}):
             hws = head.workspace_bytes(m, hm)
