@@ -216,8 +216,133 @@ __device__ __forceinline__ unsigned short split_term(float x, int t) {
     return __builtin_bit_cast(unsigned short, (T)r2);
 }
 
-// Activation fragment of one lane for MFMA step s: row `row` of a (zero when the row
-// is not valid), the 8 k values of the lane's slot, as the bf16 term its product uses;
+// Activation fragments of one lane for every MFMA step of a 32-row block.  A step takes
+// the 8 k values of its slot (group g of 8 along k) as the 16-bit term its product uses;
+// consecutive steps that feed both lane halves the same groups (the products of one group
+// pair) share one load.  Every load of the block is issued before any value is used, so a
+// wave waits for memory once per block, not once per step.  `row` must be a row of a
+// (callers pass row 0 for lanes past the batch: their results are never written).
+// `amax` is raised to the largest |value| loaded, `ss` accumulates the squares of the
+// values of product 0 (each k once over the two halves).  `vec` > 0: rows and groups are
+// 16-byte aligned, so a group is two float4 loads; vec < 0 selects the channels-first
+// layout [lines][k][T] of the tensor before the neck's transpose, T = -vec: row r is step
+// r % T of line r / T, and its k values are T floats apart.  Only the last group can
+// reach past k (k > 8G - 8); its missing values are zeros, read from a clamped address.
+template <int C, int G>
+struct ActPlan {
+    using GE = Geo<C, G>;
+    static constexpr int S = GE::S;
+    // group of step s on half h, -1 for a padding slot
+    __host__ __device__ static constexpr int grp(int s, int h) {
+        const Slot sl = GE::slot(s, h);
+        return sl.p < 0 ? -1 : sl.g;
+    }
+    // step s needs values other than step s-1's on some half
+    __host__ __device__ static constexpr bool fresh(int s) {
+        if (s == 0) return true;
+        for (int h = 0; h < 2; ++h)
+            if (grp(s, h) >= 0 && grp(s, h) != grp(s - 1, h)) return true;
+        return false;
+    }
+    // load used by step s, counted in step order
+    __host__ __device__ static constexpr int lid(int s) {
+        int l = 0;
+        for (int x = 1; x <= s; ++x) l += fresh(x) ? 1 : 0;
+        return l;
+    }
+    static constexpr int NL = lid(S - 1) + 1;
+    // group loaded for half h at fresh step s: its own, else (padding) the other half's
+    __host__ __device__ static constexpr int load_grp(int s, int h) {
+        return grp(s, h) >= 0 ? grp(s, h) : (grp(s, 1 - h) >= 0 ? grp(s, 1 - h) : 0);
+    }
+};
+
+template <int C, int G, int s>
+__device__ __forceinline__ void act_load(const float* __restrict__ rp, int64_t kst, int k, bool vec4, int h,
+                                         float (&x)[ActPlan<C, G>::NL][8]) {
+    using AP = ActPlan<C, G>;
+    if constexpr (AP::fresh(s)) {
+        constexpr int l = AP::lid(s), g0 = AP::load_grp(s, 0), g1 = AP::load_grp(s, 1);
+        constexpr bool last = g0 == G - 1 || g1 == G - 1;
+        const int g = h ? g1 : g0;
+        if (vec4) {
+            // 16-byte aligned rows, k % 4 == 0: a partial last group holds 4 values
+            const float* p = rp + 8 * g;
+            const bool hi = !last || 8 * g + 8 <= k;
+            const f32x4 v0 = reinterpret_cast<const f32x4*>(p)[0];
+            const f32x4 v1 = reinterpret_cast<const f32x4*>(p + (hi ? 4 : 0))[0];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[l][e] = v0[e];
+                x[l][4 + e] = hi ? v1[e] : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int kk = 8 * g + e;
+                const float v = rp[(int64_t)(last ? min(kk, k - 1) : kk) * kst];
+                x[l][e] = (!last || kk < k) ? v : 0.0f;
+            }
+        }
+    }
+}
+
+template <int C, int G, int s>
+__device__ __forceinline__ u16x8 act_split(const float (&x)[ActPlan<C, G>::NL][8], int h, float& amax, float& ss) {
+    using AP = ActPlan<C, G>;
+    constexpr Slot s0 = Geo<C, G>::slot(s, 0), s1 = Geo<C, G>::slot(s, 1);
+    constexpr int l = AP::lid(s);
+    if constexpr (AP::fresh(s)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, __builtin_fabsf(x[l][e]));
+    }
+    // every group is fed to product 0 once, on one half, so its squares are counted once
+    if constexpr (s0.p == 0 || s1.p == 0) {
+        const bool p0 = h ? s1.p == 0 : s0.p == 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = p0 ? fmaf(x[l][e], x[l][e], ss) : ss;
+    }
+    constexpr int t0 = s0.p < 0 ? 0 : CfgT<C>::act(s0.p), t1 = s1.p < 0 ? 0 : CfgT<C>::act(s1.p);
+    const int term = h ? t1 : t0;
+    u16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = split_term<CfgT<C>::f16>(x[l][e], term);
+    if constexpr (s0.p < 0 || s1.p < 0) {
+        const bool pad = h ? s1.p < 0 : s0.p < 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = pad ? (unsigned short)0 : f[e];
+    }
+    return f;
+}
+
+// Issue the loads of a block (act_issue), then split what they return (act_split_all).
+template <int C, int G>
+__device__ __forceinline__ void act_issue(const float* __restrict__ a, int64_t row, int k, int vec, int h,
+                                          float (&x)[ActPlan<C, G>::NL][8]) {
+    int64_t kst = 1;
+    const float* rp = a + row * (int64_t)k;
+    if (vec < 0) {
+        kst = -(int64_t)vec;
+        const int64_t line = row / kst;
+        rp = a + line * kst * k + (row - line * kst);
+    }
+    const bool vec4 = vec > 0;
+    [&]<int... s>(std::integer_sequence<int, s...>) {
+        (act_load<C, G, s>(rp, kst, k, vec4, h, x), ...);
+    }(std::make_integer_sequence<int, ActPlan<C, G>::S>{});
+}
+template <int C, int G>
+__device__ __forceinline__ void act_split_all(const float (&x)[ActPlan<C, G>::NL][8], int h,
+                                              u16x8 (&bf)[Geo<C, G>::S], float& amax, float& ss) {
+    [&]<int... s>(std::integer_sequence<int, s...>) {
+        ((bf[s] = act_split<C, G, s>(x, h, amax, ss)), ...);
+    }(std::make_integer_sequence<int, ActPlan<C, G>::S>{});
+}
+
+// Activation fragment of one lane for MFMA step s, loaded and split on its own (the
+// rescue passes' gather kernels, which hold more state, use this form: it keeps fewer
+// values live): row `row` of a (zero when the row is not valid), the 8 k values of the
+// lane's slot, as the bf16 term its product uses;
 // `amax` is raised to the largest |value| loaded, `ss` accumulates the squares of the
 // values loaded for product 0 (each k once).  `vec`: rows and groups are 16-byte
 // aligned, so each fragment is two float4 loads.  vec < 0 selects the channels-first
@@ -517,15 +642,38 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
         int64_t arow[MB];
         bool valid[MB];
         u16x8 bf[MB][S];
+        constexpr int kOps = stage_direct_min_ops<GE::REC, NT>();
+        // the first tiles start loading before the activations, so the two waits overlap
+        if (t0 < t1) {
+            if constexpr (GATHER) ring_barrier<0>();  // a previous row block's tiles are no longer read
 #pragma unroll
-        for (int b = 0; b < MB; ++b) {
-            arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
-            float amax = 0.0f, ss = 0.0f;
-            [&]<int... s>(std::integer_sequence<int, s...>) {
-                ((bf[b][s] = act_frag<C, G, s>(a, arow[b], valid[b], k, vec, h, amax, ss)), ...);
-            }(std::make_integer_sequence<int, S>{});
-            if (!GATHER && guard_header && chunk == 0)
-                guard_append(amax, ss, lim, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch, guard_cap);
+            for (int x = 0; x < kRing - 1; ++x)
+                stage_direct<GE::REC, NT>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
+        }
+        if constexpr (GATHER) {
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
+                float amax = 0.0f, ss = 0.0f;
+                [&]<int... s>(std::integer_sequence<int, s...>) {
+                    ((bf[b][s] = act_frag<C, G, s>(a, arow[b], valid[b], k, vec, h, amax, ss)), ...);
+                }(std::make_integer_sequence<int, S>{});
+            }
+        } else {
+            float araw[MB][ActPlan<C, G>::NL][8];
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
+                act_issue<C, G>(a, valid[b] ? arow[b] : 0, k, vec, h, araw[b]);
+            }
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                float amax = 0.0f, ss = 0.0f;
+                act_split_all<C, G>(araw[b], h, bf[b], amax, ss);
+                if (guard_header && chunk == 0)
+                    guard_append(amax, ss, lim, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch,
+                                 guard_cap);
+            }
         }
 
         float best[MB], sum[MB], ref[MB];
@@ -539,11 +687,6 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
         }
 
         if (t0 < t1) {
-            constexpr int kOps = stage_direct_min_ops<GE::REC, NT>();
-            if constexpr (GATHER) ring_barrier<0>();  // a previous row block's tiles are no longer read
-#pragma unroll
-            for (int x = 0; x < kRing - 1; ++x)
-                stage_direct<GE::REC, NT>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
             ring_barrier<kOps>();  // tiles t0 and t0+1 are in LDS
             f32x16 acc_a[MB], acc_b[MB];
 #pragma unroll
@@ -775,9 +918,15 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
         const int64_t arow = src.row(j0 + i, m, valid);
         float amax = 0.0f, ss = 0.0f;
         u16x8 bf[S];
-        [&]<int... s>(std::integer_sequence<int, s...>) {
-            ((bf[s] = act_frag<C, G, s>(a, arow, valid, k, vec, h, amax, ss)), ...);
-        }(std::make_integer_sequence<int, S>{});
+        if constexpr (GATHER) {
+            [&]<int... s>(std::integer_sequence<int, s...>) {
+                ((bf[s] = act_frag<C, G, s>(a, arow, valid, k, vec, h, amax, ss)), ...);
+            }(std::make_integer_sequence<int, S>{});
+        } else {
+            float araw[ActPlan<C, G>::NL][8];
+            act_issue<C, G>(a, valid ? arow : 0, k, vec, h, araw);
+            act_split_all<C, G>(araw, h, bf, amax, ss);
+        }
         if (!GATHER && guard_header && chunk == 0)
             guard_append(amax, ss, lim, valid, arow, h, guard_header, guard_rows, guard_epoch, guard_cap);
         // rows of this lane's 16 accumulators (r -> row slot 8*(r/4) + 4*h + (r%4))
