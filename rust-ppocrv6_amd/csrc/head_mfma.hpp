@@ -609,6 +609,18 @@ __device__ __forceinline__ void epi_pieces_of_half(f32x16 (&t)[MB], const float*
 constexpr int kPrefetch = 2;
 constexpr int kRing = 4;  // LDS tile slots of the main statistics pass (a power of two)
 
+// Kernel arguments read all at once: left to itself the compiler loads each one where it is
+// first used, and a kernel whose first steps depend on each other (grid position, then the
+// row list) waits for several scalar-cache misses in a row.
+template <typename T>
+__device__ __forceinline__ void arg_now(const T& x) {
+    asm volatile("" ::"s"(x));
+}
+template <typename... T>
+__device__ __forceinline__ void args_now(const T&... x) {
+    (arg_now(x), ...);
+}
+
 template <int C, int G, int MB, bool GATHER, bool NOREF, int OCC = 8 / kStatsWaves>
 __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
@@ -620,6 +632,8 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     constexpr int RPB = 32 * kStatsWaves * MB;
     constexpr int NT = 64 * kStatsWaves;
     extern __shared__ __align__(16) uint8_t lds[];
+    args_now(a, m, k, vec, rec, tiles, nsplit, tiles_per_chunk, mblocks, p_best, p_sum, p_idx, lim.prec,
+             lim.range_amax, lim.range_ss, guard_header, guard_rows, guard_epoch, guard_cap);
 
     int mbi, chunk;
     map_block(blockIdx.x, nsplit, &mbi, &chunk);

@@ -176,36 +176,37 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
 // agree bit for bit.
 constexpr int kMergeLanes = 8;
 constexpr int kMergeBatch = 8;  // partials per lane loaded together (all of them for nsplit <= 64)
-__device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, const float* __restrict__ p_sum,
-                                              const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
-                                              bool valid, int g, float* inv_out) {
-    RowStat s{-INFINITY, 0.0f, 0.0f, 0};
+// The partials of one row a lane merges, chunks c0, c0 + 8, ..., loaded before any is used
+struct MergeLoad {
+    float bv[kMergeBatch], sv[kMergeBatch];
+    int iv[kMergeBatch];
+};
+__device__ __forceinline__ void merge_issue(const float* __restrict__ p_best, const float* __restrict__ p_sum,
+                                            const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
+                                            bool valid, int c0, MergeLoad& ld) {
     if (valid) {
-        // chunks g, g + 8, g + 16, ... in order; up to kMergeBatch of them are loaded before
-        // any is merged, so their loads are in flight together
-        for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
-            float bv[kMergeBatch], sv[kMergeBatch];
-            int iv[kMergeBatch];
 #pragma unroll
-            for (int x = 0; x < kMergeBatch; ++x) {
-                const int c = c0 + x * kMergeLanes;
-                if (c < nsplit) {
-                    bv[x] = p_best[(int64_t)c * m + row];
-                    sv[x] = p_sum[(int64_t)c * m + row];
-                    iv[x] = p_idx[(int64_t)c * m + row];
-                }
-            }
-#pragma unroll
-            for (int x = 0; x < kMergeBatch; ++x) {
-                if (c0 + x * kMergeLanes < nsplit) {
-                    // partial sums are relative to their own maximum: both operands are
-                    // normalised
-                    const RowStat o{bv[x], sv[x], (bv[x] == -INFINITY) ? 0.0f : bv[x], iv[x]};
-                    s = stat_merge_norm(s, o);
-                }
+        for (int x = 0; x < kMergeBatch; ++x) {
+            const int c = c0 + x * kMergeLanes;
+            if (c < nsplit) {
+                ld.bv[x] = p_best[(int64_t)c * m + row];
+                ld.sv[x] = p_sum[(int64_t)c * m + row];
+                ld.iv[x] = p_idx[(int64_t)c * m + row];
             }
         }
     }
+}
+__device__ __forceinline__ void merge_batch(RowStat& s, const MergeLoad& ld, int nsplit, int c0) {
+#pragma unroll
+    for (int x = 0; x < kMergeBatch; ++x) {
+        if (c0 + x * kMergeLanes < nsplit) {
+            // partial sums are relative to their own maximum: both operands are normalised
+            const RowStat o{ld.bv[x], ld.sv[x], (ld.bv[x] == -INFINITY) ? 0.0f : ld.bv[x], ld.iv[x]};
+            s = stat_merge_norm(s, o);
+        }
+    }
+}
+__device__ __forceinline__ RowStat merge_lanes(RowStat s, float* inv_out) {
 #pragma unroll
     for (int off = 1; off < kMergeLanes; off <<= 1) {
         const RowStat o{__shfl_xor(s.best, off, 64), __shfl_xor(s.sum, off, 64), __shfl_xor(s.ref, off, 64),
@@ -218,6 +219,20 @@ __device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, 
     *inv_out = S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
     return s;
 }
+__device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, const float* __restrict__ p_sum,
+                                              const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
+                                              bool valid, int g, float* inv_out) {
+    RowStat s{-INFINITY, 0.0f, 0.0f, 0};
+    if (valid) {
+        // chunks g, g + 8, g + 16, ... in order, kMergeBatch of them loaded at a time
+        for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
+            MergeLoad ld;
+            merge_issue(p_best, p_sum, p_idx, m, nsplit, row, true, c0, ld);
+            merge_batch(s, ld, nsplit, c0);
+        }
+    }
+    return merge_lanes(s, inv_out);
+}
 
 __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restrict__ p_best,
                                                           const float* __restrict__ p_sum,
@@ -226,12 +241,13 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
                                                           float* __restrict__ row_max, float* __restrict__ row_inv,
                                                           unsigned long long* __restrict__ guard_header,
                                                           unsigned guard_epoch) {
-    if (guard_header && blockIdx.x == 0 && threadIdx.x == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     // 256 / kMergeLanes rows per workgroup
     const int64_t row = (int64_t)blockIdx.x * (256 / kMergeLanes) + threadIdx.x / kMergeLanes;
     const int g = threadIdx.x % kMergeLanes;
     float inv;
     const RowStat s = merged_row(p_best, p_sum, p_idx, m, nsplit, row, row < m, g, &inv);
+    // the guard list of this call is emptied for the next (row 0 exists: m >= 1)
+    if (guard_header && row == 0 && g == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     if (row >= m || g != 0) return;
     if (idx) idx[row] = s.idx;
     if (maxprob) maxprob[row] = inv;
@@ -303,21 +319,41 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
                                                          float* __restrict__ val_out, int32_t* __restrict__ seq,
                                                          int64_t* __restrict__ seq_len, float* __restrict__ score,
                                                          unsigned long long* __restrict__ guard_header,
-                                                         unsigned guard_epoch, int64_t line_len) {
+                                                         unsigned guard_epoch, int64_t line_len, int64_t even_len) {
     __shared__ int32_t s_id[kCtcRound];
-    if (guard_header && blockIdx.x == 0 && threadIdx.x == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     __shared__ float s_v[kCtcRound];
     const int tid = threadIdx.x, lane = tid & 63, g = tid % kMergeLanes, step = tid / kMergeLanes;
     const int64_t line = blockIdx.x;
-    const int64_t t0 = line_off ? min(max(line_off[line], (int64_t)0), m) : min(line * line_len, m);
-    const int64_t t1 = line_off ? min(max(line_off[line + 1], t0), m) : min(t0 + line_len, m);
+    // The first round's partials are loaded while the line's offsets are: at the start the
+    // line would have with equal lines (even_len = m / lines steps each; 0 for line 0), the
+    // usual case.  When the offsets say otherwise the round loads again.
+    const int64_t guess = min(line * (line_off ? even_len : line_len), m);
+    const bool one_batch = nsplit <= kMergeLanes * kMergeBatch;
+    MergeLoad spec;
+    if (one_batch) merge_issue(p_best, p_sum, p_idx, m, nsplit, guess + step, guess + step < m, g, spec);
+    // both offsets of the line in one wait
+    int64_t o0 = line * line_len, o1 = o0 + line_len;
+    if (line_off) {
+        o0 = line_off[line];
+        o1 = line_off[line + 1];
+    }
+    const int64_t t0 = min(max(o0, (int64_t)0), m);
+    const int64_t t1 = line_off ? min(max(o1, t0), m) : min(t0 + line_len, m);
     int64_t cnt = 0;
     float sum = -0.0f;
     int32_t carry = blank;  // index of the step before the current one
     for (int64_t base = t0; base < t1; base += kCtcRound) {
         const int64_t t = base + step;
         float v = 0.0f;
-        const RowStat st = merged_row(p_best, p_sum, p_idx, m, nsplit, t, t < t1, g, &v);
+        RowStat st;
+        if (one_batch && base == guess) {
+            // rows t < t1 <= m were loaded by the speculative issue (guess + step = t < m)
+            RowStat s0{-INFINITY, 0.0f, 0.0f, 0};
+            if (t < t1) merge_batch(s0, spec, nsplit, g);
+            st = merge_lanes(s0, &v);
+        } else {
+            st = merged_row(p_best, p_sum, p_idx, m, nsplit, t, t < t1, g, &v);
+        }
         if (g == 0) {
             const int32_t id = t < t1 ? st.idx : blank;
             if (t < t1) {
@@ -349,6 +385,9 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
     if (tid == 0) {
         seq_len[line] = cnt;
         score[line] = cnt ? sum / (float)cnt : 0.0f;
+        // the guard list of this call is emptied for the next (written last, so the
+        // kernel's first loads do not wait behind it)
+        if (guard_header && line == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     }
 }
 
@@ -409,7 +448,7 @@ int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, 
     merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
                                                        ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score,
                                                        guard ? guard->header : nullptr, guard ? guard->epoch : 0u,
-                                                       ctc.line_len);
+                                                       ctc.line_len, m / ctc.lines);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
