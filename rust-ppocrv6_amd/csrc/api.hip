@@ -1254,6 +1254,46 @@ std::vector<uint16_t> neck_half_planes(const float* w, int64_t K, int64_t N) {
     return out;
 }
 
+// fc1's and fc2's weights in the fused MLP kernel's staging order (NeckBlockDev::mlp_h),
+// each weight times 2^e1 (fc1) or 2^e2 (fc2), exact, before the split, so that the low
+// halves stay above fp16's subnormals.  fc2's contraction index runs in the order
+// K' = 32 T + 16 q + 8 h + e <-> hidden unit 32 T + 16 q + 8 (e / 4) + 4 h + e % 4, the
+// order in which fc1's transposed MFMA output leaves the hidden values in registers.
+std::vector<uint16_t> neck_mlp_tiles(const ppocr_rn_block_t& b, int64_t D, int64_t H, int e1, int e2) {
+    constexpr int kTiles = 8, kTileHalves = 16384;  // 32 KB per tile
+    std::vector<uint16_t> out((size_t)kTiles * kTileHalves, 0);
+    auto split = [](float v, uint16_t* hi, uint16_t* lo) {
+        const _Float16 h = (_Float16)v;
+        *hi = __builtin_bit_cast(uint16_t, h);
+        *lo = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
+    };
+    for (int T = 0; T < kTiles; ++T) {
+        uint16_t* t = out.data() + (size_t)T * kTileHalves;
+        // fc1: [plane][chunk c (16)][unit u (32)][8]: unit 32 T + u, k = 8 c + e
+        for (int c = 0; c < 16; ++c)
+            for (int u = 0; u < 32; ++u)
+                for (int e = 0; e < 8; ++e) {
+                    const int64_t unit = 32 * T + u, k = 8 * c + e;
+                    if (unit >= H || k >= D) continue;
+                    split(std::ldexp(b.fc1_w[k * H + unit], e1), &t[((size_t)c * 32 + u) * 8 + e],
+                          &t[((size_t)(16 + c) * 32 + u) * 8 + e]);
+                }
+        // fc2: [plane][chunk c (4)][column (128)][8]: contraction position K' = 32 T + 8 c + e
+        uint16_t* t2 = t + 8192;
+        for (int c = 0; c < 4; ++c)
+            for (int col = 0; col < 128; ++col)
+                for (int e = 0; e < 8; ++e) {
+                    const int kp = 32 * T + 8 * c + e;
+                    const int ee = kp & 7, hh = (kp >> 3) & 1, q = (kp >> 4) & 1;
+                    const int64_t unit = 32 * T + 16 * q + 8 * (ee >> 2) + 4 * hh + (ee & 3);
+                    if (unit >= H || col >= D) continue;
+                    split(std::ldexp(b.fc2_w[unit * D + col], e2), &t2[((size_t)c * 128 + col) * 8 + e],
+                          &t2[((size_t)(4 + c) * 128 + col) * 8 + e]);
+                }
+    }
+    return out;
+}
+
 // Whether the weights keep every operand of the tail's GEMMs and attention inside fp16's range,
 // with room: each operand is a LayerNorm output (|z_k| <= sqrt(D - 1) for the normalised row, so
 // |y_k| <= sqrt(D - 1) |w_k| + |b_k|), the attention's output (a convex combination of the
@@ -1267,7 +1307,7 @@ int neck_f16_exponent(double bound) {
     return e;
 }
 
-bool neck_f16_bounds_ok(const NeckHost& nh, int (*exps)[3]) {
+bool neck_f16_bounds_ok(const NeckHost& nh, int (*exps)[7]) {
     const int64_t D = nh.dim, H = nh.hidden;
     constexpr double kLimit = 16384.0;  // a quarter of fp16's largest finite value
     auto amax = [](const float* v, int64_t n) {
@@ -1300,6 +1340,10 @@ bool neck_f16_bounds_ok(const NeckHost& nh, int (*exps)[3]) {
         exps[i][0] = neck_f16_exponent(qk * (double)std::fabs(nh.scale));  // q * scale
         exps[i][1] = neck_f16_exponent(qk);                                // k
         exps[i][2] = neck_f16_exponent(v);                                 // v
+        exps[i][3] = neck_f16_exponent(amax(b.fc1_w, D * H));              // fc1's weights
+        exps[i][4] = neck_f16_exponent(amax(b.fc2_w, H * D));              // fc2's weights
+        exps[i][5] = neck_f16_exponent(y2);                                // LN2's output
+        exps[i][6] = neck_f16_exponent(hs);                                // the hidden layer
     }
     return true;
 }
@@ -1333,15 +1377,15 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
     parts.push_back({nh.lnf_w, D});
     parts.push_back({nh.lnf_b, D});
     // the fp16 planes of each block's four weights, as float-sized parts after the rest
-    int exps[kNeckMaxBlocks][3] = {};
+    int exps[kNeckMaxBlocks][7] = {};
     const bool f16 = neck_f16_bounds_ok(nh, exps);
     std::vector<std::vector<uint16_t>> planes;
     if (f16) {
         for (const ppocr_rn_block_t& b : nh.blocks) {
+            const size_t bi = (size_t)(&b - nh.blocks.data());
             planes.push_back(neck_half_planes(b.qkv_w, D, 3 * D));
             planes.push_back(neck_half_planes(b.proj_w, D, D));
-            planes.push_back(neck_half_planes(b.fc1_w, D, H));
-            planes.push_back(neck_half_planes(b.fc2_w, H, D));
+            planes.push_back(neck_mlp_tiles(b, D, H, exps[bi][3], exps[bi][4]));
         }
         for (const auto& pl : planes)
             parts.push_back({reinterpret_cast<const float*>(pl.data()), (int64_t)(pl.size() / 2)});
@@ -1402,11 +1446,14 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
         NeckBlockDev& b = nd.block[i];
         b.qkv_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
         b.proj_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
-        b.fc1_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
-        b.fc2_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
+        b.mlp_h = reinterpret_cast<const uint16_t*>(dev_ptr[q++]);
         b.attn_eq = exps[i][0];
         b.attn_ek = exps[i][1];
         b.attn_ev = exps[i][2];
+        b.mlp_e1 = exps[i][3];
+        b.mlp_e2 = exps[i][4];
+        b.mlp_ey = exps[i][5];
+        b.mlp_eh = exps[i][6];
     }
     *out = h.release();
     return PPOCR_OK;

@@ -20,6 +20,7 @@
 //   neck_cf_rows_kernel  a line's channels-first [D][T] block to token rows;
 //   neck_final_kernel  the last LayerNorm plus the shortcut.
 #include <algorithm>
+#include <cmath>
 
 #include "kernels.hpp"
 #include "neck.hpp"
@@ -379,6 +380,264 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
     }
     gemm_epilogue<SWISH, RES, 4>(acc, (int64_t)blockIdx.x * kGemmRows + wave * 32, h, n0 + 4 * i, m, n, bias, res,
                                  out);
+}
+
+// ---------------------------------------------------------------- MLP
+// x = x + fc2(swish(fc1(LN2(x)))) for 128 token rows per workgroup, the hidden layer never
+// leaving registers (fp16 halves, as neck_gemm16_kernel).  fc1 runs transposed, hidden
+// units as MFMA rows and token rows as columns: lane (i, h) then holds, for its token row i,
+// the units 8 (r / 4) + 4 h + r % 4 (r < 16) of each tile of 32 units, which are exactly the
+// eight contraction values a lane of fc2's A operand supplies per MFMA step once fc2's
+// contraction index runs in the order K' = 32 T + 16 q + 8 h + e <-> unit 32 T + 16 q +
+// 8 (e / 4) + 4 h + e % 4 (fc2's weight planes are stored in that order).  So each tile of
+// 32 hidden units is bias + swish + split in registers and consumed by fc2 at once.
+// Eight waves: waves g and g + 4 share the 32 rows of row group g, the first taking unit
+// tiles 0-3, the second 4-7 (two waves per SIMD, so one's vector work overlaps the other's
+// MFMAs); at the end the second adds its fc2 sums to the first's through LDS.  Weights stream
+// through a 2-slot LDS ring, each slot holding unit tiles j and j + 4 (NeckBlockDev::mlp_h:
+// fc1's rows of a tile as [plane][k chunk][unit], 16 KB, then fc2's matching contraction
+// block as [plane][chunk][output column], 16 KB, laid out in memory as in LDS, so each load
+// instruction reads 1 KB in one piece); the 32 lanes of a half-wave read 32 consecutive
+// chunks.
+// Operands are scaled by powers of two before their splits (sy, sh; the weight planes hold
+// scaled weights) so that the low halves stay above fp16's subnormals, which these MFMAs
+// do not all keep; s1, s2 undo the scaling of the products exactly.
+// The swish here uses the hardware exp2 and reciprocal (a few ulp from the correctly
+// rounded sigmoid, far below the tail's parity bar).
+constexpr int kMlpRows = 128;
+constexpr int kMlpTiles = 8;  // tiles of 32 hidden units (240 padded to 256)
+constexpr int kMlpTile = 32768;  // bytes of one staged unit tile (fc1 16 KB, fc2 16 KB)
+constexpr int kMlpCols = 128;    // fc2's output columns, padded
+static_assert(kNeckHidden <= 32 * kMlpTiles && kNeckDim <= kMlpCols && kNeckDim <= 128, "MLP geometry");
+// the ring (2 slots of 2 tiles), then the constants: LN2's weight and bias, fc1's bias,
+// fc2's bias (each padded to whole 16-byte chunks; padding never reaches an output)
+constexpr int kMlpConstChunks = 192;
+constexpr size_t mlp16_lds_bytes() { return (size_t)4 * kMlpTile + kMlpConstChunks * 16; }
+
+__device__ __forceinline__ float swish_fast(float z) { return z * __builtin_amdgcn_rcpf(1.0f + __expf(-z)); }
+
+__global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int64_t m,
+                                                          const uint16_t* __restrict__ wt,
+                                                          const float* __restrict__ b1,
+                                                          const float* __restrict__ ln_w,
+                                                          const float* __restrict__ ln_b, float eps,
+                                                          const float* __restrict__ b2, float sy, float s1, float sh,
+                                                          float s2, float* out) {
+    constexpr int D = kNeckDim, H = kNeckHidden, S = 8;  // fc1: k = 120 in 8 steps of 16
+    extern __shared__ __align__(16) uint8_t lm[];
+    // constants: chunks 0-29 LN2 weight, 30-59 LN2 bias, 60-123 fc1 bias, 124-155 fc2 bias
+    const float* lnw = reinterpret_cast<const float*>(lm + 4 * kMlpTile);
+    const float* lnb = lnw + D;
+    const float* b1s = lnw + 2 * D;
+    const float* b2s = b1s + 32 * kMlpTiles;
+    static_assert(D % 4 == 0 && H % 4 == 0 && 2 * D + 32 * kMlpTiles + kMlpCols <= 4 * kMlpConstChunks, "chunks");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
+    const int grp = wave & 3, half = wave >> 2;  // row group; unit tiles 4 half .. 4 half + 3
+    const int64_t rbase = (int64_t)blockIdx.x * kMlpRows + grp * 32;
+    const int64_t row = rbase + i;
+
+    // this lane's chunks of its row: k = 16 s + 8 h .. + 7 (zeros past D), every load issued
+    // before any is used
+    float av[S][8];
+    {
+        const int64_t rr = row < m ? row : 0;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int k0 = 16 * s + 8 * h;
+            const f32x4* src = reinterpret_cast<const f32x4*>(x + rr * D + (k0 < D ? k0 : 0));
+            const f32x4 v0 = src[0], v1 = src[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                av[s][e] = k0 < D ? v0[e] : 0.0f;
+                av[s][4 + e] = k0 < D ? v1[e] : 0.0f;
+            }
+        }
+    }
+    if (wave < 3) {
+        const int c = 64 * wave + lane;
+        const float* src = c < 30 ? ln_w + 4 * c
+                           : c < 60 ? ln_b + 4 * (c - 30)
+                           : c < 60 + H / 4 ? b1 + 4 * (c - 60)
+                           : c >= 124 && c < 124 + D / 4 ? b2 + 4 * (c - 124)
+                                                          : b2;  // padding: any finite values
+        if (c < 156)
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(lm + 4 * kMlpTile + 1024 * wave)),
+                16, 0, 0);
+    }
+    // unit tiles j and j + 4 into ring slot j % 2: two contiguous 32 KB tiles of wt, 8
+    // instructions of 1 KB per wave
+    auto stage = [&](int j) {
+#pragma unroll
+        for (int x8 = 0; x8 < 8; ++x8) {
+            const int xi = wave + 8 * x8;  // instruction 0..63: tile j (0..31), tile j + 4 (32..63)
+            const int T = j + 4 * (xi >> 5), xt = xi & 31;
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(wt) + (size_t)T * kMlpTile + 1024 * xt + 16 * lane;
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(lm + (j & 1) * 2 * kMlpTile + 1024 * xi)),
+                16, 0, 0);
+        }
+    };
+    // the workgroup's rows of x (128 x 480 bytes, contiguous) into ring slot 0, whole 16-byte
+    // chunks of the rows inside the batch: up to 60 instructions of 1 KB, at most 8 per wave
+    auto stage_rows = [&] {
+        const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
+        const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(x + r0 * D);
+#pragma unroll
+        for (int x8 = 0; x8 < 8; ++x8) {
+            const int xi = wave + 8 * x8;
+            if (xi < kMlpRows * D * 4 / 1024 && 1024 * xi + 16 * lane < nb)
+                __builtin_amdgcn_global_load_lds(
+                    static_cast<const void*>(src + 1024 * xi + 16 * lane),
+                    reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(lm + 1024 * xi)),
+                    16, 0, 0);
+        }
+    };
+    stage(0);
+    stage(1);
+    // LN2 of the row: its two halves meet in xor-32 shuffles
+    float sm = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm += av[s][e];
+    sm += __shfl_xor(sm, 32, 64);
+    const float mean = __fdiv_rn(sm, (float)D);
+    float var = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        if (16 * s + 8 * h < D) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = av[s][e] - mean;
+                var = fmaf(d, d, var);
+            }
+        }
+    }
+    var += __shfl_xor(var, 32, 64);
+    const float inv = inv_std_of(__fdiv_rn(var, (float)D), eps);
+    __builtin_amdgcn_s_waitcnt(0x8 | (0x7 << 4) | (0xF << 8));  // vmcnt(8): all but slot 1's loads
+    __syncthreads();                                              // slot 0 and the constants are in LDS
+    // fc1's B operand: the normalised row times sy, fp16 halves
+    u16x8 xh[S], xl[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int k0 = 16 * s + 8 * h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float y = k0 < D ? fmaf((av[s][e] - mean) * inv, lnw[k0 + e], lnb[k0 + e]) * sy : 0.0f;
+            const _Float16 yh = (_Float16)y;
+            xh[s][e] = __builtin_bit_cast(unsigned short, yh);
+            xl[s][e] = __builtin_bit_cast(unsigned short, (_Float16)(y - (float)yh));
+        }
+    }
+    f32x16 acc2[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc2[t] = f32x16{};
+    for (int j = 0; j < kMlpTiles / 2; ++j) {
+        const int T = j + 4 * half;
+        const uint8_t* w1 = lm + (j & 1) * 2 * kMlpTile + half * kMlpTile;
+        const uint8_t* w2 = w1 + 16384;
+        // fc1, transposed: units 32 T + i (A, from LDS) x the row (B)
+        f32x16 a1 = f32x16{};
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int c = 2 * s + h;
+            const u16x8 wh = *reinterpret_cast<const u16x8*>(w1 + ((size_t)c * 32 + i) * 16);
+            const u16x8 wl = *reinterpret_cast<const u16x8*>(w1 + ((size_t)(16 + c) * 32 + i) * 16);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh), __builtin_bit_cast(f16x8, xh[s]),
+                                                        a1, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh), __builtin_bit_cast(f16x8, xl[s]),
+                                                        a1, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wl), __builtin_bit_cast(f16x8, xh[s]),
+                                                        a1, 0, 0, 0);
+        }
+        // bias, swish and the split: r = 8 q + e is fc2's contraction value e of step 2 T + q
+        u16x8 hh[2], hl[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int r = 8 * q + e;
+                const int u = 32 * T + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float v = u < H ? swish_fast(a1[r] * s1 + b1s[u]) * sh : 0.0f;
+                const _Float16 vh = (_Float16)v;
+                hh[q][e] = __builtin_bit_cast(unsigned short, vh);
+                hl[q][e] = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)vh));
+            }
+        }
+        // fc2, transposed: output columns 32 t + i (A, from LDS) x the row's hidden values (B)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = 2 * q + h;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const u16x8 bh = *reinterpret_cast<const u16x8*>(w2 + ((size_t)c * kMlpCols + 32 * t + i) * 16);
+                const u16x8 bl = *reinterpret_cast<const u16x8*>(w2 + ((size_t)(4 + c) * kMlpCols + 32 * t + i) * 16);
+                acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bh),
+                                                                 __builtin_bit_cast(f16x8, hh[q]), acc2[t], 0, 0, 0);
+                acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bl),
+                                                                 __builtin_bit_cast(f16x8, hh[q]), acc2[t], 0, 0, 0);
+                acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bh),
+                                                                 __builtin_bit_cast(f16x8, hl[q]), acc2[t], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // every wave is done with slot j % 2
+        if (j + 2 < kMlpTiles / 2) {
+            stage(j + 2);
+            __builtin_amdgcn_s_waitcnt(0x8 | (0x7 << 4) | (0xF << 8));  // vmcnt(8): slot j + 1 has landed
+        } else if (j + 2 == kMlpTiles / 2) {
+            // slot 0 takes the workgroup's rows of x, the residual, while the last tiles run
+            // (their number of loads varies by wave, so slot 1 is waited for first)
+            __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0): slot 1 has landed
+            stage_rows();
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0): the rows have landed
+        }
+        __syncthreads();  // slot (j + 1) % 2 is in LDS (after the last tiles: the rows of x)
+    }
+    // lane (i, h) holds fc2 of row rbase + i at columns 32 t + 8 v + 4 h + 0..3 (acc2[t][4 v ..]).
+    // The second wave of each row group hands its sums to the first through slot 1 ([group]
+    // [t][v][lane] float4s, 16 KB per group), which adds the bias and the residual into the
+    // rows of x in slot 0; then the workgroup stores those rows in one contiguous piece.
+    f32x4* red = reinterpret_cast<f32x4*>(lm + 2 * kMlpTile) + grp * (16 * 64) + lane;
+    if (half == 1) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                red[(4 * t + v) * 64] = f32x4{acc2[t][4 * v], acc2[t][4 * v + 1], acc2[t][4 * v + 2], acc2[t][4 * v + 3]};
+    }
+    __syncthreads();
+    if (half == 0) {
+        float* xr = reinterpret_cast<float*>(lm) + (grp * 32 + i) * D;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int col = 32 * t + 8 * v + 4 * h;
+                if (col < D) {
+                    const f32x4 o = red[(4 * t + v) * 64];
+                    f32x4 xv = *reinterpret_cast<const f32x4*>(xr + col);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xv[e] = xv[e] + ((acc2[t][4 * v + e] + o[e]) * s2 + b2s[col + e]);
+                    *reinterpret_cast<f32x4*>(xr + col) = xv;
+                }
+            }
+    }
+    __syncthreads();
+    {
+        const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
+        const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);  // bytes of the block's rows
+        uint8_t* dst = reinterpret_cast<uint8_t*>(out + r0 * D);
+        for (int b0 = 16 * tid; b0 < nb; b0 += 16 * 512)
+            *reinterpret_cast<f32x4*>(dst + b0) = *reinterpret_cast<const f32x4*>(lm + b0);
+    }
 }
 
 // ---------------------------------------------------------------- attention
@@ -868,17 +1127,24 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
                            : gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr,
                                                                    0.0f, xr, x, st))
             return e;
+        if (nk.f16) {
+            // x = x + fc2(swish(fc1(LN2(x)))) in one pass
+            const int64_t gx = (m + kMlpRows - 1) / kMlpRows;
+            if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
+            neck_mlp16_kernel<<<(unsigned)gx, 512, mlp16_lds_bytes(), st>>>(
+                x, m, k.mlp_h, k.fc1_b, k.ln2_w, k.ln2_b, k.ln2_eps, k.fc2_b, std::ldexp(1.0f, k.mlp_ey),
+                std::ldexp(1.0f, -(k.mlp_e1 + k.mlp_ey)), std::ldexp(1.0f, k.mlp_eh), std::ldexp(1.0f, -(k.mlp_eh + k.mlp_e2)),
+                x);
+            PPOCR_HIP(hipGetLastError());
+            continue;
+        }
         // LN2 -> fc1 -> swish
-        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, true, false>(x, m, k.fc1_h, H, k.fc1_b, k.ln2_w, k.ln2_b,
-                                                                   k.ln2_eps, nullptr, hid, st)
-                           : gemm_go<kNeckDim, true, true, false>(x, m, k.fc1_w, H, k.fc1_b, k.ln2_w, k.ln2_b,
-                                                                  k.ln2_eps, nullptr, hid, st))
+        if (int e = gemm_go<kNeckDim, true, true, false>(x, m, k.fc1_w, H, k.fc1_b, k.ln2_w, k.ln2_b, k.ln2_eps,
+                                                         nullptr, hid, st))
             return e;
         // x = x + fc2(hid)
-        if (int e = nk.f16 ? gemm16_go<kNeckHidden, false, false, true>(hid, m, k.fc2_h, D, k.fc2_b, nullptr, nullptr,
-                                                                       0.0f, x, x, st)
-                           : gemm_go<kNeckHidden, false, false, true>(hid, m, k.fc2_w, D, k.fc2_b, nullptr, nullptr,
-                                                                      0.0f, x, x, st))
+        if (int e = gemm_go<kNeckHidden, false, false, true>(hid, m, k.fc2_w, D, k.fc2_b, nullptr, nullptr, 0.0f, x,
+                                                             x, st))
             return e;
     }
     neck_final_kernel<<<(unsigned)((m + 3) / 4), 256, 0, st>>>(x, m, D, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);

@@ -21,14 +21,23 @@ struct NeckBlockDev {
     const float *ln2_w, *ln2_b;
     float ln2_eps;
     const float *fc1_w, *fc1_b, *fc2_w, *fc2_b;
-    // fp16 planes of each W^T, [2][N][kp] (the nearest half of each weight, then the nearest
-    // half of what it leaves; k padded with zeros to kp = 128 for K <= 128, else 256), used
-    // when NeckDev::f16 is set
-    const uint16_t *qkv_h, *proj_h, *fc1_h, *fc2_h;
+    // fp16 planes of qkv's and proj's W^T, [2][N][kp] (the nearest half of each weight, then
+    // the nearest half of what it leaves; k padded with zeros to kp = 128), used when
+    // NeckDev::f16 is set
+    const uint16_t *qkv_h, *proj_h;
+    // fc1's and fc2's fp16 planes as the fused MLP kernel stages them: 8 tiles of 32 hidden
+    // units, 32 KB each, tile T = fc1's planes of units 32 T .. 32 T + 31 as [plane][k chunk
+    // of 8][unit] then fc2's planes of the matching contraction block as [plane][chunk]
+    // [output column (128)], 8 halves per entry, zeros past the hidden units and columns
+    const uint16_t* mlp_h;
     // the attention's operands scaled by powers of two before the fp16 split (q * scale by
     // 2^attn_eq, k by 2^attn_ek, v by 2^attn_ev), chosen from their bounds so that the halves
     // of all but negligible values stay above fp16's subnormals
     int attn_eq, attn_ek, attn_ev;
+    // the fused MLP's operands scaled the same way: fc1's and fc2's weight planes hold the
+    // weights times 2^mlp_e1 and 2^mlp_e2, the kernel scales LN2's output by 2^mlp_ey and
+    // the hidden layer by 2^mlp_eh before their splits, and each product by the inverse
+    int mlp_e1, mlp_e2, mlp_ey, mlp_eh;
 };
 
 struct NeckDev {
