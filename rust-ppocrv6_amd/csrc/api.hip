@@ -1219,6 +1219,8 @@ struct ppocr_rn {
     size_t device_bytes = 0;
 };
 
+// the neck's host helpers have C++ linkage (some return C++ types)
+extern "C++" {
 namespace {
 
 void free_neck(ppocr_rn* h) {
@@ -1252,6 +1254,13 @@ std::vector<uint16_t> neck_half_planes(const float* w, int64_t K, int64_t N) {
             out[(size_t)((N + c) * kp + k)] = __builtin_bit_cast(uint16_t, lo);
         }
     return out;
+}
+
+// Column of the padded qkv row (or attention row) that holds column c of the model's:
+// part c / D (q, k, v), head (c % D) / 15, value c % 15 -> 128 part + 16 head + value.
+int64_t neck_pad_col(int64_t c) {
+    const int64_t part = c / kNeckDim, r = c % kNeckDim;
+    return 128 * part + 16 * (r / kNeckHeadDim) + r % kNeckHeadDim;
 }
 
 // fc1's and fc2's weights in the fused MLP kernel's staging order (NeckBlockDev::mlp_h),
@@ -1380,15 +1389,28 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
     int exps[kNeckMaxBlocks][7] = {};
     const bool f16 = neck_f16_bounds_ok(nh, exps);
     std::vector<std::vector<uint16_t>> planes;
+    std::vector<std::vector<float>> padded_bias;
     if (f16) {
         for (const ppocr_rn_block_t& b : nh.blocks) {
             const size_t bi = (size_t)(&b - nh.blocks.data());
-            planes.push_back(neck_half_planes(b.qkv_w, D, 3 * D));
-            planes.push_back(neck_half_planes(b.proj_w, D, D));
+            // qkv's columns and proj's rows padded per head to 16 (zeros at d = 15)
+            std::vector<float> qp((size_t)D * kNeckQkvPad, 0.0f), pp((size_t)kNeckAttPad * D, 0.0f);
+            for (int64_t k = 0; k < D; ++k)
+                for (int64_t c = 0; c < 3 * D; ++c)
+                    qp[(size_t)(k * kNeckQkvPad + neck_pad_col(c))] = b.qkv_w[k * 3 * D + c];
+            for (int64_t k = 0; k < D; ++k) std::memcpy(&pp[(size_t)(neck_pad_col(k) * D)], b.proj_w + k * D, (size_t)D * 4);
+            planes.push_back(neck_half_planes(qp.data(), D, kNeckQkvPad));
+            planes.push_back(neck_half_planes(pp.data(), kNeckAttPad, D));
             planes.push_back(neck_mlp_tiles(b, D, H, exps[bi][3], exps[bi][4]));
         }
         for (const auto& pl : planes)
             parts.push_back({reinterpret_cast<const float*>(pl.data()), (int64_t)(pl.size() / 2)});
+        for (const ppocr_rn_block_t& b : nh.blocks) {
+            std::vector<float> bp(kNeckQkvPad, 0.0f);
+            for (int64_t c = 0; c < 3 * D; ++c) bp[(size_t)neck_pad_col(c)] = b.qkv_b[c];
+            padded_bias.push_back(std::move(bp));
+        }
+        for (const auto& bp : padded_bias) parts.push_back({bp.data(), (int64_t)bp.size()});
     }
     int64_t total = 0;
     for (const auto& pt : parts) total += (pt.second + 3) / 4 * 4;  // each part 16-byte aligned
@@ -1455,6 +1477,7 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
         b.mlp_ey = exps[i][5];
         b.mlp_eh = exps[i][6];
     }
+    for (size_t i = 0; f16 && i < nh.blocks.size(); ++i) nd.block[i].qkv_bp = dev_ptr[q++];
     *out = h.release();
     return PPOCR_OK;
 }
@@ -1465,6 +1488,7 @@ int check_neck(const ppocr_rn_t* h) {
 }
 
 }  // namespace
+}  // extern "C++"
 
 int ppocr_rn_create(const ppocr_rn_block_t* blocks, int nblocks, const float* lnf_w, const float* lnf_b,
                     float lnf_eps, int64_t dim, int64_t heads, int64_t hidden, float scale, int device,

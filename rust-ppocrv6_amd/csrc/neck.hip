@@ -833,11 +833,13 @@ __device__ __forceinline__ void split_half(float x, _Float16& hi, _Float16& lo) 
     lo = (_Float16)(x - (float)hi);
 }
 
+// qkv rows [m][kNeckQkvPad] (q, k, v of head h at 128 part + 16 h), output rows
+// [m][kNeckAttPad] (head h at 16 h; the padding value 15 of each head is written as 0).
 template <int HD>
 __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restrict__ qkv, int64_t m,
                                                           const int64_t* __restrict__ line_off, int64_t lines,
-                                                          int64_t line_len, int dim, float scale, int eq, int ek,
-                                                          int ev, float* __restrict__ o) {
+                                                          int64_t line_len, float scale, int eq, int ek, int ev,
+                                                          float* __restrict__ o) {
     // powers of two: exact scalings of the operands before the split, undone on the scores
     // and the output
     const float qmul = ldexpf(1.0f, eq), kmul = ldexpf(1.0f, ek), vmul = ldexpf(1.0f, ev);
@@ -853,9 +855,10 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
     if (t1 - t0 <= 0) return;
     const int T = (int)(t1 - t0);  // the launcher bounds m by INT32_MAX
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
-    const int64_t stride = 3 * (int64_t)dim;
-    const float* base = qkv + t0 * stride + h * HD;  // the line's first row, this head
-    const int sd = tid & 15, st0 = tid >> 4;  // staging: dim tid % 16 of rows tid / 16 + 16 x
+    static_assert(HD < 16 && kNeckQkvPad == 3 * 128, "padded heads");
+    constexpr int64_t stride = kNeckQkvPad;
+    const float* base = qkv + t0 * stride + 16 * h;  // the line's first row, this head
+    const int sd = 4 * (tid & 3), st0 = tid >> 2;  // staging: values sd .. sd + 3 of rows tid / 4 + 64 x
     for (int qpass = 0; qpass < T; qpass += 4 * 16 * QB) {
         // this wave's query blocks: queries qpass + 16 (wave + 4 x) + c, dims 4 g .. + 3
         f16x4 qh[QB], ql[QB];
@@ -864,13 +867,9 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
 #pragma unroll
         for (int x = 0; x < QB; ++x) {
             const int q = qpass + 16 * (wave + 4 * x) + c;
-            const float* row = base + (int64_t)q * stride;
-            float qv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int d = 4 * g + e;
-                qv[e] = (q < T && d < HD) ? row[d] : 0.0f;
-            }
+            // values 4 g .. 4 g + 3 of the query (the padding value is 0)
+            const f32x4 qv = q < T ? *reinterpret_cast<const f32x4*>(base + (int64_t)q * stride + 4 * g)
+                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 _Float16 hi, lo;
@@ -884,25 +883,34 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
         }
         for (int kb = 0; kb < T; kb += kAttnKeys) {
             const int rem = T - kb;  // keys of the line from this block on
-            // stage keys kb .. kb + 127 (zeros past the line's end and past the head's dims),
+            // stage keys kb .. kb + 127 (zeros past the line's end; the padding value is 0),
             // every load issued before the first LDS store
-            float kv[KT], vv[KT];
+            static_assert(kAttnKeys == 128, "two rows of 64 per thread");
+            f32x4 kv[2], vv[2];
 #pragma unroll
-            for (int x = 0; x < KT; ++x) {
-                const int t = st0 + 16 * x;
-                kv[x] = vv[x] = 0.0f;
-                if (t < rem && sd < HD) {
-                    const float* row = base + (int64_t)(kb + t) * stride + sd;
-                    kv[x] = row[dim];
-                    vv[x] = row[2 * dim];
-                }
+            for (int x = 0; x < 2; ++x) {
+                const int t = st0 + 64 * x;
+                const float* row = base + (int64_t)(kb + (t < rem ? t : 0)) * stride + sd;
+                const f32x4 k4 = *reinterpret_cast<const f32x4*>(row + 128);
+                const f32x4 v4 = *reinterpret_cast<const f32x4*>(row + 256);
+                kv[x] = t < rem ? k4 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                vv[x] = t < rem ? v4 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
             __syncthreads();  // the previous block's readers are done
 #pragma unroll
-            for (int x = 0; x < KT; ++x) {
-                const int tl = st0 + 16 * x;
-                split_half(kv[x] * kmul, ks[0][tl * kKhStride + sd], ks[1][tl * kKhStride + sd]);
-                split_half(vv[x] * vmul, vt[0][sd * kVtStride + tl], vt[1][sd * kVtStride + tl]);
+            for (int x = 0; x < 2; ++x) {
+                const int tl = st0 + 64 * x;
+                f16x4 kh, kl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    _Float16 hi, lo;
+                    split_half(kv[x][e] * kmul, hi, lo);
+                    kh[e] = hi;
+                    kl[e] = lo;
+                    split_half(vv[x][e] * vmul, vt[0][(sd + e) * kVtStride + tl], vt[1][(sd + e) * kVtStride + tl]);
+                }
+                *reinterpret_cast<f16x4*>(&ks[0][tl * kKhStride + sd]) = kh;
+                *reinterpret_cast<f16x4*>(&ks[1][tl * kKhStride + sd]) = kl;
             }
             __syncthreads();
 #pragma unroll
@@ -978,10 +986,10 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
             l += __shfl_xor(l, 16, 64);
             l += __shfl_xor(l, 32, 64);
             if (q < T) {
-                float* orow = o + (t0 + q) * (int64_t)dim + h * HD;
+                f32x4 ov;
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-                    if (4 * g + jj < HD) orow[4 * g + jj] = __fdiv_rn(oa[x][jj] * vdiv, l);
+                for (int jj = 0; jj < 4; ++jj) ov[jj] = __fdiv_rn(oa[x][jj] * vdiv, l);
+                *reinterpret_cast<f32x4*>(o + (t0 + q) * (int64_t)kNeckAttPad + 16 * h + 4 * g) = ov;
             }
         }
     }
@@ -1083,9 +1091,9 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
     if (lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many lines");
     float* x = ws;                       // residual stream [m][D]
     float* sc = x + m * D;               // shortcut rows [m][D]
-    float* qkv = sc + m * D;             // [m][3D]
-    float* att = qkv + m * 3 * D;        // [m][D]
-    float* hid = att + m * D;            // [m][H]
+    float* qkv = sc + m * D;             // [m][3D], or [m][kNeckQkvPad] on fp16 halves
+    float* att = qkv + m * kNeckQkvPad;  // [m][D], or [m][kNeckAttPad]
+    float* hid = att + m * kNeckAttPad;  // [m][H]
     const float* scr = shortcut_in;
     if (layout == PPOCR_NECK_CHANNELS_FIRST) {
         const dim3 grid((unsigned)((m + 31) / 32), (unsigned)((D + 31) / 32));
@@ -1109,21 +1117,21 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         const NeckBlockDev& k = nk.block[b];
         const float* xr = b == 0 ? xin : x;
         // LN1 -> qkv
-        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, false, false>(xr, m, k.qkv_h, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b,
-                                                                    k.ln1_eps, nullptr, qkv, st)
+        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, false, false>(xr, m, k.qkv_h, kNeckQkvPad, k.qkv_bp, k.ln1_w,
+                                                                    k.ln1_b, k.ln1_eps, nullptr, qkv, st)
                            : gemm_go<kNeckDim, true, false, false>(xr, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b,
                                                                    k.ln1_eps, nullptr, qkv, st))
             return e;
         const dim3 ag((unsigned)lines, (unsigned)nk.heads);
         if (nk.f16)
-            neck_attn16_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale,
+            neck_attn16_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, nk.scale,
                                                                 k.attn_eq, k.attn_ek, k.attn_ev, att);
         else
             neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
         PPOCR_HIP(hipGetLastError());
         // x = x + proj(att)
-        if (int e = nk.f16 ? gemm16_go<kNeckDim, false, false, true>(att, m, k.proj_h, D, k.proj_b, nullptr, nullptr,
-                                                                    0.0f, xr, x, st)
+        if (int e = nk.f16 ? gemm16_go<kNeckAttPad, false, false, true>(att, m, k.proj_h, D, k.proj_b, nullptr, nullptr,
+                                                                       0.0f, xr, x, st)
                            : gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr,
                                                                    0.0f, xr, x, st))
             return e;

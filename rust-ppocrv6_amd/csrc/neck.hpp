@@ -24,7 +24,11 @@ struct NeckBlockDev {
     // fp16 planes of qkv's and proj's W^T, [2][N][kp] (the nearest half of each weight, then
     // the nearest half of what it leaves; k padded with zeros to kp = 128), used when
     // NeckDev::f16 is set
+    // qkv's columns padded per head to 16 (q, k, v of head h at 128 part + 16 h + d, zero
+    // weights and bias at d = 15) and proj's rows alike (kNeckQkvPad, kNeckAttPad): with
+    // fp16 halves the attention reads and writes whole 16-byte vectors
     const uint16_t *qkv_h, *proj_h;
+    const float* qkv_bp;  // qkv's bias in the padded column order
     // fc1's and fc2's fp16 planes as the fused MLP kernel stages them: 8 tiles of 32 hidden
     // units, 32 KB each, tile T = fc1's planes of units 32 T .. 32 T + 31 as [plane][k chunk
     // of 8][unit] then fc2's planes of the matching contraction block as [plane][chunk]
@@ -54,9 +58,15 @@ struct NeckDev {
 // k of a weight's fp16 planes, padded: 128 for K <= 128, else 256.
 constexpr int neck_f16_kp(int k) { return k <= 128 ? 128 : 256; }
 
+// Row widths of qkv and of the attention output when each head's 15 values are padded to
+// 16 (the fp16-halves path).
+constexpr int kNeckQkvPad = 3 * 128, kNeckAttPad = 128;
+static_assert(kNeckDim == 8 * kNeckHeadDim && kNeckHeadDim < 16, "eight heads of at most 16 values");
+
 // Floats of workspace per token row: the residual stream and the shortcut rows (D each),
-// qkv (3D), the attention output (D) and the MLP hidden layer (H).
-constexpr int64_t kNeckWsFloatsPerRow = 6 * kNeckDim + kNeckHidden;
+// qkv (3D, or kNeckQkvPad), the attention output (D, or kNeckAttPad) and the MLP hidden
+// layer (H).
+constexpr int64_t kNeckWsFloatsPerRow = 2 * kNeckDim + kNeckQkvPad + kNeckAttPad + kNeckHidden;
 
 // The whole tail on token rows: x_in and shortcut_in in `layout` (PPOCR_NECK_ROWS: [m][D];
 // PPOCR_NECK_CHANNELS_FIRST: line b as [D][T_b] at D * (first row of b)), lines given by
