@@ -37,6 +37,32 @@ __device__ __forceinline__ float inv_std_of(float var, float eps) { return __fdi
 // reference's Sigmoid and Mul nodes round it.
 __device__ __forceinline__ float swish_of(float x) { return x * __fdiv_rn(1.0f, 1.0f + expf(-x)); }
 
+// The final LayerNorm of one row by a quad of lanes (lane % 4 = q holds the row's values
+// 30 q .. 30 q + 29 in v): sums in a fixed order, each lane's values in turn and then the
+// quad's partial sums in two xor shuffles, so the fused and the separate kernel give the
+// same bits.  v becomes the normalised values.
+constexpr int kLnQuad = kNeckDim / 4;
+__device__ __forceinline__ void final_ln_quad(float (&v)[kLnQuad], const float* lnw_q, const float* lnb_q,
+                                              float eps) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kLnQuad; ++e) s += v[e];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    const float mean = __fdiv_rn(s, (float)kNeckDim);
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kLnQuad; ++e) {
+        v[e] -= mean;
+        t = fmaf(v[e], v[e], t);
+    }
+    t += __shfl_xor(t, 1, 64);
+    t += __shfl_xor(t, 2, 64);
+    const float inv = inv_std_of(__fdiv_rn(t, (float)kNeckDim), eps);
+#pragma unroll
+    for (int e = 0; e < kLnQuad; ++e) v[e] = fmaf(v[e] * inv, lnw_q[e], lnb_q[e]);
+}
+
 // Line of token row r: the last line whose (clamped) start is at most r, by binary search
 // over the device offsets; -1 when r lies in no line.  t0, t1: that line's rows.
 __device__ __forceinline__ int64_t line_of_row(const int64_t* line_off, int64_t lines, int64_t line_len, int64_t m,
@@ -410,27 +436,37 @@ constexpr int kMlpTile = 32768;  // bytes of one staged unit tile (fc1 16 KB, fc
 constexpr int kMlpCols = 128;    // fc2's output columns, padded
 static_assert(kNeckHidden <= 32 * kMlpTiles && kNeckDim <= kMlpCols && kNeckDim <= 128, "MLP geometry");
 // the ring (2 slots of 2 tiles), then the constants: LN2's weight and bias, fc1's bias,
-// fc2's bias (each padded to whole 16-byte chunks; padding never reaches an output)
-constexpr int kMlpConstChunks = 192;
+// fc2's bias (each padded to whole 16-byte chunks; padding never reaches an output), the
+// final LayerNorm's weight and bias
+constexpr int kMlpConstChunks = 256;
 constexpr size_t mlp16_lds_bytes() { return (size_t)4 * kMlpTile + kMlpConstChunks * 16; }
 
 __device__ __forceinline__ float swish_fast(float z) { return z * __builtin_amdgcn_rcpf(1.0f + __expf(-z)); }
 
+// FINAL (the last block): the rows are then taken through the final LayerNorm and the
+// shortcut Add (neck_final_kernel's arithmetic) before the store, into fin_out.
+template <bool FINAL>
 __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int64_t m,
                                                           const uint16_t* __restrict__ wt,
                                                           const float* __restrict__ b1,
                                                           const float* __restrict__ ln_w,
                                                           const float* __restrict__ ln_b, float eps,
                                                           const float* __restrict__ b2, float sy, float s1, float sh,
-                                                          float s2, float* out) {
+                                                          float s2, float* out, const float* __restrict__ lnf_w,
+                                                          const float* __restrict__ lnf_b, float lnf_eps,
+                                                          const float* __restrict__ shortcut,
+                                                          float* __restrict__ fin_out) {
     constexpr int D = kNeckDim, H = kNeckHidden, S = 8;  // fc1: k = 120 in 8 steps of 16
     extern __shared__ __align__(16) uint8_t lm[];
-    // constants: chunks 0-29 LN2 weight, 30-59 LN2 bias, 60-123 fc1 bias, 124-155 fc2 bias
+    // constants: chunks 0-29 LN2 weight, 30-59 LN2 bias, 60-123 fc1 bias, 124-155 fc2 bias,
+    // 156-185 the final LayerNorm's weight, 186-215 its bias
     const float* lnw = reinterpret_cast<const float*>(lm + 4 * kMlpTile);
     const float* lnb = lnw + D;
     const float* b1s = lnw + 2 * D;
     const float* b2s = b1s + 32 * kMlpTiles;
-    static_assert(D % 4 == 0 && H % 4 == 0 && 2 * D + 32 * kMlpTiles + kMlpCols <= 4 * kMlpConstChunks, "chunks");
+    const float* lfw = b2s + kMlpCols;
+    const float* lfb = lfw + D;
+    static_assert(D % 4 == 0 && H % 4 == 0 && 4 * D + 32 * kMlpTiles + kMlpCols <= 4 * kMlpConstChunks, "chunks");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
     const int grp = wave & 3, half = wave >> 2;  // row group; unit tiles 4 half .. 4 half + 3
     const int64_t rbase = (int64_t)blockIdx.x * kMlpRows + grp * 32;
@@ -453,14 +489,16 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
             }
         }
     }
-    if (wave < 3) {
+    if (wave < (FINAL ? 4 : 3)) {
         const int c = 64 * wave + lane;
         const float* src = c < 30 ? ln_w + 4 * c
                            : c < 60 ? ln_b + 4 * (c - 30)
                            : c < 60 + H / 4 ? b1 + 4 * (c - 60)
                            : c >= 124 && c < 124 + D / 4 ? b2 + 4 * (c - 124)
-                                                          : b2;  // padding: any finite values
-        if (c < 156)
+                           : c >= 156 && c < 186 ? lnf_w + 4 * (c - 156)
+                           : c >= 186 && c < 216 ? lnf_b + 4 * (c - 186)
+                                                  : b2;  // padding: any finite values
+        if (c < (FINAL ? 216 : 156))
             __builtin_amdgcn_global_load_lds(
                 static_cast<const void*>(src),
                 reinterpret_cast<__attribute__((address_space(3))) void*>(
@@ -605,6 +643,17 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
     // The second wave of each row group hands its sums to the first through slot 1 ([group]
     // [t][v][lane] float4s, 16 KB per group), which adds the bias and the residual into the
     // rows of x in slot 0; then the workgroup stores those rows in one contiguous piece.
+    const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
+    const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);  // bytes of the block's rows
+    f32x4 scv[8];  // FINAL: the shortcut rows, loaded while the sums are exchanged
+    if constexpr (FINAL) {
+        const uint8_t* sc = reinterpret_cast<const uint8_t*>(shortcut + r0 * D);
+#pragma unroll
+        for (int k8 = 0; k8 < 8; ++k8) {
+            const int b0 = 16 * tid + 8192 * k8;
+            scv[k8] = b0 < nb ? *reinterpret_cast<const f32x4*>(sc + b0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
     f32x4* red = reinterpret_cast<f32x4*>(lm + 2 * kMlpTile) + grp * (16 * 64) + lane;
     if (half == 1) {
 #pragma unroll
@@ -631,9 +680,31 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
             }
     }
     __syncthreads();
-    {
-        const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
-        const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);  // bytes of the block's rows
+    if constexpr (FINAL) {
+        // the final LayerNorm of each row in place, a quad of lanes per row
+        {
+            float* xr = reinterpret_cast<float*>(lm) + (tid >> 2) * D + kLnQuad * (tid & 3);
+            float v[kLnQuad];
+#pragma unroll
+            for (int e = 0; e < kLnQuad; e += 2) {
+                const f32x2 p = *reinterpret_cast<const f32x2*>(xr + e);
+                v[e] = p[0];
+                v[e + 1] = p[1];
+            }
+            final_ln_quad(v, lfw + kLnQuad * (tid & 3), lfb + kLnQuad * (tid & 3), lnf_eps);
+#pragma unroll
+            for (int e = 0; e < kLnQuad; e += 2) *reinterpret_cast<f32x2*>(xr + e) = f32x2{v[e], v[e + 1]};
+        }
+        __syncthreads();
+        // out = the normalised rows + the shortcut rows (loaded before the reduction), both
+        // contiguous
+        uint8_t* dst = reinterpret_cast<uint8_t*>(fin_out + r0 * D);
+#pragma unroll
+        for (int k8 = 0; k8 < 8; ++k8) {
+            const int b0 = 16 * tid + 8192 * k8;
+            if (b0 < nb) *reinterpret_cast<f32x4*>(dst + b0) = *reinterpret_cast<const f32x4*>(lm + b0) + scv[k8];
+        }
+    } else {
         uint8_t* dst = reinterpret_cast<uint8_t*>(out + r0 * D);
         for (int b0 = 16 * tid; b0 < nb; b0 += 16 * 512)
             *reinterpret_cast<f32x4*>(dst + b0) = *reinterpret_cast<const f32x4*>(lm + b0);
@@ -1027,23 +1098,32 @@ __global__ __launch_bounds__(256) void neck_cf_rows_kernel(const float* __restri
 }
 
 // out[r] = LayerNorm(x[r]) + shortcut[r]: one wave per row, D <= 128 (two channels a lane).
-__global__ __launch_bounds__(256) void neck_final_kernel(const float* __restrict__ x, int64_t m, int dim,
+__global__ __launch_bounds__(256) void neck_final_kernel(const float* __restrict__ x, int64_t m,
                                                          const float* __restrict__ ln_w,
                                                          const float* __restrict__ ln_b, float eps,
                                                          const float* __restrict__ shortcut,
                                                          float* __restrict__ out) {
-    const int lane = threadIdx.x & 63;
-    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // a quad of lanes per row (whole quads leave together, so the shuffles stay within rows);
+    // x is the 16-byte aligned workspace
+    const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 2;
+    const int q = threadIdx.x & 3;
     if (r >= m) return;
-    const int c0 = 2 * lane, c1 = 2 * lane + 1;
-    const float v0 = c0 < dim ? x[r * dim + c0] : 0.0f;
-    const float v1 = c1 < dim ? x[r * dim + c1] : 0.0f;
-    const float mean = __fdiv_rn(wave_sum(v0 + v1), (float)dim);
-    const float d0 = c0 < dim ? v0 - mean : 0.0f, d1 = c1 < dim ? v1 - mean : 0.0f;
-    const float var = __fdiv_rn(wave_sum(fmaf(d0, d0, d1 * d1)), (float)dim);
-    const float inv = inv_std_of(var, eps);
-    if (c0 < dim) out[r * dim + c0] = fmaf(d0 * inv, ln_w[c0], ln_b[c0]) + shortcut[r * dim + c0];
-    if (c1 < dim) out[r * dim + c1] = fmaf(d1 * inv, ln_w[c1], ln_b[c1]) + shortcut[r * dim + c1];
+    static_assert(kLnQuad % 2 == 0, "float2 accesses (rows of 480 bytes, quarters of 120)");
+    const float* xr = x + r * kNeckDim + kLnQuad * q;
+    float v[kLnQuad];
+#pragma unroll
+    for (int e = 0; e < kLnQuad; e += 2) {
+        const f32x2 p = *reinterpret_cast<const f32x2*>(xr + e);
+        v[e] = p[0];
+        v[e + 1] = p[1];
+    }
+    final_ln_quad(v, ln_w + kLnQuad * q, ln_b + kLnQuad * q, eps);
+    // the shortcut rows and out may be only 4-byte aligned here (the fused path takes the
+    // 16-byte aligned ones)
+    const float* sr = shortcut + r * kNeckDim + kLnQuad * q;
+    float* orow = out + r * kNeckDim + kLnQuad * q;
+#pragma unroll
+    for (int e = 0; e < kLnQuad; ++e) orow[e] = v[e] + sr[e];
 }
 
 template <int K, bool LN, bool SWISH, bool RES>
@@ -1113,6 +1193,10 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         else
             xin = x_in;
     }
+    // the fused MLP kernel of the last block finishes the tail itself when the shortcut rows
+    // and out are 16-byte aligned
+    const bool fused_final =
+        ((reinterpret_cast<uintptr_t>(scr) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     for (int b = 0; b < nk.blocks; ++b) {
         const NeckBlockDev& k = nk.block[b];
         const float* xr = b == 0 ? xin : x;
@@ -1139,11 +1223,16 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
             // x = x + fc2(swish(fc1(LN2(x)))) in one pass
             const int64_t gx = (m + kMlpRows - 1) / kMlpRows;
             if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
-            neck_mlp16_kernel<<<(unsigned)gx, 512, mlp16_lds_bytes(), st>>>(
+            // the last block also applies the final LayerNorm and the shortcut (the rows are 16-byte
+            // aligned: the workspace, the shortcut rows and out, checked below)
+            const bool fin = b + 1 == nk.blocks && fused_final;
+            auto* kern = fin ? neck_mlp16_kernel<true> : neck_mlp16_kernel<false>;
+            kern<<<(unsigned)gx, 512, mlp16_lds_bytes(), st>>>(
                 x, m, k.mlp_h, k.fc1_b, k.ln2_w, k.ln2_b, k.ln2_eps, k.fc2_b, std::ldexp(1.0f, k.mlp_ey),
                 std::ldexp(1.0f, -(k.mlp_e1 + k.mlp_ey)), std::ldexp(1.0f, k.mlp_eh), std::ldexp(1.0f, -(k.mlp_eh + k.mlp_e2)),
-                x);
+                x, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);
             PPOCR_HIP(hipGetLastError());
+            if (fin) return PPOCR_OK;
             continue;
         }
         // LN2 -> fc1 -> swish
@@ -1155,7 +1244,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
                                                              x, st))
             return e;
     }
-    neck_final_kernel<<<(unsigned)((m + 3) / 4), 256, 0, st>>>(x, m, D, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);
+    neck_final_kernel<<<(unsigned)((m + 63) / 64), 256, 0, st>>>(x, m, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

@@ -139,6 +139,34 @@ def test_neck_from_a_model_file_and_the_device_entry(rh, tmp_path):
     b.close()
 
 
+def test_neck_final_layernorm_with_unaligned_rows(rh):
+    """The last block's fused kernel finishes the tail (final LayerNorm + shortcut) when the
+    shortcut rows and the output are 16-byte aligned; otherwise a separate kernel does, with
+    the same arithmetic: the same bits either way (rows 4 bytes off alignment)."""
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    w = neck_weights(seed=23)
+    neck = _make(rh, w)
+    x, sc, off = _inputs([120, 61, 3], seed=17)
+    m = int(off[-1])
+    want = neck.forward(x, sc, off)
+    L = rh._lib.lib()
+    dx, doff = DeviceArray.from_numpy(x), DeviceArray.from_numpy(off)
+    dsc = DeviceArray.from_numpy(np.concatenate([[0.0], sc.reshape(-1)]).astype(np.float32))
+    dout = DeviceArray((m * DIM + 1,), np.float32)
+    wsb = neck.workspace_bytes(m)
+    dws = DeviceArray((wsb,), np.uint8)
+    import ctypes
+    off4 = lambda d: ctypes.c_void_p(d.p.value + 4)  # noqa: E731
+    rh._check(L.ppocr_rn_forward_dev(neck.handle, dx.p, off4(dsc), m, doff.p, 3, rh.NECK_ROWS, off4(dout), dws.p, wsb,
+                                     None))
+    synchronize()
+    got = dout.numpy()[1:].reshape(m, DIM)
+    assert np.array_equal(got, want)
+    for d in (dx, doff, dsc, dout, dws):
+        d.free()
+    neck.close()
+
+
 def test_neck_then_head_against_the_oracle(orc, rh):
     """The tail feeding the head (PP-OCRv6_small_rec from the flatten output to the CTC
     sequences): argmax and sequences equal to the oracle's tail feeding the oracle's head
