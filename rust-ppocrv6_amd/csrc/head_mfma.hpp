@@ -716,8 +716,8 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             // re-reference, the barrier (after which tile j+2 is in LDS).  Past the end the
             // MFMAs read a stale ring slot and the load repeats the last tile: harmless, and it
             // keeps the body branch-free.
-            auto step = [&](int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
-                const unsigned rel = (unsigned)(j - t0);
+            auto step = [&]<int R>(int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
+                constexpr unsigned rel = (unsigned)R;  // (j - t0) % kRing
                 stage_direct<GE::REC, NT>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
                                       lds + ((rel + kRing - 1) & (kRing - 1)) * GE::BUF, tid);
                 const uint8_t* bufn = lds + ((rel + 1) & (kRing - 1)) * GE::BUF;
@@ -774,11 +774,18 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                 ring_barrier<kOps>();
             };
             int j = t0;
-            for (; j + 1 < t1; j += 2) {
-                step(j, acc_a, acc_b);
-                step(j + 1, acc_b, acc_a);
+            // unrolled by the ring's size, so every ring slot offset is a constant (immediate
+            // LDS offsets, no address arithmetic per tile)
+            static_assert(kRing == 4, "the unrolled loop walks four slots");
+            for (; j + 3 < t1; j += 4) {
+                step.template operator()<0>(j, acc_a, acc_b);
+                step.template operator()<1>(j + 1, acc_b, acc_a);
+                step.template operator()<2>(j + 2, acc_a, acc_b);
+                step.template operator()<3>(j + 3, acc_b, acc_a);
             }
-            if (j < t1) step(j, acc_a, acc_b);
+            if (j < t1) step.template operator()<0>(j, acc_a, acc_b);
+            if (j + 1 < t1) step.template operator()<1>(j + 1, acc_b, acc_a);
+            if (j + 2 < t1) step.template operator()<2>(j + 2, acc_a, acc_b);
             // the ring's last loads (repeats of the last tile) land before the workgroup ends
             __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
         }
