@@ -10,10 +10,11 @@ namespace ppocr {
 
 bool mfma_supports_groups(int G) { return G == 15 || G == 10; }
 
-// Grid of row blocks x vocabulary chunks (the kernels map block ids so that workgroup id
-// mod 8, the XCD it lands on, selects the chunk).
-static int grid_blocks(int mblocks, int nsplit) {
+// Grid of row blocks x vocabulary chunks, laid out as map_block<rows_on_one_xcd> reads it
+// (workgroup id mod 8 is the XCD a workgroup lands on).
+static int grid_blocks(int mblocks, int nsplit, bool rows_on_one_xcd) {
     if (nsplit >= 8) return mblocks * nsplit;
+    if (rows_on_one_xcd) return ((mblocks + 7) / 8) * nsplit * 8;
     const int r8 = 8 / nsplit;
     return ((mblocks + r8 - 1) / r8) * 8;
 }
@@ -44,8 +45,9 @@ int stats_rows_per_block_mfma(int cfg, int64_t m) { return 32 * kStatsWaves * ma
 // that fit on the 256 CUs of an MI355X at once), and a workgroup costs a fixed start and
 // finish (its rows' activations, the pipeline fill, the partials) worth about `fixed`
 // tiles of the main loop.  The chunk count from 4 to 64 minimising rounds x (fixed + tiles
-// per chunk) is taken.  At least 4 chunks keep each XCD's slice of the weight records (the
-// chunks of workgroup id mod 8) within its L2.  Most kernels run 2 workgroups per CU with
+// per chunk) is taken.  From 8 chunks up each XCD keeps its slice of the weight records (the
+// chunks of workgroup id mod 8) in its L2; with 4, an XCD takes all chunks of its row blocks,
+// and its workgroups walk the chunks' tiles in step.  Most kernels run 2 workgroups per CU with
 // a fixed cost of 8 tiles (measured: 30720 rows run 5% faster in 4 chunks of 147 tiles,
 // one round, than in 8 chunks of 74, two rounds).  The two-term modes' one-block-per-wave
 // kernel (small batches: 128-row workgroups, 51 KB of LDS, 148 VGPRs) runs 3 per CU, fixed
@@ -160,7 +162,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
     const int nsplit = rows_nsplit(mblocks);
     const int tpc = (tg.tiles + nsplit - 1) / nsplit;
-    const int64_t grid = grid_blocks((int)mblocks, nsplit);
+    const int64_t grid = grid_blocks((int)mblocks, nsplit, false);
     if (grid > 0x7fffffff) return fail(PPOCR_ERR_INVALID_ARG, "MatMulQuantizedB: m too large");
     const int vec = vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
@@ -203,7 +205,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
                                  nullptr, nullptr, nullptr, 0, *guard, st);
     // rescue: the flagged rows again, three bf16 activation terms, every column
     const int slots = (int)std::min<int64_t>(mblocks, kRescueSlots);
-    const int rgrid = grid_blocks(slots, nsplit);
+    const int rgrid = grid_blocks(slots, nsplit, false);
     x.rec = rec_rescue;
     x.mblocks = slots;
     x.lim = none;
@@ -244,7 +246,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
     const int64_t mblocks = (m + rpb - 1) / rpb;
     if (mblocks > (1 << 24)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
     const int tpc = (tg.tiles + nsplit - 1) / nsplit;
-    const int grid = grid_blocks((int)mblocks, nsplit);
+    const int grid = grid_blocks((int)mblocks, nsplit, true);
     const int vec = line_len > 0 ? -(int)line_len : vec_ok(a, k);
     const int rcfg = rescue_cfg(cfg);
     // No reset launch: the list is emptied by its epoch (first use) and by the merge below.
@@ -281,7 +283,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
         // (with exact class indices)
         const int rrpb = stats_rows_per_block_mfma(rcfg, m);
         const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, kRescueSlots);
-        const int rgrid = grid_blocks(slots, nsplit);
+        const int rgrid = grid_blocks(slots, nsplit, true);
         x.rec = rec_rescue;
         x.mblocks = slots;
         x.lim = GuardLimits{0.0f, 0.0f, 0.0f};
