@@ -300,7 +300,8 @@ typedef struct {
 } ppocr_rn_block_t;
 
 /* The neck's weights resident in HBM (Model keeps them in its weight map,
- * src/engine/loader.rs:34-92).  scale: the attention's Mul constant. */
+ * src/engine/loader.rs:34-92).  scale: the attention's Mul constant (finite; otherwise
+ * PPOCR_ERR_INVALID_ARG). */
 int ppocr_rn_create(const ppocr_rn_block_t* blocks, int nblocks, const float* lnf_w, const float* lnf_b,
                     float lnf_eps, int64_t dim, int64_t heads, int64_t hidden, float scale, int device,
                     ppocr_rn_t** out);
@@ -320,8 +321,10 @@ int ppocr_rn_gemm_halves(const ppocr_rn_t* h);
 size_t ppocr_rn_workspace_bytes(const ppocr_rn_t* h, int64_t m);
 /* out [m][dim] token rows = the tail applied to x and shortcut (both in `layout`), lines
  * by d_line_off[0..lines] (read on the device, clamped into [0, m]; attention never mixes
- * tokens of different lines).  d_workspace: ppocr_rn_workspace_bytes(h, m) bytes, 16-byte
- * aligned, or NULL (stream-ordered scratch). */
+ * tokens of different lines).  Rows of [0, m) that no line covers (offsets that leave gaps
+ * or end before m) have no attention output, and their rows of out are undefined.
+ * d_workspace: ppocr_rn_workspace_bytes(h, m) bytes, 16-byte aligned, or NULL
+ * (stream-ordered scratch). */
 int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_shortcut, int64_t m,
                          const int64_t* d_line_off, int64_t lines, int layout, float* d_out, void* d_workspace,
                          size_t workspace_bytes, void* stream);

@@ -1343,10 +1343,13 @@ bool neck_f16_bounds_ok(const NeckHost& nh, int (*exps)[7]) {
         const double hs = y2 * col_l1(b.fc1_w, D, H, 0, H) + amax(b.fc1_b, H);               // fc2's input
         const double wmax = std::max(std::max(amax(b.qkv_w, D * 3 * D), amax(b.proj_w, D * D)),
                                      std::max(amax(b.fc1_w, D * H), amax(b.fc2_w, H * D)));
-        if (!(y1 <= kLimit && y2 <= kLimit && qk <= kLimit && v <= kLimit && hs <= kLimit && wmax <= kLimit))
+        // q is split into fp16 halves after its scaling, so q * |scale| is held to the limit too
+        const double qs = qk * (double)std::fabs(nh.scale);
+        if (!(y1 <= kLimit && y2 <= kLimit && qk <= kLimit && qs <= kLimit && v <= kLimit && hs <= kLimit &&
+              wmax <= kLimit))
             return false;
         const size_t i = (size_t)(&b - nh.blocks.data());
-        exps[i][0] = neck_f16_exponent(qk * (double)std::fabs(nh.scale));  // q * scale
+        exps[i][0] = neck_f16_exponent(qs);                                // q * scale
         exps[i][1] = neck_f16_exponent(qk);                                // k
         exps[i][2] = neck_f16_exponent(v);                                 // v
         exps[i][3] = neck_f16_exponent(amax(b.fc1_w, D * H));              // fc1's weights
@@ -1367,7 +1370,7 @@ int neck_create(const NeckHost& nh, int device, ppocr_rn_t** out) {
                                                std::to_string(nh.hidden) + " (built for 120, 8 x 15, 240)");
     if (nh.blocks.empty() || nh.blocks.size() > (size_t)kNeckMaxBlocks)
         return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": 1 to " + std::to_string(kNeckMaxBlocks) + " blocks");
-    if (!nh.lnf_w || !nh.lnf_b || !(nh.scale == nh.scale) || !(nh.lnf_eps >= 0.0f))
+    if (!nh.lnf_w || !nh.lnf_b || !std::isfinite(nh.scale) || !(nh.lnf_eps >= 0.0f))
         return fail(PPOCR_ERR_INVALID_ARG, std::string(op) + ": null final LayerNorm or bad constants");
     const int64_t D = nh.dim, H = nh.hidden;
     // per block: ln1 w,b (D each), qkv (D*3D + 3D), proj (D*D + D), ln2 (2D), fc1 (D*H + H), fc2 (H*D + D)

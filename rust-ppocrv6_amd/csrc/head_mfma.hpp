@@ -709,8 +709,10 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             bt[b] = -1;
         }
 
+        // the loads of the kRing - 3 newest staged tiles may still be in flight at a barrier
+        constexpr int kLead = (kRing - 3) * kOps;
         if (t0 < t1) {
-            ring_barrier<kOps>();  // tiles t0 and t0+1 are in LDS
+            ring_barrier<kLead>();  // tiles t0 and t0+1 are in LDS
             f32x16 acc_a[MB], acc_b[MB];
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
@@ -780,21 +782,24 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                 }
 #pragma unroll
                 for (int b = 0; b < MB; ++b) sum[b] += st.tsum[b];
-                ring_barrier<kOps>();
+                ring_barrier<kLead>();
+            };
+            // step R of the ring: the accumulator sets alternate (kRing is even)
+            auto step_of = [&]<int R>(int jj) {
+                if constexpr (R % 2 == 0) step.template operator()<R>(jj, acc_a, acc_b);
+                else step.template operator()<R>(jj, acc_b, acc_a);
             };
             int j = t0;
             // unrolled by the ring's size, so every ring slot offset is a constant (immediate
             // LDS offsets, no address arithmetic per tile)
-            static_assert(kRing == 4, "the unrolled loop walks four slots");
-            for (; j + 3 < t1; j += 4) {
-                step.template operator()<0>(j, acc_a, acc_b);
-                step.template operator()<1>(j + 1, acc_b, acc_a);
-                step.template operator()<2>(j + 2, acc_a, acc_b);
-                step.template operator()<3>(j + 3, acc_b, acc_a);
-            }
-            if (j < t1) step.template operator()<0>(j, acc_a, acc_b);
-            if (j + 1 < t1) step.template operator()<1>(j + 1, acc_b, acc_a);
-            if (j + 2 < t1) step.template operator()<2>(j + 2, acc_a, acc_b);
+            static_assert(kRing >= 4 && (kRing & (kRing - 1)) == 0, "the ring is a power of two, at least 4");
+            for (; j + kRing - 1 < t1; j += kRing)
+                [&]<int... R>(std::integer_sequence<int, R...>) {
+                    (step_of.template operator()<R>(j + R), ...);
+                }(std::make_integer_sequence<int, kRing>{});
+            [&]<int... R>(std::integer_sequence<int, R...>) {
+                ((j + R < t1 ? step_of.template operator()<R>(j + R) : void()), ...);
+            }(std::make_integer_sequence<int, kRing - 1>{});
             // the ring's last loads (repeats of the last tile) land before the workgroup ends
             __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
         }

@@ -14,6 +14,7 @@
 // tiny one).  Graph validity checks are those of Model::load (src/engine/model.rs:40-66).
 #include "model_graph.hpp"
 
+#include <cmath>
 #include <cstring>
 #include <map>
 
@@ -297,6 +298,149 @@ int find_rec_neck(const StFile& f, RecNeckNames* out) {
         return true;
     };
 
+    // The attention at p, from the qkv Reshape's output r up to the next MatMul with a weight,
+    // node by node, each input checked against what the steps before it produced:
+    //   Transpose(r) perm [2,0,3,1,4]; q, k and v as parts 0, 1 and 2 of its first axis
+    //   (Slice [i, i+1) on axis 0 then Squeeze axis 0, or Gather index i on axis 0);
+    //   Mul(q, scalar) (optionally Reshape'd to Shape(q)); Transpose(k) perm [0,1,3,2];
+    //   MatMul(q * scale, k^T); Softmax over the last axis; MatMul(p, v);
+    //   Transpose perm [0,2,1,3]; Reshape [0,-1,D].
+    // Any other node in the span (a mask or bias Add, another scaling, another Softmax
+    // axis, operands wired otherwise) refuses the graph: the kernels compute exactly
+    // softmax(q * scale * k^T) v per head.  Advances p to the projection MatMul.
+    std::string att_why;
+    auto i64s = [&](const std::string& s, std::vector<int64_t>* v) {
+        const StTensor* t = weight(s);
+        if (!t || t->dtype != "I64" || t->bytes % 8 != 0) return false;
+        v->resize(t->bytes / 8);
+        std::memcpy(v->data(), t->data, t->bytes);
+        return true;
+    };
+    auto int_attr = [&](const GNode* n, const char* key, int64_t dflt, int64_t* v) {
+        const JVal* a = n->attrs ? n->attrs->get(key) : nullptr;
+        if (!a) {
+            *v = dflt;
+            return true;
+        }
+        if (!a->is_int) return false;
+        *v = a->i;
+        return true;
+    };
+    auto axes_attr_is0 = [&](const GNode* n) {
+        const JVal* a = n->attrs ? n->attrs->get("axes") : nullptr;
+        if (a) return a->kind == JVal::kArr && a->arr.size() == 1 && a->arr[0].is_int && a->arr[0].i == 0;
+        std::vector<int64_t> v;  // opset 13: axes as a second input
+        return n->in.size() == 2 && i64s(n->in[1], &v) && v.size() == 1 && v[0] == 0;
+    };
+    auto attention = [&](const std::string& r, int64_t D, float* scale, std::string* att) {
+        enum Role { kR, kT, kSlice0, kSlice1, kSlice2, kQ, kK, kV, kQs, kShapeQ, kKt, kS, kP, kO, kOt, kAtt };
+        std::map<std::string, int> role;
+        role[R(r)] = kR;
+        bool have[kAtt + 1] = {};
+        auto role_of = [&](const std::string& x) {
+            auto it = role.find(R(x));
+            return it == role.end() ? -1 : it->second;
+        };
+        auto give = [&](const GNode* n, int rl) {
+            if (have[rl]) return false;  // each value of the pattern is made once
+            have[rl] = true;
+            role[n->out[0]] = rl;
+            return true;
+        };
+        auto fail_at = [&](const GNode* n, const char* why) {
+            att_why = std::string(why) + " at node '" + n->name + "' (" + n->op + ")";
+            return false;
+        };
+        for (; p < ord.size(); ++p) {
+            const GNode* n = ord[p];
+            if (n->op == "MatMul" && n->in.size() == 2 && weight(n->in[1])) break;
+            const int r0 = role_of(n->in[0]);
+            if (n->op == "Transpose") {
+                if (n->in.size() != 1) return fail_at(n, "Transpose inputs");
+                if (r0 == kR && perm_is(n, {2, 0, 3, 1, 4})) {
+                    if (!give(n, kT)) return fail_at(n, "second q/k/v Transpose");
+                } else if (r0 == kK && perm_is(n, {0, 1, 3, 2})) {
+                    if (!give(n, kKt)) return fail_at(n, "second k Transpose");
+                } else if (r0 == kO && perm_is(n, {0, 2, 1, 3})) {
+                    if (!give(n, kOt)) return fail_at(n, "second output Transpose");
+                } else {
+                    return fail_at(n, "unexpected Transpose");
+                }
+            } else if (n->op == "Slice") {
+                // Slice(data, starts, ends[, axes[, steps]]): [i, i+1) on axis 0
+                std::vector<int64_t> st, en, ax{0}, sp{1};
+                if (r0 != kT || n->in.size() < 3 || n->in.size() > 5 || !i64s(n->in[1], &st) || !i64s(n->in[2], &en) ||
+                    (n->in.size() > 3 && !i64s(n->in[3], &ax)) || (n->in.size() > 4 && !i64s(n->in[4], &sp)))
+                    return fail_at(n, "Slice of q, k, v");
+                if (st.size() != 1 || en.size() != 1 || ax.size() != 1 || sp.size() != 1 || ax[0] != 0 ||
+                    sp[0] != 1 || st[0] < 0 || st[0] > 2 || en[0] != st[0] + 1)
+                    return fail_at(n, "Slice other than one part of axis 0");
+                if (!give(n, kSlice0 + (int)st[0])) return fail_at(n, "part sliced twice");
+            } else if (n->op == "Squeeze") {
+                if (r0 < kSlice0 || r0 > kSlice2 || !axes_attr_is0(n)) return fail_at(n, "Squeeze of a q, k, v part");
+                if (!give(n, kQ + (r0 - kSlice0))) return fail_at(n, "part squeezed twice");
+            } else if (n->op == "Gather") {
+                std::vector<int64_t> ix;
+                int64_t axis = 0;
+                if (r0 != kT || n->in.size() != 2 || !i64s(n->in[1], &ix) || ix.size() != 1 || ix[0] < 0 ||
+                    ix[0] > 2 || !int_attr(n, "axis", 0, &axis) || axis != 0)
+                    return fail_at(n, "Gather other than one part of axis 0");
+                if (!give(n, kQ + (int)ix[0])) return fail_at(n, "part gathered twice");
+            } else if (n->op == "Mul") {
+                float v = 0.0f;
+                if (n->in.size() != 2) return fail_at(n, "Mul inputs");
+                const int r1 = role_of(n->in[1]);
+                const bool ok = (r0 == kQ && r1 < 0 && scalar(n->in[1], &v)) || (r1 == kQ && r0 < 0 && scalar(n->in[0], &v));
+                if (!ok) return fail_at(n, "Mul other than q by a scalar constant");
+                if (!std::isfinite(v)) return fail_at(n, "non-finite attention scale");
+                if (!give(n, kQs)) return fail_at(n, "second scaling of q");
+                *scale = v;
+            } else if (n->op == "Shape") {
+                if (r0 != kQ || n->in.size() != 1) return fail_at(n, "Shape other than q's");
+                if (!give(n, kShapeQ)) return fail_at(n, "second Shape");
+            } else if (n->op == "Reshape") {
+                if (n->in.size() != 2) return fail_at(n, "Reshape inputs");
+                std::vector<int64_t> shape;
+                if (r0 == kQs && role_of(n->in[1]) == kShapeQ) {
+                    role[n->out[0]] = kQs;  // q * scale back to q's own shape
+                } else if (r0 == kOt && i64s(n->in[1], &shape) && shape.size() == 3 && shape[0] == 0 &&
+                           shape[1] == -1 && shape[2] == D) {
+                    if (!give(n, kAtt)) return fail_at(n, "second output Reshape");
+                } else {
+                    return fail_at(n, "unexpected Reshape");
+                }
+            } else if (n->op == "MatMul") {
+                if (n->in.size() != 2) return fail_at(n, "MatMul inputs");
+                const int r1 = role_of(n->in[1]);
+                if (r0 == kQs && r1 == kKt) {
+                    if (!give(n, kS)) return fail_at(n, "second score MatMul");
+                } else if (r0 == kP && r1 == kV) {
+                    if (!give(n, kO)) return fail_at(n, "second value MatMul");
+                } else {
+                    return fail_at(n, "MatMul other than (q * scale) k^T or p v");
+                }
+            } else if (n->op == "Softmax") {
+                int64_t axis = -1;
+                if (r0 != kS || n->in.size() != 1 || !int_attr(n, "axis", -1, &axis) || (axis != -1 && axis != 3))
+                    return fail_at(n, "Softmax other than over the keys of the scores");
+                if (!give(n, kP)) return fail_at(n, "second Softmax");
+            } else {
+                return fail_at(n, "node outside the attention pattern");
+            }
+        }
+        if (p >= ord.size()) {
+            att_why = "no projection MatMul after it";
+            return false;
+        }
+        if (!have[kAtt]) {
+            att_why = "the pattern is incomplete";
+            return false;
+        }
+        for (const auto& kv : role)
+            if (kv.second == kAtt) *att = kv.first;
+        return true;
+    };
+
     Ln ln;
     while (p < ord.size() && !layer_norm(p, &ln)) ++p;
     if (p >= ord.size()) return bad("no LayerNorm sub-graph");
@@ -327,37 +471,24 @@ int find_rec_neck(const StFile& f, RecNeckNames* out) {
         bk.ln1_w = R(ln.w);
         bk.ln1_b = R(ln.b);
         bk.ln1_eps = ln.eps;
-        if (!at("Reshape") || R(ord[p]->in[0]) != qkv || ord[p]->in.size() != 2) return bad("qkv Reshape");
+        if (!at("Reshape") || ord[p]->in.size() != 2 || R(ord[p]->in[0]) != qkv) return bad("qkv Reshape");
         const StTensor* shp = weight(ord[p]->in[1]);
         if (!shp || shp->dtype != "I64" || shp->bytes != 40) return bad("qkv Reshape shape");
         int64_t sv[5];
         std::memcpy(sv, shp->data, 40);
-        if (sv[2] != 3 || sv[3] <= 0 || sv[4] <= 0 || sv[3] * sv[4] != D) return bad("qkv Reshape [0,-1,3,H,D/H]");
+        if (sv[0] != 0 || sv[1] != -1 || sv[2] != 3 || sv[3] <= 0 || sv[4] <= 0 || sv[3] * sv[4] != D)
+            return bad("qkv Reshape [0,-1,3,H,D/H]");
         if (out->heads && out->heads != sv[3]) return bad("blocks with different head counts");
         out->heads = sv[3];
+        const std::string rsh = ord[p]->out[0];
         ++p;
-        // the attention, up to the next MatMul with a weight
-        int softmax = 0, act_mm = 0;
         float scale = 0.0f;
-        bool have_scale = false;
-        for (; p < ord.size(); ++p) {
-            const GNode* n = ord[p];
-            if (n->op == "MatMul" && n->in.size() == 2 && weight(n->in[1])) break;
-            if (n->op == "MatMul") ++act_mm;
-            if (n->op == "Softmax") ++softmax;
-            if (n->op == "Mul" && n->in.size() == 2) {
-                float v;
-                if (scalar(n->in[1], &v) || scalar(n->in[0], &v)) {
-                    if (have_scale) return bad("two scale constants in one attention");
-                    scale = v;
-                    have_scale = true;
-                }
-            }
-        }
-        if (softmax != 1 || act_mm != 2 || !have_scale) return bad("attention (Mul scale, 2 MatMul, Softmax)");
+        std::string att;
+        if (!attention(rsh, D, &scale, &att)) return bad("attention: " + att_why);
         if (out->scale != 0.0f && out->scale != scale) return bad("blocks with different attention scales");
         out->scale = scale;
-        const std::string att = R(ord[p]->in[0]);
+        if (!at("MatMul") || ord[p]->in.size() != 2 || !weight(ord[p]->in[1]) || R(ord[p]->in[0]) != att)
+            return bad("attention output is not the projection MatMul's input");
         int64_t nd = D;
         std::string proj;
         if (!linear(att, D, &nd, &bk.proj_w, &bk.proj_b, &proj)) return bad("attention projection MatMul [D][D] + Add");
@@ -420,7 +551,7 @@ int find_rec_neck(const StFile& f, RecNeckNames* out) {
     if (!at("Transpose") || R(ord[p]->in[0]) != R(sq) || !perm_is(ord[p], {0, 2, 1})) return bad("Transpose [0,2,1] before the head");
     const std::string t8 = ord[p]->out[0];
     ++p;
-    if (!at("MatMul") || R(ord[p]->in[0]) != R(t8) || R(ord[p]->in[1]) != head.weight)
+    if (!at("MatMul") || ord[p]->in.size() != 2 || R(ord[p]->in[0]) != R(t8) || R(ord[p]->in[1]) != head.weight)
         return bad("the tail does not feed the head's MatMul");
     return PPOCR_OK;
 }

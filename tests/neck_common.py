@@ -64,7 +64,7 @@ def _layer_norm(g, x, w, b, eps, tag):
     return g.node("Identity", [g.node("Add", [mu, g.const(f"{tag}.b", b)])])
 
 
-def svtr_graph(w, head_w=None, head_b=None):
+def svtr_graph(w, head_w=None, head_b=None, variant=None):
     """Nodes and tensors of a recognition graph from the flattened features [B, D, T] and the
     shortcut [B, D, 1, T] (graph inputs) to the head's Softmax, built as PP-OCRv6_small_rec
     lays its tail out: Transpose.0, blocks of LayerNorm sub-graph, MatMul + Add, Reshape
@@ -72,7 +72,14 @@ def svtr_graph(w, head_w=None, head_b=None):
     [0,1,3,2], MatMul, Softmax(axis 3), MatMul, Transpose [0,2,1,3], Reshape [0,-1,D],
     MatMul + Add, residual Add, LayerNorm, MatMul + Add, Sigmoid, Mul, MatMul + Add, residual
     Add; then the final LayerNorm, Reshape [0,1,-1,D] (after its shape arithmetic),
-    Transpose [0,3,1,2], Add(shortcut), Squeeze(axis 2), Transpose [0,2,1] and the head."""
+    Transpose [0,3,1,2], Add(shortcut), Squeeze(axis 2), Transpose [0,2,1] and the head.
+
+    `variant` alters the first block's attention or the node order, for the graph search's
+    refusals: "gather" (q, k, v by Gather instead of Slice + Squeeze; still the pattern),
+    "mask_add" (an Add on the scores), "softmax_queries" (Softmax over axis 2),
+    "k_perm" (k transposed [0,2,1,3]), "k_as_v" (MatMul(p, k)), "scale_twice" (q scaled
+    twice), "head_first" (the head's nodes listed first and the list ending inside the
+    first attention), "one_input_matmul" (a one-input MatMul after the last Transpose)."""
     g = _G()
     x = g.node("Transpose", ["feat"], {"perm": [0, 2, 1]})
     i64 = lambda *v: np.array(v, np.int64)
@@ -82,17 +89,28 @@ def svtr_graph(w, head_w=None, head_b=None):
         qkv = g.node("Add", [g.node("MatMul", [y, g.const(f"{t}.qkv.w", b["qkv_w"])]), g.const(f"{t}.qkv.b", b["qkv_b"])])
         r5 = g.node("Reshape", [qkv, g.const(f"{t}.shape5", i64(0, -1, 3, HEADS, DIM // HEADS))])
         tr = g.node("Transpose", [r5], {"perm": [2, 0, 3, 1, 4]})
+        var = variant if bi == 0 else None
         parts = []
         for j in range(3):
+            if var == "gather":
+                parts.append(g.node("Gather", [tr, g.const(f"{t}.g{j}", np.array(j, np.int64))], {"axis": 0}))
+                continue
             sl = g.node("Slice", [tr, g.const(f"{t}.s{j}", i64(j)), g.const(f"{t}.e{j}", i64(j + 1)),
                                   g.const(f"{t}.a{j}", i64(0)), g.const(f"{t}.p{j}", i64(1))])
             parts.append(g.node("Squeeze", [sl], {"axes": [0]}))
         q = g.node("Mul", [parts[0], g.const(f"{t}.scale", np.array([SCALE], np.float32))])
+        if var == "scale_twice":
+            q = g.node("Mul", [q, g.const(f"{t}.scale2", np.array([2.0], np.float32))])
         q = g.node("Reshape", [q, g.node("Shape", [parts[0]])])
-        kt = g.node("Transpose", [parts[1]], {"perm": [0, 1, 3, 2]})
-        p = g.node("Softmax", [g.node("MatMul", [q, kt])], {"axis": 3})
-        o = g.node("MatMul", [p, parts[2]])
+        kt = g.node("Transpose", [parts[1]], {"perm": [0, 2, 1, 3] if var == "k_perm" else [0, 1, 3, 2]})
+        sc = g.node("MatMul", [q, kt])
+        if var == "mask_add":
+            sc = g.node("Add", [sc, g.const(f"{t}.mask", np.zeros((1,), np.float32))])
+        p = g.node("Softmax", [sc], {"axis": 2 if var == "softmax_queries" else 3})
+        o = g.node("MatMul", [p, parts[1] if var == "k_as_v" else parts[2]])
         o = g.node("Reshape", [g.node("Transpose", [o], {"perm": [0, 2, 1, 3]}), g.const(f"{t}.shape3", i64(0, -1, DIM))])
+        if bi == 0:
+            att_end = len(g.nodes)  # nodes of the graph up to the first attention's output
         pr = g.node("Add", [g.node("MatMul", [o, g.const(f"{t}.proj.w", b["proj_w"])]), g.const(f"{t}.proj.b", b["proj_b"])])
         x = g.node("Add", [x, pr])
         y = _layer_norm(g, x, b["ln2_w"], b["ln2_b"], b["ln2_eps"], f"{t}.ln2")
@@ -106,11 +124,19 @@ def svtr_graph(w, head_w=None, head_b=None):
     z = g.node("Transpose", [g.node("Reshape", [z, shp])], {"perm": [0, 3, 1, 2]})
     z = g.node("Squeeze", [g.node("Add", [z, "shortcut"])], {"axes": [2]})
     z = g.node("Transpose", [z], {"perm": [0, 2, 1]})
+    last_transpose = len(g.nodes) - 1
+    if variant == "one_input_matmul":
+        g.node("MatMul", [z])
     outputs = [z]
     if head_w is not None:
         lg = g.node("Add", [g.node("MatMul", [z, g.const("head.w", head_w)]), g.const("head.b", head_b)])
         outputs = [g.node("Softmax", [lg], {"axis": 2})]
-    return {"inputs": ["feat", "shortcut"], "outputs": outputs, "nodes": g.nodes}, g.tensors
+    nodes = g.nodes
+    if variant == "head_first":
+        # the head (its MatMul, Add, Softmax) and the Transpose feeding it first, then the
+        # graph's first nodes up to the first attention's output: no weighted MatMul follows it
+        nodes = nodes[-3:] + [nodes[last_transpose]] + nodes[:att_end]
+    return {"inputs": ["feat", "shortcut"], "outputs": outputs, "nodes": nodes}, g.tensors
 
 
 def write_model(path, graph, tensors):

@@ -193,6 +193,41 @@ def test_graph_search_finds_the_synthetic_tail(tmp_path):
     assert got["input"] == "feat" and got["shortcut"] == "shortcut"
 
 
+@pytest.mark.parametrize("variant,msg", [
+    ("gather", None),
+    ("mask_add", "node outside the attention pattern"),
+    ("softmax_queries", "Softmax other than over the keys"),
+    ("k_perm", "unexpected Transpose"),
+    ("k_as_v", "MatMul other than (q * scale) k^T or p v"),
+    ("scale_twice", "Mul other than q by a scalar constant"),
+    ("head_first", "no projection MatMul after it"),
+    ("one_input_matmul", "the tail does not feed the head's MatMul"),
+])
+def test_graph_search_refuses_other_attention_structures(tmp_path, variant, msg):
+    """The graph search takes exactly the attention the kernels compute, softmax(q * scale *
+    k^T) v per head, with each node's inputs traced to the q, k and v parts of the qkv
+    Reshape: an Add on the scores, a Softmax over the queries, k transposed otherwise, k
+    used as v or a second scaling refuse the file (PPOCR_ERR_MODEL with the node named).
+    q, k and v taken by Gather is the same computation and is accepted.  The structures of
+    a head listed before the tail (the attention scan then runs to the end of the node list)
+    and a one-input MatMul after the last Transpose are refused without reading past a
+    list; the driver is the AddressSanitizer / UBSan build, so any such read fails it."""
+    w = neck_weights()
+    head_w = np.random.default_rng(5).standard_normal((DIM, 64)).astype(np.float32) * 0.05
+    graph, tensors = svtr_graph(w, head_w, np.zeros(64, np.float32), variant=variant)
+    path = str(tmp_path / f"svtr_{variant}.safetensors")
+    write_model(path, graph, tensors)
+    if msg is None:
+        got = _parse_neck(path)
+        assert (got["heads"], len(got["blocks"])) == (HEADS, 2) and got["scale"] == SCALE
+        return
+    exe = os.path.join(ROOT, "rust-ppocrv6_amd", "lib", "_asan", "parser_check")
+    out = subprocess.run([exe, "--neck", path], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr[-3000:]
+    assert "runtime error" not in out.stderr and "Sanitizer" not in out.stderr, out.stderr[-3000:]
+    assert "necks 0" in out.stdout and msg in out.stdout, out.stdout
+
+
 @pytest.mark.skipif(not os.path.exists(REF_MODEL), reason="the reference's model files are not here")
 def test_graph_search_on_the_real_models():
     got = _parse_neck(REF_MODEL)
