@@ -148,6 +148,14 @@ impl GpuHead {
         self.quantized
     }
 
+    /// Classes (the vocabulary) and the width of an activation row.
+    pub fn n(&self) -> usize {
+        self.n
+    }
+    pub fn k(&self) -> usize {
+        self.k
+    }
+
     /// Model::weight_footprint_bytes' share of this weight (src/engine/model.rs:651-667).
     pub fn footprint_bytes(&self) -> usize {
         unsafe { sys::ppocr_rh_footprint_bytes(self.h) }

@@ -2,9 +2,15 @@
 every function include/ppocr_rechead.h declares is declared in the ppocr-hip-sys crate's
 extern "C" block with the same parameter and return types (C type -> Rust type mapping
 below), nothing else is declared there, and every call the reference-side wrapper makes
-through the crate names a declared function with its number of arguments."""
+through the crate names a declared function with its number of arguments.  The edits of the
+reference's executor and pipeline (reference_patch/patches/*.patch) apply to the reference's
+files, are what make_patches.py writes, and call only wrapper and Model methods that exist,
+with their number of arguments."""
 import os
 import re
+import shutil
+import subprocess
+import sys
 
 import pytest
 
@@ -120,3 +126,85 @@ def test_reference_side_calls_match_the_declarations():
                 assert len(args) == len(decls[name][1]), (f, name, len(args))
                 calls += 1
     assert calls >= 10
+
+
+REF = "/root/reference"
+PATCHES = {"engine_model.patch": "src/engine/model.rs", "pipeline.patch": "src/pipeline.rs"}
+
+
+def _call_args(text, start):
+    """Arguments of the call whose '(' ends at text[start - 1]: split at top-level commas."""
+    depth, i, args, cur = 1, start, [], ""
+    while depth:
+        ch = text[i]
+        if ch in "([{":
+            depth += 1
+        elif ch in ")]}":
+            depth -= 1
+        if depth == 1 and ch == ",":
+            args.append(cur)
+            cur = ""
+        elif depth:
+            cur += ch
+        i += 1
+    if cur.strip():
+        args.append(cur)
+    return [a for a in args if a.strip()]
+
+
+def _rust_fns(text):
+    """pub fn name(params) -> number of parameters other than self."""
+    out = {}
+    for m in re.finditer(r"pub(?:\(crate\))? fn (\w+)\s*(?:<[^>]*>)?\(", text):
+        params = _call_args(text, m.end())
+        out[m.group(1)] = len([p for p in params if not re.match(r"\s*&?\s*(mut\s+)?self\b", p)])
+    return out
+
+
+def _added(patch):
+    return "\n".join(l[1:] for l in open(os.path.join(PATCH, "patches", patch)).read().splitlines()
+                     if l.startswith("+") and not l.startswith("+++"))
+
+
+@pytest.mark.skipif(not os.path.isdir(REF) or not shutil.which("patch"), reason="the reference crate is not here")
+def test_patches_apply_to_the_reference_and_are_current(tmp_path):
+    for patch, rel in PATCHES.items():
+        dst = tmp_path / rel
+        dst.parent.mkdir(parents=True, exist_ok=True)
+        shutil.copy(os.path.join(REF, rel), dst)
+        r = subprocess.run(["patch", "-p1", "--dry-run", "-i", os.path.join(PATCH, "patches", patch)],
+                           cwd=tmp_path, capture_output=True, text=True)
+        assert r.returncode == 0 and "FAILED" not in r.stdout and "fuzz" not in r.stdout, (patch, r.stdout, r.stderr)
+    # regenerate into a scratch copy of the generator's folder: the committed diffs are its output
+    scratch = tmp_path / "gen"
+    shutil.copytree(PATCH, scratch, ignore=shutil.ignore_patterns("patches"))
+    subprocess.run([sys.executable, str(scratch / "make_patches.py"), REF], check=True, capture_output=True)
+    for patch in PATCHES:
+        assert (scratch / "patches" / patch).read_text() == open(os.path.join(PATCH, "patches", patch)).read(), patch
+
+
+def test_patch_calls_name_existing_methods_with_their_arity():
+    head = _rust_fns(open(os.path.join(PATCH, "src", "ops", "gpu_head.rs")).read())
+    ctc = _rust_fns(open(os.path.join(PATCH, "src", "postprocess", "ctc", "gpu.rs")).read())
+    model_added = _added("engine_model.patch")
+    model = _rust_fns(model_added)
+    assert {"attach_gpu_heads", "rec_head", "forward_until"} <= set(model)
+    expect = {
+        # receiver pattern -> the methods it may call, with where they are defined
+        r"\bhead\.(\w+)\(": head,
+        r"GpuHead::(\w+)\(": head,
+        r"self\.ctc_decoder\.(\w+)\(": ctc,
+        r"(?:self\.)?rec_model\.(\w+)\(": model,
+    }
+    seen = 0
+    for patch in PATCHES:
+        text = _added(patch)
+        for pat, defs in expect.items():
+            for m in re.finditer(pat, text):
+                name = m.group(1)
+                if defs is model and name not in model:
+                    continue  # the reference's own Model methods (quantize_matmul_weights, ...)
+                assert name in defs, (patch, name)
+                assert len(_call_args(text, m.end())) == defs[name], (patch, name)
+                seen += 1
+    assert seen >= 8
