@@ -400,8 +400,12 @@ def find_rec_head(path):
     return {"weight": os.fsdecode(wb.value), "bias": bias or None, "n": n.value, "k": k.value}
 
 
-def matmul_quantized_b(a, qw, bias=None, mode=MODE_BF16X2):
-    """matmul_quantized_b(a, qw, bias) (src/ops/matmul.rs:1204-1336) on the GPU."""
+def matmul_quantized_b(a, qw, bias=None, mode=MODE_AUTO):
+    """matmul_quantized_b(a, qw, bias) (src/ops/matmul.rs:1204-1336) on the GPU, in the
+    library's default arithmetic unless `mode` says otherwise.  The head (the packed weight
+    and its tile records in HBM) is built on the first call with a given QuantizedWeight and
+    bias and kept on that QuantizedWeight, as Model keeps its packed weight resident; a
+    QuantizedWeight is not modified after it is built (the reference's is immutable)."""
     a = _f32(a)
     if a.ndim < 1:
         raise OcrError("MatMulQuantizedB", "Operand must have valid dimensions")
@@ -409,15 +413,20 @@ def matmul_quantized_b(a, qw, bias=None, mode=MODE_BF16X2):
         raise OcrError("MatMulQuantizedB", f"Inner dimensions must match: {a.shape[-1]} != {qw.cols}")
     if bias is not None and np.asarray(bias).size != qw.rows:
         raise OcrError("MatMulQuantized", f"bias has {np.asarray(bias).size} elements but n is {qw.rows}")
-    head = RecHead(qw=qw, bias=bias)
-    try:
-        return head.logits(a, mode)
-    finally:
-        head.close()
+    b = None if bias is None else _f32(bias)
+    key = None if b is None else b.tobytes()
+    heads = qw.__dict__.setdefault("_gpu_heads", {})
+    head = heads.get(key)
+    if head is None:
+        head = heads[key] = RecHead(qw=qw, bias=b)
+    return head.logits(a, mode)
 
 
-def matmul_transposed_b(a, b_t, bias=None, mode=MODE_BF16X3):
-    """matmul_transposed_b(a, b_t, bias) (src/ops/matmul.rs:514-897) on the GPU."""
+def matmul_transposed_b(a, b_t, bias=None, mode=MODE_AUTO):
+    """matmul_transposed_b(a, b_t, bias) (src/ops/matmul.rs:514-897) on the GPU, in the
+    library's default arithmetic unless `mode` says otherwise.  The FP32 head is built for
+    the call (b_t is a plain array that may change between calls); for repeated calls with
+    one weight build a RecHead(w_t=...) once, as Model keeps its transposed weight."""
     a = _f32(a)
     b_t = _f32(b_t)
     if a.ndim < 1 or b_t.ndim != 2:

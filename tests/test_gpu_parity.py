@@ -369,17 +369,24 @@ def test_large_batch_logits_and_probs_single_pass(orc, rh, head, rhead):
     assert_close_rel(gotp[sample], refp, "large-batch probs")
 
 
-def test_stress_1024_fused(orc, rh):
-    """m = 245760, zero-weight rows, +-5 outliers, 1% rows x50, 2% near-tie rows."""
+@pytest.mark.parametrize("mode", [None, 2], ids=["auto", "bf16x2"])
+def test_stress_1024_fused(orc, rh, mode):
+    """m = 245760, zero-weight rows, +-5 outliers, 1% rows x50, 2% near-tie rows.  In
+    BF16X2 the +-5 outliers put the precision limit near max|a| = 1.6, so the guard sends
+    nearly every row to the three-term rescue pass: the whole batch goes through the gather
+    kernels."""
     from ppocr_rechead import workloads as wl
-    print("stress_1024 build", flush=True)
+    print(f"stress_1024 build (mode {mode})", flush=True)
     wk = wl.make("stress_1024", pack=orc.pack_int8)
     a, q, s, bias = wk["a"], wk["q"], wk["scales"], wk["bias"]
     head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
-    print("stress_1024 fused argmax", flush=True)
-    got = head.decode(a, wk["line_off"])
-    head.close()
     m = a.shape[0]
+    guarded = head.guarded_rows(a, mode)
+    print(f"stress_1024 fused decode, {int(guarded.sum())} of {m} rows guarded", flush=True)
+    if mode == 2:
+        assert guarded.mean() > 0.9
+    got = head.decode(a, wk["line_off"], mode)
+    head.close()
     assert got["idx"].min() >= 0 and got["idx"].max() < 18710
     assert np.all((got["maxprob"] > 0) & (got["maxprob"] <= 1))
     rng = np.random.default_rng(15)
@@ -686,3 +693,30 @@ def test_probs_consistent_with_the_statistics_pass(orc, rh):
         print(f"  mode {mode}: max|p - 1| = {err:.2e}")
         assert err < 1e-6, (mode, err)
     head.close()
+
+
+def test_free_functions_run_auto_on_a_resident_head(orc, rh, head):
+    """The mirror's operator functions: matmul_quantized_b runs the library's default
+    arithmetic (AUTO) on a head built once per QuantizedWeight and bias (a second call reuses
+    it: same handle, same results) and stays within the bar of the oracle; an explicit mode
+    and another bias get heads of their own; matmul_transposed_b runs AUTO on an FP32 head."""
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((300, 120)).astype(np.float32)
+    qw = rh.QuantizedWeight(head["q"], head["s"])
+    got1 = rh.matmul_quantized_b(a, qw, head["bias"])
+    h1 = qw._gpu_heads[head["bias"].tobytes()].handle.value
+    got2 = rh.matmul_quantized_b(a, qw, head["bias"])
+    assert qw._gpu_heads[head["bias"].tobytes()].handle.value == h1 and np.array_equal(got1, got2)
+    ref = orc.matmul_quantized_b(a, head["q"], head["s"], head["bias"], partition_threads=1)
+    assert np.abs(got1 - ref).max() < TOL
+    auto = qw._gpu_heads[head["bias"].tobytes()].auto_mode()
+    assert np.array_equal(got1, rh.matmul_quantized_b(a, qw, head["bias"], mode=auto))
+    got_nb = rh.matmul_quantized_b(a, qw)
+    assert len(qw._gpu_heads) == 2
+    assert np.abs(got_nb - orc.matmul_quantized_b(a, head["q"], head["s"], None, partition_threads=1)).max() < TOL
+    w_t = (rng.standard_normal((500, 120)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal(500) * 0.01).astype(np.float32)
+    got_f = rh.matmul_transposed_b(a, w_t, b)
+    assert np.abs(got_f - orc.matmul_transposed_b(a, w_t, b, partition_threads=1)).max() < TOL
+    for hd in qw._gpu_heads.values():
+        hd.close()
