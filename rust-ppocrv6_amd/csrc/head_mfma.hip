@@ -131,6 +131,9 @@ static int rows_nsplit(int64_t mblocks) {
 // rescue costs the launch whatever the grid, and a heavy one (a head with large weight
 // outliers guards many rows) needs the whole GPU.
 constexpr int kRescueSlots = 128;
+// Precision limits below it make the two-term bf16 main pass skip row blocks whose rows all
+// go to the rescue.
+constexpr float kVoteLimit = 4.0f;
 
 // How the rows flagged by the precision guard of `cfg` are recomputed: an INT8 head's two
 // activation terms become three bf16 terms (exact products with int8 weights); an FP32
@@ -272,6 +275,11 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
                   guarded ? guard->rows : nullptr,
                   guarded ? guard->epoch : 0u,
                   guarded ? guard->capacity : 0};
+    // A precision limit below typical |a| (rows of unit variance reach max|a| ~ 2.5-3.5 over
+    // 120 values) sends nearly every row to the rescue: the main pass then votes per row
+    // block and skips the blocks it would compute for nothing.  Above the limit the vote
+    // would only cost time (0.3% on the dense batch, 2% on one line): the other variant runs.
+    x.vote = guarded && cfg == CFG_Q2 && rcfg == CFG_Q3 && guard->amax_limit < kVoteLimit;
     const int mb = rpb / (32 * kStatsWaves);
     if (int e = call_stats_main(cfg, tg.G, x, mb, noref, (unsigned)grid, st)) return e;
     if (guarded && rcfg == kRescueFma) {

@@ -324,6 +324,29 @@ __device__ __forceinline__ u16x8 act_split(const float (&x)[ActPlan<C, G>::NL][8
     return f;
 }
 
+// `x` in a vector register, opaque to the optimiser: values computed from it are computed
+// where they are used.  The gather kernels pass k through it, so the last group's bounds
+// (eight offsets and masks) are not hoisted out of the row-block loop and kept live in
+// scalar registers across the tile loop, which spills them.
+__device__ __forceinline__ int opaque_vgpr(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// First value of row `row` of a, and (kst) the floats between its consecutive k values.
+// vec >= 0: rows of k floats.  vec < 0: the channels-first layout [lines][k][T] of the
+// tensor before the neck's transpose, T = -vec: row r is step r % T of line r / T, and its
+// k values are T floats apart.
+__device__ __forceinline__ const float* row_ptr(const float* a, int64_t row, int k, int vec, int64_t& kst) {
+    if (vec >= 0) {
+        kst = 1;
+        return a + row * (int64_t)k;
+    }
+    kst = -(int64_t)vec;
+    const int64_t line = row / kst;
+    return a + line * kst * k + (row - line * kst);
+}
+
 // Issue the loads of a block (act_issue), then split what they return (act_split_all).
 template <int C, int G>
 __device__ __forceinline__ void act_issue(const float* __restrict__ a, int64_t row, int k, int vec, int h,
@@ -351,42 +374,44 @@ __device__ __forceinline__ void act_split_all(const float (&x)[ActPlan<C, G>::NL
 // Activation fragment of one lane for MFMA step s, loaded and split on its own (the
 // rescue passes' gather kernels, which hold more state, use this form: it keeps fewer
 // values live): row `row` of a (zero when the row is not valid), the 8 k values of the
-// lane's slot, as the bf16 term its product uses;
-// `amax` is raised to the largest |value| loaded, `ss` accumulates the squares of the
-// values loaded for product 0 (each k once).  `vec`: rows and groups are 16-byte
-// aligned, so each fragment is two float4 loads.  vec < 0 selects the channels-first
-// layout [lines][k][T] of the tensor before the neck's transpose, T = -vec: row r is step
-// r % T of line r / T, and its k values are T floats apart.
+// lane's slot, as the bf16 term its product uses; `rp` points at the row's first value
+// and `kst` floats separate consecutive k (row_ptr).  `amax` is raised to the largest
+// |value| loaded, `ss` accumulates the squares of the values loaded for product 0 (each k
+// once).  G = ceil(k / 8), so only group G - 1 can be partial, and only the steps that
+// feed it compare k values against k (per-element compares on every step are loop
+// invariants the compiler keeps in scalar registers, which spill).  `vec4`: rows are
+// 16-byte aligned and k % 4 == 0, so a fragment is two float4 loads and a partial last
+// group holds 4 values.
 template <int C, int G, int s>
-__device__ __forceinline__ u16x8 act_frag(const float* __restrict__ a, int64_t row, bool valid, int k, int vec,
+__device__ __forceinline__ u16x8 act_frag(const float* __restrict__ rp, int64_t kst, bool valid, int k, bool vec4,
                                           int h, float& amax, float& ss) {
     u16x8 f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = 0;
     constexpr Slot s0 = Geo<C, G>::slot(s, 0), s1 = Geo<C, G>::slot(s, 1);
+    constexpr bool last = (s0.p >= 0 && s0.g == G - 1) || (s1.p >= 0 && s1.g == G - 1);
     const int p = h ? s1.p : s0.p, g = h ? s1.g : s0.g;
     if (p < 0 || !valid) return f;
     constexpr int t0 = s0.p < 0 ? 0 : CfgT<C>::act(s0.p), t1 = s1.p < 0 ? 0 : CfgT<C>::act(s1.p);
     const int term = h ? t1 : t0;
-    const float* src = a + row * (int64_t)k + 8 * g;
-    int64_t kst = 1;  // floats between consecutive k
-    if (vec < 0) {
-        kst = -(int64_t)vec;
-        const int64_t line = row / kst;
-        src = a + line * kst * k + (row - line * kst) + 8 * g * kst;
-    }
+    const float* src = rp + 8 * g * kst;
     float x[8];
-    if (vec > 0 && 8 * g + 8 <= k) {
+    if (vec4) {
+        const bool hi = !last || 8 * g + 8 <= k;
         const f32x4 v0 = reinterpret_cast<const f32x4*>(src)[0];
-        const f32x4 v1 = reinterpret_cast<const f32x4*>(src)[1];
+        const f32x4 v1 = reinterpret_cast<const f32x4*>(src + (hi ? 4 : 0))[0];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             x[e] = v0[e];
-            x[4 + e] = v1[e];
+            x[4 + e] = hi ? v1[e] : 0.0f;
         }
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (8 * g + e < k) ? src[e * kst] : 0.0f;
+        for (int e = 0; e < 8; ++e) {
+            const int kk = 8 * g + e;
+            const float v = src[(int64_t)(last ? min(kk, k - 1) - 8 * g : e) * kst];
+            x[e] = (!last || kk < k) ? v : 0.0f;
+        }
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -423,22 +448,48 @@ struct RowSource {
 // The list's header is (epoch << 32) | count: the first append of a call installs the
 // call's epoch with count 0 (a header with another epoch counts as empty; epochs have the
 // top bit set, so no index, count or non-negative float left in the workspace matches
-// one), then each append takes the next slot.  Slots past the capacity are dropped.
-__device__ __forceinline__ void guard_append(float amax, float ss, const GuardLimits& lim, bool valid, int64_t row,
-                                             int h, unsigned long long* guard_header, int* guard_rows, unsigned epoch,
-                                             int capacity) {
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    ss += __shfl_xor(ss, 32, 64);
-    if (h == 0 && valid && (amax > lim.prec || (amax > lim.range_amax && ss > lim.range_ss))) {
+// one), then each append takes the next slot.  Slots past the capacity are dropped (the
+// capacity is the batch's row count, and each row is appended once per call).  The test
+// takes the |a| maximum and the sum of squares of both lanes' k groups.
+// Appends the rows of the lanes whose `hit` is set, one atomic per wave: the wave's first
+// such lane reserves popcount(hits) slots, and each lane writes at the base plus the hits
+// of the lanes below it (one atomic per row serialises on the header when a head guards
+// most rows).  Called by every lane of the wave.
+__device__ __forceinline__ void guard_push(bool hit, int64_t row, unsigned long long* guard_header, int* guard_rows,
+                                           unsigned epoch, int capacity) {
+    const unsigned long long mask = __ballot(hit);
+    if (mask == 0ull) return;
+    const int lane = (int)__lane_id();
+    const int leader = __ffsll((long long)mask) - 1;
+    unsigned base = 0;
+    if (lane == leader) {
         unsigned long long cur = __hip_atomic_load(guard_header, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         while ((unsigned)(cur >> 32) != epoch) {
             const unsigned long long prev = atomicCAS(guard_header, cur, (unsigned long long)epoch << 32);
             if (prev == cur) break;
             cur = prev;  // another lane or workgroup changed it first; look again
         }
-        const int pos = (int)(unsigned)atomicAdd(guard_header, 1ull);
+        base = (unsigned)atomicAdd(guard_header, (unsigned long long)__popcll(mask));
+    }
+    base = (unsigned)__shfl((int)base, leader, 64);
+    if (hit) {
+        const int pos = (int)(base + (unsigned)__popcll(mask & ((1ull << lane) - 1ull)));
         if (pos >= 0 && pos < capacity) guard_rows[pos] = (int)row;
     }
+}
+__device__ __forceinline__ void guard_append(float amax, float ss, const GuardLimits& lim, bool valid, int64_t row,
+                                             int h, unsigned long long* guard_header, int* guard_rows, unsigned epoch,
+                                             int capacity) {
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    ss += __shfl_xor(ss, 32, 64);
+    const bool hit = h == 0 && valid && (amax > lim.prec || (amax > lim.range_amax && ss > lim.range_ss));
+    guard_push(hit, row, guard_header, guard_rows, epoch, capacity);
+}
+// The same test, returned on both lanes of the row (the sums agree: addition commutes).
+__device__ __forceinline__ bool guard_hit(float amax, float ss, const GuardLimits& lim, bool valid) {
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    ss += __shfl_xor(ss, 32, 64);
+    return valid && (amax > lim.prec || (amax > lim.range_amax && ss > lim.range_ss));
 }
 
 // Entries of the guard list for this call's epoch (0 for a header of another epoch).
@@ -630,7 +681,24 @@ __device__ __forceinline__ void args_now(const T&... x) {
     (arg_now(x), ...);
 }
 
-template <int C, int G, int MB, bool GATHER, bool NOREF, int OCC = 8 / kStatsWaves>
+// LDS of the main statistics pass: the tile ring, each wave's saved best tile and, in the
+// voting variant, one flag per wave (built where 16 more bytes keep the workgroups per CU:
+// 2, or 3 for the two-term modes' one-block kernel; 160 KiB per CU, 512-byte granules).
+template <int C, int G, int MB>
+constexpr int main_vote_off() {
+    return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
+}
+template <int C, int G, int MB>
+constexpr bool main_vote_fits() {
+    constexpr int per_cu = (MB == 1 && (C == CFG_Q2 || C == CFG_H2)) ? 3 : 2;
+    return (main_vote_off<C, G, MB>() + 16 + 511) / 512 * 512 * per_cu <= 160 * 1024;
+}
+template <int C, int G, int MB, bool VOTE>
+constexpr int main_lds_bytes() {
+    return main_vote_off<C, G, MB>() + (VOTE ? 16 : 0);
+}
+
+template <int C, int G, int MB, bool GATHER, bool NOREF, bool VOTE = false, int OCC = 8 / kStatsWaves>
 __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
@@ -659,6 +727,11 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const int lb = i * 16 + h * 512;
     // this lane's saved values of its best tile: [block][quad][lane] x 4 floats
     f32x4* save = reinterpret_cast<f32x4*>(lds + kRing * GE::BUF) + wave * (MB * 4 * 64) + lane;
+    // VOTE: one flag per wave, whether it holds a row the rescue pass does not recompute
+    constexpr bool kVote = VOTE && !GATHER;
+    static_assert(!kVote || main_vote_fits<C, G, MB>(), "no LDS left for the vote");
+    static_assert(kStatsWaves == 4, "the vote is read as one u32x4");
+    unsigned* vote = reinterpret_cast<unsigned*>(lds + main_vote_off<C, G, MB>());
 
     auto row_block = [&](int64_t blk) {
         const int64_t mrow0 = blk * RPB + wave * (32 * MB);
@@ -678,8 +751,11 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             for (int b = 0; b < MB; ++b) {
                 arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
                 float amax = 0.0f, ss = 0.0f;
+                int64_t kst;
+                const float* rp = row_ptr(a, arow[b], k, vec, kst);
+                const int kv = opaque_vgpr(k);
                 [&]<int... s>(std::integer_sequence<int, s...>) {
-                    ((bf[b][s] = act_frag<C, G, s>(a, arow[b], valid[b], k, vec, h, amax, ss)), ...);
+                    ((bf[b][s] = act_frag<C, G, s>(rp, kst, valid[b], kv, vec > 0, h, amax, ss)), ...);
                 }(std::make_integer_sequence<int, S>{});
             }
         } else {
@@ -689,13 +765,29 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                 arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
                 act_issue<C, G>(a, valid[b] ? arow[b] : 0, k, vec, h, araw[b]);
             }
+            [[maybe_unused]] bool keep = false;  // a row of this lane the rescue pass does not recompute
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
                 float amax = 0.0f, ss = 0.0f;
                 act_split_all<C, G>(araw[b], h, bf[b], amax, ss);
-                if (guard_header && chunk == 0)
+                if constexpr (kVote) {
+                    if (guard_header) {
+                        const bool hit = guard_hit(amax, ss, lim, valid[b]);
+                        if (chunk == 0)
+                            guard_push(h == 0 && hit, arow[b], guard_header, guard_rows, guard_epoch, guard_cap);
+                        keep = keep || (valid[b] && !hit);
+                    } else {
+                        keep = keep || valid[b];
+                    }
+                } else if (guard_header && chunk == 0) {
                     guard_append(amax, ss, lim, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch,
                                  guard_cap);
+                }
+            }
+            // the vote on skipping the block (after the ring barrier below)
+            if constexpr (kVote) {
+                const bool wave_keep = __any(keep);
+                if (guard_header && lane == 0) vote[wave] = wave_keep ? 1u : 0u;
             }
         }
 
@@ -713,6 +805,21 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
         constexpr int kLead = (kRing - 3) * kOps;
         if (t0 < t1) {
             ring_barrier<kLead>();  // tiles t0 and t0+1 are in LDS
+            // Every row of the block on the guard list (a head whose weight outliers put the
+            // limit below typical activations): the rescue pass overwrites all of their
+            // partials, in every chunk, so the tiles are skipped.  Each chunk's workgroup
+            // tests the same rows with the same arithmetic, so they agree, and every wave
+            // reads the same flags (written before the barrier, in LDS nothing else uses).
+            // The staged tile loads land before the workgroup ends.
+            if constexpr (kVote) {
+                if (guard_header) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(vote);
+                    if ((v[0] | v[1] | v[2] | v[3]) == 0u) {
+                        vm_wait<0>();
+                        return;
+                    }
+                }
+            }
             f32x16 acc_a[MB], acc_b[MB];
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
@@ -954,8 +1061,11 @@ __global__ __launch_bounds__(64 * (kWriterWaves + 1), 1) void rows_w_kernel(
         float amax = 0.0f, ss = 0.0f;
         u16x8 bf[S];
         if constexpr (GATHER) {
+            int64_t kst;
+            const float* rp = row_ptr(a, arow, k, vec, kst);
+            const int kv = opaque_vgpr(k);
             [&]<int... s>(std::integer_sequence<int, s...>) {
-                ((bf[s] = act_frag<C, G, s>(a, arow, valid, k, vec, h, amax, ss)), ...);
+                ((bf[s] = act_frag<C, G, s>(rp, kst, valid, kv, vec > 0, h, amax, ss)), ...);
             }(std::make_integer_sequence<int, S>{});
         } else {
             float araw[ActPlan<C, G>::NL][8];
@@ -1053,15 +1163,10 @@ template <int C>
 constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1 || C == CFG_H2) ? 2 : 1;
 }
-// LDS of the main statistics pass: the tile ring and each wave's saved best tile.
-template <int C, int G, int MB>
-constexpr int main_lds_bytes() {
-    return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
-}
-
-template <int C, int G, int MB, bool GATHER, bool NOREF>
+template <int C, int G, int MB, bool GATHER, bool NOREF, bool VOTE = false>
 static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
-    stats_main_kernel<C, G, MB, GATHER, NOREF><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
+    stats_main_kernel<C, G, MB, GATHER, NOREF, VOTE>
+        <<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB, VOTE>(), st>>>(
         x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.p_best, x.p_sum, x.p_idx, x.lim,
         x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap);
 }
@@ -1070,7 +1175,26 @@ static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
 // wave, with or without the reference shift (noref); the others their one variant.
 template <int C, int G>
 int stats_main_cfg(const StatsLaunch& x, int mb, bool noref, unsigned grid, hipStream_t st) {
-    if constexpr (C == CFG_Q2 || C == CFG_H2) {
+    if constexpr (C == CFG_Q2) {
+        // the voting variants only where the host asks for them (a low precision limit)
+        if (mb == 1) {
+            if (x.vote) {
+                if (noref) stats_go<C, G, 1, false, true, true>(x, grid, st);
+                else stats_go<C, G, 1, false, false, true>(x, grid, st);
+            } else {
+                if (noref) stats_go<C, G, 1, false, true>(x, grid, st);
+                else stats_go<C, G, 1, false, false>(x, grid, st);
+            }
+        } else {
+            if (x.vote) {
+                if (noref) stats_go<C, G, 2, false, true, true>(x, grid, st);
+                else stats_go<C, G, 2, false, false, true>(x, grid, st);
+            } else {
+                if (noref) stats_go<C, G, 2, false, true>(x, grid, st);
+                else stats_go<C, G, 2, false, false>(x, grid, st);
+            }
+        }
+    } else if constexpr (C == CFG_H2) {
         if (mb == 1) {
             if (noref) stats_go<C, G, 1, false, true>(x, grid, st);
             else stats_go<C, G, 1, false, false>(x, grid, st);

@@ -55,6 +55,8 @@ struct StatsLaunch {
     int* guard_rows;
     unsigned guard_epoch;
     int guard_cap;
+    // the two-term bf16 main pass skips row blocks the guard sends whole to the rescue
+    bool vote = false;
 };
 struct RowsLaunch {
     const float* a;
