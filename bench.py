@@ -66,6 +66,18 @@ def timed(fn, stream, steps, warmup):
     return e0.elapsed_ms(e1) / steps, wall / steps * 1e3
 
 
+def ramp(fn, seconds=0.2):
+    """Untimed passes of fn() for about `seconds` before a timed leg (beside its --warmup
+    steps): the timed steps then start at the clocks this load holds, as the legs measured
+    after them do (the first leg measured ~10% slow otherwise)."""
+    from ppocr_rechead.hip import synchronize
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        synchronize()
+
+
 def traffic_from_profiles(kernel_key):
     """HBM bytes per launch measured with rocprofv3 --pmc (committed under profiles/)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -173,10 +185,28 @@ def copy_probe(mib):
             "GBps_read_plus_write": round(2 * nbytes / (ms / 1e3) / 1e9, 1)}
 
 
-def measured_peaks():
+def write_probe(nbytes):
+    """HBM write ceiling: streaming 16-byte stores over a buffer of `nbytes` (the probe
+    library's write kernel, timed with HIP events): the bound of the unfused logits writer,
+    which stores the same bytes."""
+    import ctypes
+    from ppocr_rechead.hip import DeviceArray, synchronize
+    lib = ctypes.CDLL(os.path.join(ROOT, "rust-ppocrv6_amd", "lib", "libppocr_probe.so"))
+    nbytes -= nbytes % 16
+    buf = DeviceArray((nbytes,), np.uint8)
+    gb, ms = ctypes.c_double(), ctypes.c_double()
+    rc = lib.ppocr_probe_write(buf.p, ctypes.c_int64(nbytes), ctypes.byref(gb), ctypes.byref(ms))
+    synchronize()
+    buf.free()
+    if rc:
+        raise RuntimeError(f"write probe failed ({rc})")
+    return {"bytes": nbytes, "ms": round(ms.value, 4), "GBps": round(gb.value, 1)}
+
+
+def measured_peaks(write_bytes=0):
     """Peaks measured on this GPU in the same run, beside the datasheet ones: dense bf16
-    MFMA with every operand in registers (the benchmark's probe library), and a 256 MiB
-    device-to-device copy."""
+    MFMA with every operand in registers (the benchmark's probe library), a 256 MiB
+    device-to-device copy and, with write_bytes, streaming writes of that many bytes."""
     import ctypes
     lib = ctypes.CDLL(os.path.join(ROOT, "rust-ppocrv6_amd", "lib", "libppocr_probe.so"))
     tf, ms = ctypes.c_double(), ctypes.c_double()
@@ -188,9 +218,65 @@ def measured_peaks():
     if rc:
         raise RuntimeError(f"MFMA data-operand probe failed ({rc})")
     cp = copy_probe(256)
-    return {"bf16_mfma_TFLOPs": round(tf.value, 1), "mfma_probe_ms": round(ms.value, 3),
-            "bf16_mfma_TFLOPs_kernel_operands": round(tfd.value, 1), "mfma_data_probe_ms": round(msd.value, 3),
-            "copy_GBps_read_plus_write": cp["GBps_read_plus_write"]}
+    out = {"bf16_mfma_TFLOPs": round(tf.value, 1), "mfma_probe_ms": round(ms.value, 3),
+           "bf16_mfma_TFLOPs_kernel_operands": round(tfd.value, 1), "mfma_data_probe_ms": round(msd.value, 3),
+           "copy_GBps_read_plus_write": cp["GBps_read_plus_write"]}
+    if write_bytes:
+        wp = write_probe(write_bytes)
+        out["stream_write_GBps"] = wp["GBps"]
+        out["stream_write_bytes"] = wp["bytes"]
+    return out
+
+
+def neck_kernels(nk, dfx, dsc, m, doff, lines, dfeat, dnws, nws, stream, neck_step, work, reps):
+    """Each kernel of the SVTR tail timed on its own: the forward with a HIP event between
+    its launches (ppocr_rn_forward_marked_dev), each marked forward queued behind an unmarked
+    one so the intervals hold kernels, not launch latency; averaged over `reps` forwards.
+    Each kernel is set against its binding bound: the fp16 MFMA rate measured on the tail's
+    operand patterns divided by the 3 products of the fp16-halves arithmetic (algorithmic
+    flops), or the HBM rate of a device copy (algorithmic bytes), whichever takes longer."""
+    import ctypes
+    import ppocr_rechead as rh
+    from ppocr_rechead.hip import Event
+    L = rh._lib.lib()
+    plib = ctypes.CDLL(os.path.join(ROOT, "rust-ppocrv6_amd", "lib", "libppocr_probe.so"))
+    tf, pms = ctypes.c_double(), ctypes.c_double()
+    rc = plib.ppocr_probe_mfma_f16_data(ctypes.c_int(10000), ctypes.byref(tf), ctypes.byref(pms))
+    if rc:
+        raise RuntimeError(f"fp16 MFMA probe failed ({rc})")
+    hbm = copy_probe(256)["GBps_read_plus_write"]
+    products = 3 if nk.gemm_halves else None
+    ceiling = tf.value / products if products else FP32_PEAK_TFLOPS
+    ne = 16
+    evs = [Event() for _ in range(ne)]
+    ev_arr = (ctypes.c_void_p * ne)(*[e.h.value for e in evs])
+    names = (ctypes.c_char_p * ne)()
+    rec = ctypes.c_int()
+    acc = None
+    ramp(neck_step, 0.05)
+    for _ in range(reps):
+        neck_step()
+        rh._check(L.ppocr_rn_forward_marked_dev(nk.handle, dfx.p, dsc.p, m, doff.p, lines, rh.NECK_ROWS, dfeat.p,
+                                                dnws.p, nws, stream.h, ev_arr, ne, names, ctypes.byref(rec)))
+        evs[rec.value - 1].synchronize()
+        t = [evs[i - 1].elapsed_ms(evs[i]) for i in range(1, rec.value)]
+        acc = t if acc is None else [x + y for x, y in zip(acc, t)]
+    got = [names[i].decode() for i in range(1, rec.value)]
+    if got != [w[0] for w in work]:
+        raise RuntimeError(f"tail kernels {got} do not match the work model {[w[0] for w in work]}")
+    out = []
+    for (name, flops, nbytes), tot in zip(work, acc):
+        ms = tot / reps
+        t_m = flops / (ceiling * 1e12) * 1e3
+        t_h = nbytes / (hbm * 1e9) * 1e3
+        out.append({"name": name, "ms": round(ms, 4), "GFLOP": round(flops / 1e9, 3), "MB": round(nbytes / 1e6, 2),
+                    "TFLOPs": round(flops / (ms / 1e3) / 1e12, 1), "GBps": round(nbytes / (ms / 1e3) / 1e9, 1),
+                    "bound": "mfma" if t_m >= t_h else "hbm", "bound_ms": round(max(t_m, t_h), 4),
+                    "frac": round(max(t_m, t_h) / ms, 4)})
+    bound = {"f16_mfma_TFLOPs_tail_operands": round(tf.value, 1), "products_per_multiply_add": products,
+             "mfma_ceiling_TFLOPs": round(ceiling, 1), "copy_GBps_read_plus_write": hbm,
+             "marked_forward_ms": round(sum(acc) / reps, 4)}
+    return out, bound
 
 
 def make_workload(name):
@@ -242,6 +328,7 @@ def other_config(name, modes, steps, warmup, samples=None):
             rh._check(L.ppocr_rh_decode_dev(head.handle, da.p, m, doff.p, lines, mode, didx.p, dmp.p, dseq.p,
                                             dlen.p, dscore.p, dws.p, ws, st))
 
+        ramp(step)
         ms, _ = timed(step, stream, steps, warmup)
         flops = 2.0 * m * n * k
         r = {"ms_per_step": round(ms, 4), "rows_per_s": round(m / (ms / 1e3), 1),
@@ -333,12 +420,32 @@ def main():
     out = {}
     flops = 2.0 * m * n * k
     if args.only in ("", "fused"):
+        ramp(fused_step)
         ms_step, wall_ms = timed(fused_step, stream, args.steps, args.warmup)
         synchronize()
         gpu_res = {"idx": didx.numpy(), "maxprob": dmp.numpy(), "seq": dseq.numpy(), "seq_len": dlen.numpy(),
                    "score": dscore.numpy()}
         ms_head, _ = timed(fused_argmax, stream, args.steps, args.warmup)
         out["fused"] = (ms_step, wall_ms, ms_head)
+        # the library's default arithmetic (AUTO: the mode the head's weights suit) on the
+        # same batch, beside the split the headline runs
+        default = None
+        if mode != 5:
+            aws = head.workspace_bytes(m, 5)
+            daws = DeviceArray((max(aws, 1),), np.uint8)
+
+            def auto_step():
+                rh._check(L.ppocr_rh_decode_dev(head.handle, da.p, m, doff.p, lines, 5, didx.p, dmp.p, dseq.p,
+                                                dlen.p, dscore.p, daws.p, aws, st))
+
+            ramp(auto_step, 0.05)
+            ms_auto, _ = timed(auto_step, stream, args.steps, args.warmup)
+            amode = head.auto_mode()
+            default = {"mode": f"auto ({MODE_NAMES[amode]})", "ms_per_step": round(ms_auto, 5),
+                       "rows_per_s": round(m / (ms_auto / 1e3), 1),
+                       "guarded_rows": int(head.guarded_rows(a, amode).sum()) if amode in TERMS else 0}
+            daws.free()
+        out["default"] = default
 
     unf = None
     if args.only in ("", "unfused"):
@@ -386,11 +493,14 @@ def main():
         nflops = float(sum(int(t) * wl.neck_flops_per_row(int(t)) for t in steps_of))
         synchronize()
         feats = dfeat.numpy()
+        kernels, bound = neck_kernels(nk, dfx, dsc, m, doff, lines, dfeat, dnws, nws, stream, neck_step,
+                                      wl.neck_kernel_work(steps_of, len(nw["blocks"])), max(20, args.steps // 4))
         neck = {"blocks": len(nw["blocks"]), "ms_per_step": round(ms_n, 4), "rows_per_s": round(m / (ms_n / 1e3), 1),
                 "TFLOPs": round(nflops / (ms_n / 1e3) / 1e12, 2),
-                "fp32_peak_frac": round(nflops / (ms_n / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4),
                 "flops_per_step": nflops, "head_input_max_abs": round(float(np.abs(feats).max()), 2),
                 "matmul_arithmetic": "fp16 halves (3 products)" if nk.gemm_halves else "fp32",
+                "bound": bound, "kernels": kernels,
+                "frac_of_binding_bound": round(sum(x["bound_ms"] for x in kernels) / ms_n, 4),
                 "neck_then_head": {}}
         for hm in sorted({mode, 5}):
             hws = head.workspace_bytes(m, hm)
@@ -442,7 +552,11 @@ def main():
                 "entry": "ppocr_rh_decode (host activations in, host sequences out)"}
 
     copy = copy_probe(args.copy_probe) if args.copy_probe > 0 else None
-    peaks = measured_peaks() if args.only == "" else None
+    peaks = measured_peaks(int(4 * m * n)) if args.only == "" else None
+    if unf and peaks and peaks.get("stream_write_GBps"):
+        # the logits writer against the streaming-write ceiling of the same bytes
+        unf["stream_write_GBps"] = peaks["stream_write_GBps"]
+        unf["logits_frac_of_stream_write"] = round(unf["logits_kernel_GBps"] / peaks["stream_write_GBps"], 4)
 
     others = None
     fp32_samples = {}
@@ -492,7 +606,10 @@ def main():
             "data": "synthetic (seeded N(0,1) activations, N(0,0.05^2) weights packed to INT8 on the GPU)",
             "config": {"workload": f"{args.workload}: {lines} lines x T=120, m={m}, k={k}, n={n}, fused "
                                    "projection+softmax-max+argmax+CTC",
-                       "mode": MODE_NAMES[mode] + (f" ({MODE_NAMES[rmode]})" if mode == 5 else "")},
+                       "mode": MODE_NAMES[mode] + (f" ({MODE_NAMES[rmode]})" if mode == 5 else ""),
+                       "guarded_rows": int(head.guarded_rows(a, rmode).sum()) if rmode in TERMS else 0,
+                       "clock_ramp_s": 0.2},
+            "library_default": out.get("default"),
             "roofline": {"bound": "mfma" if rmode else "valu",
                          "kernel": "ppocr_rh_argmax_dev: stats_main_kernel (>= 95% of the time) + "
                                    "guarded-row rescue and merge kernels",

@@ -330,6 +330,16 @@ int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_s
                          size_t workspace_bytes, void* stream);
 int ppocr_rn_forward(const ppocr_rn_t* h, const float* x, const float* shortcut, const int64_t* line_off,
                      int64_t lines, int layout, float* out);
+/* No counterpart in the reference (measurement of the tail's kernels one by one):
+ * ppocr_rn_forward_dev, with events[0] (hipEvent_t handles, created by the caller) recorded
+ * on the stream before the first kernel and events[i] after the i-th; names[i] receives the
+ * name of the kernel that ends at events[i] (static strings; "start" for events[0]) and
+ * *recorded the number of events used.  PPOCR_ERR_INVALID_ARG when nevents is too small
+ * (2 blocks in the row layout take 9). */
+int ppocr_rn_forward_marked_dev(const ppocr_rn_t* h, const float* d_x, const float* d_shortcut, int64_t m,
+                                const int64_t* d_line_off, int64_t lines, int layout, float* d_out,
+                                void* d_workspace, size_t workspace_bytes, void* stream, void* const* events,
+                                int nevents, const char** names, int* recorded);
 
 #ifdef __cplusplus
 }

@@ -1609,6 +1609,36 @@ int ppocr_rn_forward_dev(const ppocr_rn_t* h, const float* d_x, const float* d_s
                        reinterpret_cast<float*>(ws.p), st);
 }
 
+int ppocr_rn_forward_marked_dev(const ppocr_rn_t* h, const float* d_x, const float* d_shortcut, int64_t m,
+                                const int64_t* d_line_off, int64_t lines, int layout, float* d_out,
+                                void* d_workspace, size_t workspace_bytes, void* stream, void* const* events,
+                                int nevents, const char** names, int* recorded) {
+    if (int e = check_neck(h)) return e;
+    if (!events || !names || !recorded || nevents < 1)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null event list");
+    *recorded = 0;
+    if (m < 0 || lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: negative row or line count");
+    if (layout != PPOCR_NECK_ROWS && layout != PPOCR_NECK_CHANNELS_FIRST)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: unknown layout " + std::to_string(layout));
+    if (m == 0) return PPOCR_OK;
+    if (m > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
+    if (!d_x || !d_shortcut || !d_out || !d_line_off || lines == 0)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: null pointer or no lines");
+    const size_t need = ppocr_rn_workspace_bytes(h, m);
+    if (reinterpret_cast<uintptr_t>(d_workspace) & 15)
+        return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: the workspace must be 16-byte aligned");
+    DeviceGuard dg(h->device);
+    if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecNeckHip: hipSetDevice failed");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Workspace ws;
+    if (int e = ws.get(d_workspace, workspace_bytes, need, st, "RecNeckHip")) return e;
+    NeckMarks marks{reinterpret_cast<hipEvent_t*>(const_cast<void**>(events)), names, nevents, 0};
+    const int e = launch_neck(h->dev, d_x, d_shortcut, m, d_line_off, lines, 0, layout, d_out,
+                              reinterpret_cast<float*>(ws.p), st, &marks);
+    *recorded = marks.count;
+    return e;
+}
+
 int ppocr_rn_forward(const ppocr_rn_t* h, const float* x, const float* shortcut, const int64_t* line_off,
                      int64_t lines, int layout, float* out) {
     if (int e = check_neck(h)) return e;

@@ -1160,7 +1160,15 @@ int gemm_go(const float* a, int64_t m, const float* w, int n, const float* bias,
 }  // namespace
 
 int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, int64_t m, const int64_t* line_off,
-                int64_t lines, int64_t line_len, int layout, float* out, float* ws, hipStream_t st) {
+                int64_t lines, int64_t line_len, int layout, float* out, float* ws, hipStream_t st, NeckMarks* marks) {
+    // an event after the kernel just launched (and its name), when marks are asked for
+    auto mark = [&](const char* name) -> int {
+        if (!marks) return PPOCR_OK;
+        if (marks->count >= marks->capacity) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too few events");
+        PPOCR_HIP(hipEventRecord(marks->events[marks->count], st));
+        marks->names[marks->count++] = name;
+        return PPOCR_OK;
+    };
     const int D = nk.dim, H = nk.hidden;
     if (D != kNeckDim || H != kNeckHidden || nk.heads * kNeckHeadDim != D)
         return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: unsupported neck geometry");
@@ -1169,6 +1177,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
     if (m <= 0) return PPOCR_OK;
     if (lines <= 0 || (!line_off && line_len <= 0)) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: no lines");
     if (lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many lines");
+    if (int e = mark("start")) return e;
     float* x = ws;                       // residual stream [m][D]
     float* sc = x + m * D;               // shortcut rows [m][D]
     float* qkv = sc + m * D;             // [m][3D], or [m][kNeckQkvPad] on fp16 halves
@@ -1180,6 +1189,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         neck_cf_rows_kernel<<<grid, 256, 0, st>>>(x_in, m, D, line_off, lines, line_len, x);
         neck_cf_rows_kernel<<<grid, 256, 0, st>>>(shortcut_in, m, D, line_off, lines, line_len, sc);
         PPOCR_HIP(hipGetLastError());
+        if (int e = mark("channels_first_to_rows")) return e;
         scr = sc;
     }
     // the residual stream: the first block reads it from the input rows (row layout; the
@@ -1188,9 +1198,10 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
     // later blocks work in place
     const float* xin = x;
     if (layout == PPOCR_NECK_ROWS) {
-        if (reinterpret_cast<uintptr_t>(x_in) & 15)
+        if (reinterpret_cast<uintptr_t>(x_in) & 15) {
             PPOCR_HIP(hipMemcpyAsync(x, x_in, (size_t)m * D * 4, hipMemcpyDeviceToDevice, st));
-        else
+            if (int e = mark("copy")) return e;
+        } else
             xin = x_in;
     }
     // the fused MLP kernel of the last block finishes the tail itself when the shortcut rows
@@ -1206,6 +1217,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
                            : gemm_go<kNeckDim, true, false, false>(xr, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b,
                                                                    k.ln1_eps, nullptr, qkv, st))
             return e;
+        if (int e = mark("ln1_qkv")) return e;
         const dim3 ag((unsigned)lines, (unsigned)nk.heads);
         if (nk.f16)
             neck_attn16_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, nk.scale,
@@ -1213,12 +1225,14 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         else
             neck_attn_kernel<kNeckHeadDim><<<ag, 256, 0, st>>>(qkv, m, line_off, lines, line_len, D, nk.scale, att);
         PPOCR_HIP(hipGetLastError());
+        if (int e = mark("attention")) return e;
         // x = x + proj(att)
         if (int e = nk.f16 ? gemm16_go<kNeckAttPad, false, false, true>(att, m, k.proj_h, D, k.proj_b, nullptr, nullptr,
                                                                        0.0f, xr, x, st)
                            : gemm_go<kNeckDim, false, false, true>(att, m, k.proj_w, D, k.proj_b, nullptr, nullptr,
                                                                    0.0f, xr, x, st))
             return e;
+        if (int e = mark("proj_residual")) return e;
         if (nk.f16) {
             // x = x + fc2(swish(fc1(LN2(x)))) in one pass
             const int64_t gx = (m + kMlpRows - 1) / kMlpRows;
@@ -1232,6 +1246,7 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
                 std::ldexp(1.0f, -(k.mlp_e1 + k.mlp_ey)), std::ldexp(1.0f, k.mlp_eh), std::ldexp(1.0f, -(k.mlp_eh + k.mlp_e2)),
                 x, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);
             PPOCR_HIP(hipGetLastError());
+            if (int e = mark(fin ? "mlp_final_ln_shortcut" : "mlp")) return e;
             if (fin) return PPOCR_OK;
             continue;
         }
@@ -1239,14 +1254,16 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         if (int e = gemm_go<kNeckDim, true, true, false>(x, m, k.fc1_w, H, k.fc1_b, k.ln2_w, k.ln2_b, k.ln2_eps,
                                                          nullptr, hid, st))
             return e;
+        if (int e = mark("ln2_fc1_swish")) return e;
         // x = x + fc2(hid)
         if (int e = gemm_go<kNeckHidden, false, false, true>(hid, m, k.fc2_w, D, k.fc2_b, nullptr, nullptr, 0.0f, x,
                                                              x, st))
             return e;
+        if (int e = mark("fc2_residual")) return e;
     }
     neck_final_kernel<<<(unsigned)((m + 63) / 64), 256, 0, st>>>(x, m, nk.lnf_w, nk.lnf_b, nk.lnf_eps, scr, out);
     PPOCR_HIP(hipGetLastError());
-    return PPOCR_OK;
+    return mark("final_ln_shortcut");
 }
 
 }  // namespace ppocr

@@ -72,7 +72,16 @@ constexpr int64_t kNeckWsFloatsPerRow = 2 * kNeckDim + kNeckQkvPad + kNeckAttPad
 // PPOCR_NECK_CHANNELS_FIRST: line b as [D][T_b] at D * (first row of b)), lines given by
 // device offsets line_off[0..lines] or, with line_off null, line_len rows each; out [m][D]
 // token rows (the input of the head's MatMul).  ws: kNeckWsFloatsPerRow * m floats.
+// With `marks`, an event is recorded on st before the first kernel and after each kernel,
+// and the kernel's name kept beside it (measurement of the kernels one by one).
+struct NeckMarks {
+    hipEvent_t* events;
+    const char** names;  // names[i]: the kernel that ends at events[i] ("start" for events[0])
+    int capacity;
+    int count;
+};
 int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, int64_t m, const int64_t* line_off,
-                int64_t lines, int64_t line_len, int layout, float* out, float* ws, hipStream_t st);
+                int64_t lines, int64_t line_len, int layout, float* out, float* ws, hipStream_t st,
+                NeckMarks* marks = nullptr);
 
 }  // namespace ppocr

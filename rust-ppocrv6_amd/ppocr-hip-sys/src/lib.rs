@@ -171,4 +171,11 @@ extern "C" {
                                 d_workspace: *mut c_void, workspace_bytes: usize, stream: *mut c_void) -> c_int;
     pub fn ppocr_rn_forward(h: *const ppocr_rn_t, x: *const f32, shortcut: *const f32, line_off: *const i64,
                             lines: i64, layout: c_int, out: *mut f32) -> c_int;
+    /// Measurement only (no counterpart in the reference): the forward with a HIP event
+    /// recorded before the first kernel and after each one.
+    pub fn ppocr_rn_forward_marked_dev(h: *const ppocr_rn_t, d_x: *const f32, d_shortcut: *const f32, m: i64,
+                                       d_line_off: *const i64, lines: i64, layout: c_int, d_out: *mut f32,
+                                       d_workspace: *mut c_void, workspace_bytes: usize, stream: *mut c_void,
+                                       events: *const *mut c_void, nevents: c_int, names: *mut *const c_char,
+                                       recorded: *mut c_int) -> c_int;
 }

@@ -87,6 +87,9 @@ SIGNATURES = {
     "ppocr_rn_workspace_bytes": (_sz, [_vp, _i64]),
     "ppocr_rn_forward_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _sz, _vp]),
     "ppocr_rn_forward": (_int, [_vp, _vp, _vp, _vp, _i64, _int, _vp]),
+    "ppocr_rn_forward_marked_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp, _sz, _vp,
+                                           ctypes.POINTER(_vp), _int, ctypes.POINTER(ctypes.c_char_p),
+                                           ctypes.POINTER(_int)]),
 }
 
 _lib = None

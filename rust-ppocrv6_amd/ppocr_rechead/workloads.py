@@ -153,6 +153,25 @@ def neck_weights(seed=SEED_NECK, blocks=2):
     return {"blocks": bl, "lnf_w": f(d, s=1.7, mu=3.0), "lnf_b": f(d, s=0.6, mu=-0.5), "lnf_eps": 1e-6}
 
 
+def neck_kernel_work(steps_of, blocks=2):
+    """Algorithmic work of each kernel of the tail's forward on token rows (row layout), in
+    launch order: (name, flops, HBM bytes).  Flops: 2 per multiply-add of each MatMul and of
+    the attention's scores and weighted values (sum over lines of 4 T^2 D); bytes: fp32 rows
+    read and written once (the weights, under 0.3 MB per block, are left out)."""
+    d, h = NECK_DIM, NECK_HIDDEN
+    steps_of = np.asarray(steps_of, np.int64)
+    m = int(steps_of.sum())
+    row = 4 * d * m  # bytes of one [m][d] fp32 tensor
+    out = []
+    for b in range(blocks):
+        last = b + 1 == blocks
+        out += [("ln1_qkv", 2.0 * m * d * 3 * d, row + 3 * row),
+                ("attention", 4.0 * d * float((steps_of.astype(np.float64) ** 2).sum()), 3 * row + row),
+                ("proj_residual", 2.0 * m * d * d, 3 * row),
+                ("mlp_final_ln_shortcut" if last else "mlp", 2.0 * m * (d * h + h * d), (3 if last else 2) * row)]
+    return out
+
+
 def neck_flops_per_row(steps, blocks=2):
     """Algorithmic FLOPs of the tail per token row of a line of `steps` tokens: the four
     MatMuls of each block (2 D 3D + 2 D D + 2 D H + 2 H D) and its attention (2 steps D for

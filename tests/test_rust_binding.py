@@ -28,6 +28,7 @@ C_TO_RUST = {
     "int*": "*mut c_int", "const ppocr_rh_t*": "*const ppocr_rh_t", "ppocr_rh_t*": "*mut ppocr_rh_t",
     "ppocr_rh_t**": "*mut *mut ppocr_rh_t", "float": "f32", "const ppocr_rn_block_t*": "*const ppocr_rn_block_t",
     "const ppocr_rn_t*": "*const ppocr_rn_t", "ppocr_rn_t*": "*mut ppocr_rn_t", "ppocr_rn_t**": "*mut *mut ppocr_rn_t",
+    "void* const*": "*const *mut c_void", "const char**": "*mut *const c_char",
 }
 
 
