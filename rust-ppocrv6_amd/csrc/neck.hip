@@ -280,34 +280,36 @@ template <int K>
 constexpr int gemm16_kp() {
     return K <= 128 ? 128 : 256;
 }
-template <int K, bool LN>
+template <int K, bool LN, int TPW>
 constexpr size_t gemm16_lds_bytes() {
-    return (size_t)2 * kGemmCols * gemm16_kp<K>() * 2 + (LN ? 2 * K * 4 : 0);
+    return (size_t)2 * (32 * TPW) * gemm16_kp<K>() * 2 + (LN ? 2 * K * 4 : 0);
 }
 
-template <int K, bool LN, bool SWISH, bool RES>
+// TPW: tiles of 32 columns per wave, so 32 TPW columns per workgroup.
+template <int K, bool LN, bool SWISH, bool RES, int TPW>
 __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __restrict__ a, int64_t m,
                                                           const uint16_t* __restrict__ wt, int n,
                                                           const float* __restrict__ bias,
                                                           const float* __restrict__ ln_w,
                                                           const float* __restrict__ ln_b, float eps,
                                                           const float* res, float* out) {
-    constexpr int KP = gemm16_kp<K>(), S = KP / 16, NCH = KP / 8;
+    constexpr int KP = gemm16_kp<K>(), S = KP / 16, NCH = KP / 8, NC = 32 * TPW;
     static_assert(K % 8 == 0 && K <= KP, "8-element chunks of k");
-    extern __shared__ __align__(16) uint8_t ls16[];  // [2][128][NCH] chunks of 16 bytes, then (LN) [2][K] floats
+    static_assert(TPW == 2 || TPW == 4, "tiles per wave");
+    extern __shared__ __align__(16) uint8_t ls16[];  // [2][NC][NCH] chunks of 16 bytes, then (LN) [2][K] floats
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    const int n0 = blockIdx.y * kGemmCols;
-    // stage both planes: chunk e of the stage = plane e / (128 NCH), column (e / NCH) % 128,
-    // slot e % NCH, holding the column's chunk slot ^ ((column / 4) % 8); a column past n
+    const int n0 = blockIdx.y * NC;
+    // stage both planes: chunk e of the stage = plane e / (NC NCH), column (e / NCH) % NC,
+    // slot e % NCH, holding the column's chunk slot ^ ((column / TPW) % 8); a column past n
     // reloads column 0 (its results are never stored, and each output column depends only
     // on its own weights)
-    constexpr int CH = 2 * kGemmCols * NCH;
+    constexpr int CH = 2 * NC * NCH;
     static_assert(CH % 64 == 0 && NCH % 8 == 0, "whole instructions; slots permuted within groups of 8");
     for (int x = wave; x < CH / 64; x += 4) {
         const int e = 64 * x + lane;
-        const int p = e / (kGemmCols * NCH), c = (e / NCH) % kGemmCols, sl = e % NCH;
+        const int p = e / (NC * NCH), c = (e / NCH) % NC, sl = e % NCH;
         const int col = n0 + c < n ? n0 + c : 0;
-        const uint16_t* src = wt + ((size_t)p * n + col) * KP + 8 * (sl ^ ((c >> 2) & 7));
+        const uint16_t* src = wt + ((size_t)p * n + col) * KP + 8 * (sl ^ ((c / TPW) & 7));
         __builtin_amdgcn_global_load_lds(
             static_cast<const void*>(src),
             reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(ls16 + 1024 * x)),
@@ -324,23 +326,23 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
                 0);
         }
     }
-    // this lane's chunks of its row: k = 16 s + 8 h .. + 7 (zeros past K)
+    // this lane's chunks of its row: k = 16 s + 8 h .. + 7 (zeros past K and past m), every
+    // load from an address inside the batch and issued before any is used (a branch per
+    // chunk made the compiler wait for each)
     const int64_t row = (int64_t)blockIdx.x * kGemmRows + wave * 32 + i;
+    const bool row_ok = row < m;
+    const float* arow = a + (row_ok ? row : 0) * K;
     float av[S][8];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int k0 = 16 * s + 8 * h;
-        if (row < m && k0 < K) {
-            const f32x4* src = reinterpret_cast<const f32x4*>(a + row * K + k0);
-            const f32x4 v0 = src[0], v1 = src[1];
+        const bool ok = row_ok && k0 < K;
+        const f32x4* src = reinterpret_cast<const f32x4*>(arow + (k0 < K ? k0 : 0));
+        const f32x4 v0 = src[0], v1 = src[1];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                av[s][e] = v0[e];
-                av[s][4 + e] = v1[e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) av[s][e] = 0.0f;
+        for (int e = 0; e < 4; ++e) {
+            av[s][e] = ok ? v0[e] : 0.0f;
+            av[s][4 + e] = ok ? v1[e] : 0.0f;
         }
     }
     float mean = 0.0f, inv = 0.0f;
@@ -376,24 +378,30 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             float x = av[s][e];
-            if constexpr (LN) x = k0 < K ? fmaf((x - mean) * inv, lnl[k0 + e], lnl[K + k0 + e]) : 0.0f;
+            if constexpr (LN) {
+                // computed for every k (the parameters' index clamped to the last k, inside
+                // the LDS block) and then masked
+                const int kc = min(k0 + e, K - 1);
+                const float y = fmaf((x - mean) * inv, lnl[kc], lnl[K + kc]);
+                x = k0 < K ? y : 0.0f;
+            }
             const _Float16 xh = (_Float16)x;
             const _Float16 xl = (_Float16)(x - (float)xh);
             ahi[s][e] = __builtin_bit_cast(unsigned short, xh);
             alo[s][e] = __builtin_bit_cast(unsigned short, xl);
         }
     }
-    f32x16 acc[4];
+    f32x16 acc[TPW];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
-    // column 4 i + t, chunk 2 s + h: slot (2 s + h) ^ (i % 8)
-    const uint8_t* whi = ls16 + (size_t)(4 * i) * NCH * 16;
-    const uint8_t* wlo = whi + (size_t)kGemmCols * NCH * 16;
+    for (int t = 0; t < TPW; ++t) acc[t] = f32x16{};
+    // column TPW i + t, chunk 2 s + h: slot (2 s + h) ^ (i % 8)
+    const uint8_t* whi = ls16 + (size_t)(TPW * i) * NCH * 16;
+    const uint8_t* wlo = whi + (size_t)NC * NCH * 16;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int sl = (2 * s + h) ^ (i & 7);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < TPW; ++t) {
             const u16x8 bh = *reinterpret_cast<const u16x8*>(whi + ((size_t)t * NCH + sl) * 16);
             const u16x8 bl = *reinterpret_cast<const u16x8*>(wlo + ((size_t)t * NCH + sl) * 16);
             acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
@@ -404,42 +412,53 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
                                                             __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
         }
     }
-    gemm_epilogue<SWISH, RES, 4>(acc, (int64_t)blockIdx.x * kGemmRows + wave * 32, h, n0 + 4 * i, m, n, bias, res,
-                                 out);
+    gemm_epilogue<SWISH, RES, TPW>(acc, (int64_t)blockIdx.x * kGemmRows + wave * 32, h, n0 + TPW * i, m, n, bias, res,
+                                   out);
 }
 
 // ---------------------------------------------------------------- MLP
 // x = x + fc2(swish(fc1(LN2(x)))) for 128 token rows per workgroup, the hidden layer never
-// leaving registers (fp16 halves, as neck_gemm16_kernel).  fc1 runs transposed, hidden
+// leaving the chip (fp16 halves, as neck_gemm16_kernel).  fc1 runs transposed, hidden
 // units as MFMA rows and token rows as columns: lane (i, h) then holds, for its token row i,
 // the units 8 (r / 4) + 4 h + r % 4 (r < 16) of each tile of 32 units, which are exactly the
-// eight contraction values a lane of fc2's A operand supplies per MFMA step once fc2's
+// eight contraction values a lane of fc2's B operand supplies per MFMA step once fc2's
 // contraction index runs in the order K' = 32 T + 16 q + 8 h + e <-> unit 32 T + 16 q +
-// 8 (e / 4) + 4 h + e % 4 (fc2's weight planes are stored in that order).  So each tile of
-// 32 hidden units is bias + swish + split in registers and consumed by fc2 at once.
-// Eight waves: waves g and g + 4 share the 32 rows of row group g, the first taking unit
-// tiles 0-3, the second 4-7 (two waves per SIMD, so one's vector work overlaps the other's
-// MFMAs); at the end the second adds its fc2 sums to the first's through LDS.  Weights stream
-// through a 2-slot LDS ring, each slot holding unit tiles j and j + 4 (NeckBlockDev::mlp_h:
-// fc1's rows of a tile as [plane][k chunk][unit], 16 KB, then fc2's matching contraction
-// block as [plane][chunk][output column], 16 KB, laid out in memory as in LDS, so each load
+// 8 (e / 4) + 4 h + e % 4 (fc2's weight planes are stored in that order).
+// Eight waves, a producer and a consumer per row group of 32 rows, one of each per SIMD: in
+// step j the producer (waves 0-3) runs fc1, bias, swish and the split of unit tile j and
+// writes the halves to LDS, lane by lane in the order the consumer's lanes read them; the
+// consumer (waves 4-7) runs fc2 of tile j - 1 on the halves written in the step before.  So
+// one wave's vector work (the swish) overlaps the other's MFMAs (both roles in one wave each
+// did them in turn, and the barriers kept the two waves of a SIMD in the same phase).  One
+// barrier per step.  The weights stream through two LDS rings two steps ahead, fc1's part of
+// each tile for the producer and fc2's for the consumer (NeckBlockDev::mlp_h: per tile,
+// fc1's rows as [plane][k chunk][unit], 16 KB, then fc2's matching contraction block as
+// [plane][chunk][output column], 16 KB, laid out in memory as in LDS, so each load
 // instruction reads 1 KB in one piece); the 32 lanes of a half-wave read 32 consecutive
-// chunks.
+// chunks.  After the last step the consumer holds its rows' complete fc2 sums.
 // Operands are scaled by powers of two before their splits (sy, sh; the weight planes hold
 // scaled weights) so that the low halves stay above fp16's subnormals, which these MFMAs
 // do not all keep; s1, s2 undo the scaling of the products exactly.
 // The swish here uses the hardware exp2 and reciprocal (a few ulp from the correctly
 // rounded sigmoid, far below the tail's parity bar).
 constexpr int kMlpRows = 128;
-constexpr int kMlpTiles = 8;  // tiles of 32 hidden units (240 padded to 256)
-constexpr int kMlpTile = 32768;  // bytes of one staged unit tile (fc1 16 KB, fc2 16 KB)
+constexpr int kMlpTiles = 8;     // tiles of 32 hidden units (240 padded to 256)
+constexpr int kMlpPart = 16384;  // bytes of a tile's fc1 part, of its fc2 part, of a hidden buffer
 constexpr int kMlpCols = 128;    // fc2's output columns, padded
 static_assert(kNeckHidden <= 32 * kMlpTiles && kNeckDim <= kMlpCols && kNeckDim <= 128, "MLP geometry");
-// the ring (2 slots of 2 tiles), then the constants: LN2's weight and bias, fc1's bias,
+// LDS: the fc1 ring (3 parts: loads are issued two steps ahead), hidden buffer 0, the fc2
+// ring (3 parts), hidden buffer 1, then the constants: LN2's weight and bias, fc1's bias,
 // fc2's bias (each padded to whole 16-byte chunks; padding never reaches an output), the
-// final LayerNorm's weight and bias
+// final LayerNorm's weight and bias.  In the last step the first four parts (64 KB: the fc1
+// ring and hidden buffer 0, none of them read then) take the workgroup's rows of x, the
+// residual.
+constexpr int kMlpRing = 3;
+constexpr int kMlpW1 = 0, kMlpH0 = kMlpRing * kMlpPart, kMlpW2 = (kMlpRing + 1) * kMlpPart;
+constexpr int kMlpH1 = (2 * kMlpRing + 1) * kMlpPart, kMlpConst = (2 * kMlpRing + 2) * kMlpPart;
 constexpr int kMlpConstChunks = 256;
-constexpr size_t mlp16_lds_bytes() { return (size_t)4 * kMlpTile + kMlpConstChunks * 16; }
+static_assert(kMlpW1 == 0 && kMlpH0 + kMlpPart == 4 * kMlpPart && kMlpRows * kNeckDim * 4 <= 4 * kMlpPart,
+              "the rows of x fit the four parts at the start of LDS");
+constexpr size_t mlp16_lds_bytes() { return (size_t)kMlpConst + kMlpConstChunks * 16; }
 
 __device__ __forceinline__ float swish_fast(float z) { return z * __builtin_amdgcn_rcpf(1.0f + __expf(-z)); }
 
@@ -460,35 +479,21 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
     extern __shared__ __align__(16) uint8_t lm[];
     // constants: chunks 0-29 LN2 weight, 30-59 LN2 bias, 60-123 fc1 bias, 124-155 fc2 bias,
     // 156-185 the final LayerNorm's weight, 186-215 its bias
-    const float* lnw = reinterpret_cast<const float*>(lm + 4 * kMlpTile);
+    const float* lnw = reinterpret_cast<const float*>(lm + kMlpConst);
     const float* lnb = lnw + D;
     const float* b1s = lnw + 2 * D;
     const float* b2s = b1s + 32 * kMlpTiles;
     const float* lfw = b2s + kMlpCols;
     const float* lfb = lfw + D;
     static_assert(D % 4 == 0 && H % 4 == 0 && 4 * D + 32 * kMlpTiles + kMlpCols <= 4 * kMlpConstChunks, "chunks");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    const int grp = wave & 3, half = wave >> 2;  // row group; unit tiles 4 half .. 4 half + 3
-    const int64_t rbase = (int64_t)blockIdx.x * kMlpRows + grp * 32;
-    const int64_t row = rbase + i;
+    const int tid = threadIdx.x, lane = tid & 63, i = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave & 3;
+    const bool producer = wave < 4;
+    const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
+    const int64_t row = r0 + grp * 32 + i;
+    const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);  // bytes of the block's rows
 
-    // this lane's chunks of its row: k = 16 s + 8 h .. + 7 (zeros past D), every load issued
-    // before any is used
-    float av[S][8];
-    {
-        const int64_t rr = row < m ? row : 0;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int k0 = 16 * s + 8 * h;
-            const f32x4* src = reinterpret_cast<const f32x4*>(x + rr * D + (k0 < D ? k0 : 0));
-            const f32x4 v0 = src[0], v1 = src[1];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                av[s][e] = k0 < D ? v0[e] : 0.0f;
-                av[s][4 + e] = k0 < D ? v1[e] : 0.0f;
-            }
-        }
-    }
     if (wave < (FINAL ? 4 : 3)) {
         const int c = 64 * wave + lane;
         const float* src = c < 30 ? ln_w + 4 * c
@@ -502,29 +507,26 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
             __builtin_amdgcn_global_load_lds(
                 static_cast<const void*>(src),
                 reinterpret_cast<__attribute__((address_space(3))) void*>(
-                    reinterpret_cast<uintptr_t>(lm + 4 * kMlpTile + 1024 * wave)),
+                    reinterpret_cast<uintptr_t>(lm + kMlpConst + 1024 * wave)),
                 16, 0, 0);
     }
-    // unit tiles j and j + 4 into ring slot j % 2: two contiguous 32 KB tiles of wt, 8
-    // instructions of 1 KB per wave
-    auto stage = [&](int j) {
+    // one 16 KB part (0: fc1's, 1: fc2's) of unit tile T into LDS at dst: 16 instructions of
+    // 1 KB, two per wave
+    auto stage_part = [&](int T, int part, int dst) {
 #pragma unroll
-        for (int x8 = 0; x8 < 8; ++x8) {
-            const int xi = wave + 8 * x8;  // instruction 0..63: tile j (0..31), tile j + 4 (32..63)
-            const int T = j + 4 * (xi >> 5), xt = xi & 31;
-            const uint8_t* src = reinterpret_cast<const uint8_t*>(wt) + (size_t)T * kMlpTile + 1024 * xt + 16 * lane;
+        for (int x2 = 0; x2 < 2; ++x2) {
+            const int xi = wave + 8 * x2;
+            const uint8_t* src =
+                reinterpret_cast<const uint8_t*>(wt) + (size_t)T * (2 * kMlpPart) + part * kMlpPart + 1024 * xi + 16 * lane;
             __builtin_amdgcn_global_load_lds(
                 static_cast<const void*>(src),
-                reinterpret_cast<__attribute__((address_space(3))) void*>(
-                    reinterpret_cast<uintptr_t>(lm + (j & 1) * 2 * kMlpTile + 1024 * xi)),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(lm + dst + 1024 * xi)),
                 16, 0, 0);
         }
     };
-    // the workgroup's rows of x (128 x 480 bytes, contiguous) into ring slot 0, whole 16-byte
+    // the workgroup's rows of x (128 x 480 bytes, contiguous) into LDS at 0, whole 16-byte
     // chunks of the rows inside the batch: up to 60 instructions of 1 KB, at most 8 per wave
     auto stage_rows = [&] {
-        const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
-        const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);
         const uint8_t* src = reinterpret_cast<const uint8_t*>(x + r0 * D);
 #pragma unroll
         for (int x8 = 0; x8 < 8; ++x8) {
@@ -536,116 +538,154 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
                     16, 0, 0);
         }
     };
-    stage(0);
-    stage(1);
-    // LN2 of the row: its two halves meet in xor-32 shuffles
-    float sm = 0.0f;
+    stage_part(0, 0, kMlpW1);
+    stage_part(1, 0, kMlpW1 + kMlpPart);
+    stage_part(0, 1, kMlpW2);
+
+    // producer: its row's chunks k = 16 s + 8 h .. + 7 (zeros past D), every load issued
+    // before any is used, then LN2 (the row's two halves meet in xor-32 shuffles)
+    float av[S][8];
+    float mean = 0.0f, inv = 0.0f;
+    if (producer) {
+        const int64_t rr = row < m ? row : 0;
 #pragma unroll
-    for (int s = 0; s < S; ++s)
+        for (int s = 0; s < S; ++s) {
+            const int k0 = 16 * s + 8 * h;
+            const f32x4* src = reinterpret_cast<const f32x4*>(x + rr * D + (k0 < D ? k0 : 0));
+            const f32x4 v0 = src[0], v1 = src[1];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sm += av[s][e];
-    sm += __shfl_xor(sm, 32, 64);
-    const float mean = __fdiv_rn(sm, (float)D);
-    float var = 0.0f;
+            for (int e = 0; e < 4; ++e) {
+                av[s][e] = k0 < D ? v0[e] : 0.0f;
+                av[s][4 + e] = k0 < D ? v1[e] : 0.0f;
+            }
+        }
+        float sm = 0.0f;
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-        if (16 * s + 8 * h < D) {
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sm += av[s][e];
+        sm += __shfl_xor(sm, 32, 64);
+        mean = __fdiv_rn(sm, (float)D);
+        float var = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (16 * s + 8 * h < D) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = av[s][e] - mean;
+                    var = fmaf(d, d, var);
+                }
+            }
+        }
+        var += __shfl_xor(var, 32, 64);
+        inv = inv_std_of(__fdiv_rn(var, (float)D), eps);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0): the first parts, the constants
+    __syncthreads();
+    // producer: fc1's B operand, the normalised row times sy, fp16 halves
+    u16x8 xh[S], xl[S];
+    if (producer) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int k0 = 16 * s + 8 * h;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float d = av[s][e] - mean;
-                var = fmaf(d, d, var);
+                // computed for every k (past D it reads other constants of LDS) and then
+                // masked, so no branch per value
+                const float yv = fmaf((av[s][e] - mean) * inv, lnw[k0 + e], lnb[k0 + e]) * sy;
+                const float y = k0 < D ? yv : 0.0f;
+                const _Float16 yh = (_Float16)y;
+                xh[s][e] = __builtin_bit_cast(unsigned short, yh);
+                xl[s][e] = __builtin_bit_cast(unsigned short, (_Float16)(y - (float)yh));
             }
         }
     }
-    var += __shfl_xor(var, 32, 64);
-    const float inv = inv_std_of(__fdiv_rn(var, (float)D), eps);
-    __builtin_amdgcn_s_waitcnt(0x8 | (0x7 << 4) | (0xF << 8));  // vmcnt(8): all but slot 1's loads
-    __syncthreads();                                              // slot 0 and the constants are in LDS
-    // fc1's B operand: the normalised row times sy, fp16 halves
-    u16x8 xh[S], xl[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        const int k0 = 16 * s + 8 * h;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float y = k0 < D ? fmaf((av[s][e] - mean) * inv, lnw[k0 + e], lnb[k0 + e]) * sy : 0.0f;
-            const _Float16 yh = (_Float16)y;
-            xh[s][e] = __builtin_bit_cast(unsigned short, yh);
-            xl[s][e] = __builtin_bit_cast(unsigned short, (_Float16)(y - (float)yh));
-        }
-    }
+    // hidden buffer of tile T for this row group: [q][plane][lane] 16-byte chunks
+    auto hbuf = [&](int T) { return lm + ((T & 1) ? kMlpH1 : kMlpH0) + grp * 4096; };
     f32x16 acc2[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc2[t] = f32x16{};
-    for (int j = 0; j < kMlpTiles / 2; ++j) {
-        const int T = j + 4 * half;
-        const uint8_t* w1 = lm + (j & 1) * 2 * kMlpTile + half * kMlpTile;
-        const uint8_t* w2 = w1 + 16384;
-        // fc1, transposed: units 32 T + i (A, from LDS) x the row (B)
-        f32x16 a1 = f32x16{};
+    for (int j = 0; j <= kMlpTiles; ++j) {
+        // the loads for the step after next: fc1 of tile j + 2, fc2 of tile j + 1 (their ring
+        // slots were last read in the step before); in the last step, the rows of x
+        const bool ld1 = j + 2 < kMlpTiles, ld2 = j + 1 < kMlpTiles;
+        if (ld1) stage_part(j + 2, 0, kMlpW1 + ((j + 2) % kMlpRing) * kMlpPart);
+        if (ld2) stage_part(j + 1, 1, kMlpW2 + ((j + 1) % kMlpRing) * kMlpPart);
+        if (j == kMlpTiles) stage_rows();
+        if (producer) {
+            if (j < kMlpTiles) {
+                const int T = j;
+                const uint8_t* w1 = lm + kMlpW1 + (T % kMlpRing) * kMlpPart;
+                // fc1, transposed: units 32 T + i (A, from LDS) x the row (B)
+                f32x16 a1 = f32x16{};
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int c = 2 * s + h;
-            const u16x8 wh = *reinterpret_cast<const u16x8*>(w1 + ((size_t)c * 32 + i) * 16);
-            const u16x8 wl = *reinterpret_cast<const u16x8*>(w1 + ((size_t)(16 + c) * 32 + i) * 16);
-            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh), __builtin_bit_cast(f16x8, xh[s]),
-                                                        a1, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh), __builtin_bit_cast(f16x8, xl[s]),
-                                                        a1, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wl), __builtin_bit_cast(f16x8, xh[s]),
-                                                        a1, 0, 0, 0);
-        }
-        // bias, swish and the split: r = 8 q + e is fc2's contraction value e of step 2 T + q
-        u16x8 hh[2], hl[2];
+                for (int s = 0; s < S; ++s) {
+                    const int c = 2 * s + h;
+                    const u16x8 wh = *reinterpret_cast<const u16x8*>(w1 + ((size_t)c * 32 + i) * 16);
+                    const u16x8 wl = *reinterpret_cast<const u16x8*>(w1 + ((size_t)(16 + c) * 32 + i) * 16);
+                    a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh),
+                                                                __builtin_bit_cast(f16x8, xh[s]), a1, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh),
+                                                                __builtin_bit_cast(f16x8, xl[s]), a1, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wl),
+                                                                __builtin_bit_cast(f16x8, xh[s]), a1, 0, 0, 0);
+                }
+                // bias, swish and the split: r = 8 q + e is fc2's contraction value e of step
+                // 2 T + q; the halves go to LDS for the consumer lane of the same (i, h)
+                uint8_t* hb = hbuf(T);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+                for (int q = 0; q < 2; ++q) {
+                    u16x8 hh, hl;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int r = 8 * q + e;
-                const int u = 32 * T + 8 * (r >> 2) + 4 * h + (r & 3);
-                const float v = u < H ? swish_fast(a1[r] * s1 + b1s[u]) * sh : 0.0f;
-                const _Float16 vh = (_Float16)v;
-                hh[q][e] = __builtin_bit_cast(unsigned short, vh);
-                hl[q][e] = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)vh));
+                    for (int e = 0; e < 8; ++e) {
+                        const int r = 8 * q + e;
+                        const int u = 32 * T + 8 * (r >> 2) + 4 * h + (r & 3);
+                        // computed for every unit (b1s holds 32 * kMlpTiles values, padded) and
+                        // then masked: as a condition around the swish, each value was a branch
+                        const float sw = swish_fast(a1[r] * s1 + b1s[u]) * sh;
+                        const float v = u < H ? sw : 0.0f;
+                        const _Float16 vh = (_Float16)v;
+                        hh[e] = __builtin_bit_cast(unsigned short, vh);
+                        hl[e] = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)vh));
+                    }
+                    *reinterpret_cast<u16x8*>(hb + ((size_t)(2 * q) * 64 + lane) * 16) = hh;
+                    *reinterpret_cast<u16x8*>(hb + ((size_t)(2 * q + 1) * 64 + lane) * 16) = hl;
+                }
+            }
+        } else if (j >= 1) {
+            const int T = j - 1;
+            const uint8_t* w2 = lm + kMlpW2 + (T % kMlpRing) * kMlpPart;
+            const uint8_t* hb = hbuf(T);
+            // fc2, transposed: output columns 32 t + i (A, from LDS) x the row's hidden values (B)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const u16x8 hh = *reinterpret_cast<const u16x8*>(hb + ((size_t)(2 * q) * 64 + lane) * 16);
+                const u16x8 hl = *reinterpret_cast<const u16x8*>(hb + ((size_t)(2 * q + 1) * 64 + lane) * 16);
+                const int c = 2 * q + h;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const u16x8 bh = *reinterpret_cast<const u16x8*>(w2 + ((size_t)c * kMlpCols + 32 * t + i) * 16);
+                    const u16x8 bl = *reinterpret_cast<const u16x8*>(w2 + ((size_t)(4 + c) * kMlpCols + 32 * t + i) * 16);
+                    acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bh),
+                                                                     __builtin_bit_cast(f16x8, hh), acc2[t], 0, 0, 0);
+                    acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bl),
+                                                                     __builtin_bit_cast(f16x8, hh), acc2[t], 0, 0, 0);
+                    acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bh),
+                                                                     __builtin_bit_cast(f16x8, hl), acc2[t], 0, 0, 0);
+                }
             }
         }
-        // fc2, transposed: output columns 32 t + i (A, from LDS) x the row's hidden values (B)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int c = 2 * q + h;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const u16x8 bh = *reinterpret_cast<const u16x8*>(w2 + ((size_t)c * kMlpCols + 32 * t + i) * 16);
-                const u16x8 bl = *reinterpret_cast<const u16x8*>(w2 + ((size_t)(4 + c) * kMlpCols + 32 * t + i) * 16);
-                acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bh),
-                                                                 __builtin_bit_cast(f16x8, hh[q]), acc2[t], 0, 0, 0);
-                acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bl),
-                                                                 __builtin_bit_cast(f16x8, hh[q]), acc2[t], 0, 0, 0);
-                acc2[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bh),
-                                                                 __builtin_bit_cast(f16x8, hl[q]), acc2[t], 0, 0, 0);
-            }
-        }
-        __syncthreads();  // every wave is done with slot j % 2
-        if (j + 2 < kMlpTiles / 2) {
-            stage(j + 2);
-            __builtin_amdgcn_s_waitcnt(0x8 | (0x7 << 4) | (0xF << 8));  // vmcnt(8): slot j + 1 has landed
-        } else if (j + 2 == kMlpTiles / 2) {
-            // slot 0 takes the workgroup's rows of x, the residual, while the last tiles run
-            // (their number of loads varies by wave, so slot 1 is waited for first)
-            __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0): slot 1 has landed
-            stage_rows();
-        } else {
-            __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0): the rows have landed
-        }
-        __syncthreads();  // slot (j + 1) % 2 is in LDS (after the last tiles: the rows of x)
+        // the parts of the next step (issued a step ago) have landed; this step's own loads
+        // (two instructions per part, per wave) may stay in flight, except the rows of x
+        if (ld1 && ld2) __builtin_amdgcn_s_waitcnt(0x4 | (0x7 << 4) | (0xF << 8));  // vmcnt(4)
+        else if (ld1 || ld2) __builtin_amdgcn_s_waitcnt(0x2 | (0x7 << 4) | (0xF << 8));  // vmcnt(2)
+        else __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
+        __syncthreads();  // every wave is done with this step's parts
     }
-    // lane (i, h) holds fc2 of row rbase + i at columns 32 t + 8 v + 4 h + 0..3 (acc2[t][4 v ..]).
-    // The second wave of each row group hands its sums to the first through slot 1 ([group]
-    // [t][v][lane] float4s, 16 KB per group), which adds the bias and the residual into the
-    // rows of x in slot 0; then the workgroup stores those rows in one contiguous piece.
-    const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
-    const int nb = (int)(min((int64_t)kMlpRows, m - r0) * D * 4);  // bytes of the block's rows
-    f32x4 scv[8];  // FINAL: the shortcut rows, loaded while the sums are exchanged
+    // lane (i, h) of a consumer holds fc2 of row grp * 32 + i at columns 32 t + 8 v + 4 h +
+    // 0..3 (acc2[t][4 v ..]): bias and the residual into the rows of x in LDS; then the
+    // workgroup stores those rows in one contiguous piece.
+    f32x4 scv[8];  // FINAL: the shortcut rows, loaded while the sums are added
     if constexpr (FINAL) {
         const uint8_t* sc = reinterpret_cast<const uint8_t*>(shortcut + r0 * D);
 #pragma unroll
@@ -654,16 +694,7 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
             scv[k8] = b0 < nb ? *reinterpret_cast<const f32x4*>(sc + b0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
-    f32x4* red = reinterpret_cast<f32x4*>(lm + 2 * kMlpTile) + grp * (16 * 64) + lane;
-    if (half == 1) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                red[(4 * t + v) * 64] = f32x4{acc2[t][4 * v], acc2[t][4 * v + 1], acc2[t][4 * v + 2], acc2[t][4 * v + 3]};
-    }
-    __syncthreads();
-    if (half == 0) {
+    if (!producer) {
         float* xr = reinterpret_cast<float*>(lm) + (grp * 32 + i) * D;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -671,10 +702,9 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
             for (int v = 0; v < 4; ++v) {
                 const int col = 32 * t + 8 * v + 4 * h;
                 if (col < D) {
-                    const f32x4 o = red[(4 * t + v) * 64];
                     f32x4 xv = *reinterpret_cast<const f32x4*>(xr + col);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) xv[e] = xv[e] + ((acc2[t][4 * v + e] + o[e]) * s2 + b2s[col + e]);
+                    for (int e = 0; e < 4; ++e) xv[e] = xv[e] + (acc2[t][4 * v + e] * s2 + b2s[col + e]);
                     *reinterpret_cast<f32x4*>(xr + col) = xv;
                 }
             }
@@ -741,6 +771,11 @@ __device__ __forceinline__ int perm_dim(int d) { return 4 * (d & 3) + (d >> 2); 
 __device__ __forceinline__ float max_f32(float a, float b) {
     float r;
     asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
     return r;
 }
 
@@ -894,7 +929,10 @@ __global__ __launch_bounds__(256) void neck_attn_kernel(const float* __restrict_
 // scaling by a power of two, undone on the scores and the output: the MFMA takes fp16
 // subnormal inputs as zeros (measured: the halves of values below 0.25 would vanish), so
 // the scalings lift the low halves above fp16's smallest normal (6.1e-5).  q, k and v use
-// exponents from their bounds (neck creation); the probabilities, in (0, 1], 2^15.
+// exponents from their bounds (neck creation); the probabilities, in (0, 1], 2^15.  The
+// head's 16th dim (padding) of V holds 1, so row 15 of O^T accumulates sum(p) beside the
+// weighted values (rescaled with them by the online softmax), and the softmax's exponent
+// folds the scalings: p = 2^{s ec + eb} with one fma.
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 constexpr int kKhStride = 20;  // halves per K row in LDS: 16 dims + 4, so the 16 rows a
                                // lane group reads at once fall in distinct banks
@@ -914,7 +952,9 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
     // powers of two: exact scalings of the operands before the split, undone on the scores
     // and the output
     const float qmul = ldexpf(1.0f, eq), kmul = ldexpf(1.0f, ek), vmul = ldexpf(1.0f, ev);
-    const float sdiv = ldexpf(1.0f, -(eq + ek)), vdiv = ldexpf(1.0f, -ev);
+    const float vdiv = ldexpf(1.0f, -ev);
+    // the exponent of the softmax per unit of raw score: 2^-(eq + ek) log2(e)
+    const float ec = ldexpf(1.4426950408889634f, -(eq + ek));
     static_assert(HD <= 16, "one 16-wide MFMA tile holds a head's dims");
     constexpr int KT = kAttnKeyTiles, QB = kAttnQBlocks;
     __shared__ __align__(16) _Float16 ks[2][kAttnKeys * kKhStride];  // K block [hi, lo][t][dim]
@@ -934,7 +974,7 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
         // this wave's query blocks: queries qpass + 16 (wave + 4 x) + c, dims 4 g .. + 3
         f16x4 qh[QB], ql[QB];
         f32x4 oa[QB];
-        float mx[QB], ls[QB];
+        float mx[QB];
 #pragma unroll
         for (int x = 0; x < QB; ++x) {
             const int q = qpass + 16 * (wave + 4 * x) + c;
@@ -950,7 +990,6 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
             }
             oa[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             mx[x] = -INFINITY;
-            ls[x] = 0.0f;
         }
         for (int kb = 0; kb < T; kb += kAttnKeys) {
             const int rem = T - kb;  // keys of the line from this block on
@@ -978,7 +1017,13 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
                     split_half(kv[x][e] * kmul, hi, lo);
                     kh[e] = hi;
                     kl[e] = lo;
-                    split_half(vv[x][e] * vmul, vt[0][(sd + e) * kVtStride + tl], vt[1][(sd + e) * kVtStride + tl]);
+                    if (sd + e == 15) {
+                        // the padding dim of V holds 1: row 15 of O^T is then sum(p)
+                        vt[0][15 * kVtStride + tl] = (_Float16)1.0f;
+                        vt[1][15 * kVtStride + tl] = (_Float16)0.0f;
+                    } else {
+                        split_half(vv[x][e] * vmul, vt[0][(sd + e) * kVtStride + tl], vt[1][(sd + e) * kVtStride + tl]);
+                    }
                 }
                 *reinterpret_cast<f16x4*>(&ks[0][tl * kKhStride + sd]) = kh;
                 *reinterpret_cast<f16x4*>(&ks[1][tl * kKhStride + sd]) = kl;
@@ -990,6 +1035,8 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
                 if (q0 >= T) continue;  // uniform over the wave
                 // one query block at a time: interleaved, their scores would all be live
                 __builtin_amdgcn_sched_barrier(0);
+                // scores in the MFMA's units (q and k scaled by 2^eq and 2^ek; the softmax's
+                // exponent takes the scaling back, below)
                 f32x4 sc[KT];
 #pragma unroll
                 for (int t = 0; t < KT; ++t) {
@@ -997,18 +1044,20 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
                     const f16x4 kl = *reinterpret_cast<const f16x4*>(&ks[1][(16 * t + c) * kKhStride + 4 * g]);
                     f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, qh[x], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, ql[x], acc, 0, 0, 0);
-                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh[x], acc, 0, 0, 0) * sdiv;
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh[x], acc, 0, 0, 0);
                 }
-                // keys past the line's end score -inf (their p is then exactly 0); the block's
-                // maximum for query q0 + c: this lane's keys, then the lane groups
+                // keys past the line's end score -inf (their p is then exactly 0), tested only in
+                // the tiles that reach past it; the block's maximum for query q0 + c: this lane's
+                // keys, then the lane groups
                 float bm = -INFINITY;
 #pragma unroll
                 for (int t = 0; t < KT; ++t) {
+                    if (16 * t + 16 > rem) {  // uniform; the asm keeps it a branch, not selects
+                        asm volatile("");
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        sc[t][jj] = (16 * t + 4 * g + jj < rem) ? sc[t][jj] : -INFINITY;
-                        bm = max_f32(bm, sc[t][jj]);
+                        for (int jj = 0; jj < 4; ++jj) sc[t][jj] = (16 * t + 4 * g + jj < rem) ? sc[t][jj] : -INFINITY;
                     }
+                    bm = max3_f32(max3_f32(bm, sc[t][0], sc[t][1]), sc[t][2], sc[t][3]);
                 }
                 bm = max_f32(bm, __shfl_xor(bm, 16, 64));
                 bm = max_f32(bm, __shfl_xor(bm, 32, 64));
@@ -1016,26 +1065,27 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
                 if (kb > 0) {
                     // rescale the sums so far (every block of a pass after the first follows one
                     // that set a finite maximum)
-                    const float corr = __expf(mx[x] - nm);
-                    ls[x] *= corr;
-                    oa[x] = oa[x] * corr;
+                    const float corr = __builtin_amdgcn_exp2f((mx[x] - nm) * ec);
+                    oa[x] = oa[x] * corr;  // the sum of p (row 15) with the rest
                 }
                 mx[x] = nm;
-                float l = 0.0f;
+                // p = 2^15 e^{(s - max) 2^-(eq+ek)} = 2^{s ec + eb}: one fma and one exp2 per key.  The
+                // 2^15 (exact; it cancels in sum(p v) / sum(p)) keeps the halves of small
+                // probabilities above fp16's subnormals.
+                const float eb = fmaf(-nm, ec, 15.0f);
                 f32x4 ob = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int t = 0; t < KT; ++t) {
                     f16x4 ph, pl;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
-                        // p scaled by 2^15 (exact; it cancels in sum(p v) / sum(p)), so the halves
-                        // of small probabilities stay above fp16's subnormals
-                        const float p = __expf(sc[t][jj] - nm) * 32768.0f;
-                        l += p;
-                        _Float16 hi, lo;
-                        split_half(p, hi, lo);
-                        ph[jj] = hi;
-                        pl[jj] = lo;
+                        const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][jj], ec, eb));
+                        // the halves: p with its low 13 mantissa bits cleared (exact in fp16 for
+                        // p >= 2^-14; below, the conversion rounds it, an error under 2^-25 on
+                        // p's scale of 2^15) and the exact remainder, rounded to fp16
+                        const float hi = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
+                        ph[jj] = (_Float16)hi;
+                        pl[jj] = (_Float16)(p - hi);
                     }
                     // O^T += V^T P^T: even and odd key tiles on two accumulators
                     const f16x4 vh = *reinterpret_cast<const f16x4*>(&vt[0][c * kVtStride + 16 * t + 4 * g]);
@@ -1046,20 +1096,19 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
                     acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph, acc, 0, 0, 0);
                 }
                 oa[x] += ob;
-                ls[x] += l;
             }
         }
         // per query: the sums of the four lane groups; lane l writes query q0 + c, dims 4 g + j
 #pragma unroll
         for (int x = 0; x < QB; ++x) {
             const int q = qpass + 16 * (wave + 4 * x) + c;
-            float l = ls[x];
-            l += __shfl_xor(l, 16, 64);
-            l += __shfl_xor(l, 32, 64);
+            // sum(p) of query c: row 15 of O^T, held by lane group 3
+            const float l = __shfl(oa[x][3], 48 + c, 64);
             if (q < T) {
                 f32x4 ov;
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) ov[jj] = __fdiv_rn(oa[x][jj] * vdiv, l);
+                if (g == 3) ov[3] = 0.0f;  // the padding value
                 *reinterpret_cast<f32x4*>(o + (t0 + q) * (int64_t)kNeckAttPad + 16 * h + 4 * g) = ov;
             }
         }
@@ -1126,15 +1175,22 @@ __global__ __launch_bounds__(256) void neck_final_kernel(const float* __restrict
     for (int e = 0; e < kLnQuad; ++e) orow[e] = v[e] + sr[e];
 }
 
+// Tiles of 32 columns per wave of the fp16-halves GEMMs: 2, so 64 columns per workgroup
+// (qkv's 384 columns in 6 column blocks, 1440 workgroups for the dense batch; proj's 120 in
+// 2), with 32 KB of weights per workgroup, so up to 3 workgroups per CU.
+constexpr int kGemm16TilesPerWave = 2;
+
 template <int K, bool LN, bool SWISH, bool RES>
 int gemm16_go(const float* a, int64_t m, const uint16_t* wt, int n, const float* bias, const float* ln_w,
               const float* ln_b, float eps, const float* res, float* out, hipStream_t st) {
     static_assert(gemm16_kp<K>() == neck_f16_kp(K), "the planes' padding");
+    constexpr int TPW = kGemm16TilesPerWave;
     const int64_t gx = (m + kGemmRows - 1) / kGemmRows;
-    const int gy = (n + kGemmCols - 1) / kGemmCols;
+    const int gy = (n + 32 * TPW - 1) / (32 * TPW);
     if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
-    neck_gemm16_kernel<K, LN, SWISH, RES><<<dim3((unsigned)gx, (unsigned)gy), 256, gemm16_lds_bytes<K, LN>(), st>>>(
-        a, m, wt, n, bias, ln_w, ln_b, eps, res, out);
+    neck_gemm16_kernel<K, LN, SWISH, RES, TPW>
+        <<<dim3((unsigned)gx, (unsigned)gy), 256, gemm16_lds_bytes<K, LN, TPW>(), st>>>(a, m, wt, n, bias, ln_w, ln_b,
+                                                                                     eps, res, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }

@@ -39,6 +39,12 @@ def _f32_limit(w_t):
     return min(16.0 / float(np.abs(w_t).max()), 4.0 / float(np.sqrt((w * w).sum(axis=1)).max()))
 
 
+def _f16_limit_f32(w_t):
+    """An FP32 head's limit with fp16 halves of both operands (F16X2): min(32768, 64 / L2)."""
+    w = np.abs(w_t.astype(np.float64))
+    return min(32768.0, 64.0 / float(np.sqrt((w * w).sum(axis=1)).max()))
+
+
 def _f16_limit_int8(q, s):
     """The INT8 head's limit with two fp16 activation terms: min(32768, 512 / L2)."""
     qa = np.abs(q.astype(np.int64))
@@ -155,13 +161,15 @@ def test_int8_logits_around_the_precision_limit(orc, rh, head):
     assert_close_rel(mp, r["maxprob"], "int8 limit maxprob")
 
 
-def test_fp32_head_precision_guard(orc, rh):
-    """BF16X3 on an FP32 head: rows of max|a| 0.5 .. 0.99 of its precision limit stay on the
-    MFMA path, rows above it (to x50 of an N(0,1) row) are recomputed in fp32 FMA.  Logits,
-    the fused argmax and the probabilities against the oracle."""
+@pytest.mark.parametrize("mode", [3, 4], ids=["bf16x3", "f16x2"])
+def test_fp32_head_precision_guard(orc, rh, mode):
+    """BF16X3 and F16X2 on an FP32 head: rows of max|a| 0.5 .. 0.99 of the mode's precision
+    limit stay on the MFMA path, rows above it (to 3x the limit, and x50 of an N(0,1) row)
+    are recomputed in fp32 FMA.  Logits, the fused argmax and the probabilities against the
+    oracle.  The limit is computed here from the weights and checked against the library's."""
     from ppocr_rechead import workloads as wl
     w_t, bias = wl.weights()
-    lim = _f32_limit(w_t)
+    lim = _f32_limit(w_t) if mode == 3 else _f16_limit_f32(w_t)
     rng = np.random.default_rng(34)
     fr = np.concatenate([np.linspace(0.5, 0.99, 64), np.linspace(1.01, 3.0, 32)])
     a = rng.standard_normal((fr.size, 120)).astype(np.float32)
@@ -169,10 +177,11 @@ def test_fp32_head_precision_guard(orc, rh):
     big = rng.standard_normal((32, 120)).astype(np.float32) * np.float32(50.0)
     a = np.concatenate([a, big]).astype(np.float32)
     head = rh.RecHead(w_t=w_t, bias=bias)
-    print(f"fp32 head guard, limit {lim:.3f}", flush=True)
-    got = head.logits(a, 3)
-    idx, mp = head.argmax(a, 3)
-    probs = head.probs(a, 3)
+    print(f"fp32 head guard, mode {mode}, limit {lim:.3f}", flush=True)
+    assert head.guard_limits(mode)[0] == pytest.approx(lim, rel=1e-5)
+    got = head.logits(a, mode)
+    idx, mp = head.argmax(a, mode)
+    probs = head.probs(a, mode)
     head.close()
     ref = oracle_head_f32(orc, a, w_t, bias, np.array([0, a.shape[0]], np.int64), want_probs=True)
     lg = f64_logits_f32(a, w_t, bias)
@@ -180,9 +189,9 @@ def test_fp32_head_precision_guard(orc, rh):
     err = np.abs(got - ref["logits"])
     print(f"  max|logits diff|: under {err[:64].max():.2e}, over {err[64:96].max():.2e}, x50 {err[96:].max():.2e}")
     assert np.all(err <= tol)
-    check_argmax(idx, ref["idx"], top2_gap(lg), label="fp32 guard")
-    assert_close_rel(mp, ref["maxprob"], "fp32 guard maxprob", row_scale=rel_scale(lg))
-    assert_close_rel(probs, ref["probs"], "fp32 guard probs", row_scale=rel_scale(lg))
+    check_argmax(idx, ref["idx"], top2_gap(lg), label=f"fp32 guard mode {mode}")
+    assert_close_rel(mp, ref["maxprob"], f"fp32 guard maxprob mode {mode}", row_scale=rel_scale(lg))
+    assert_close_rel(probs, ref["probs"], f"fp32 guard probs mode {mode}", row_scale=rel_scale(lg))
 
 
 def test_dense_256_whole_batch(orc, rh, head):
