@@ -425,12 +425,13 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
 // contraction index runs in the order K' = 32 T + 16 q + 8 h + e <-> unit 32 T + 16 q +
 // 8 (e / 4) + 4 h + e % 4 (fc2's weight planes are stored in that order).
 // Eight waves, a producer and a consumer per row group of 32 rows, one of each per SIMD: in
-// step j the producer (waves 0-3) runs fc1, bias, swish and the split of unit tile j and
-// writes the halves to LDS, lane by lane in the order the consumer's lanes read them; the
-// consumer (waves 4-7) runs fc2 of tile j - 1 on the halves written in the step before.  So
-// one wave's vector work (the swish) overlaps the other's MFMAs (both roles in one wave each
-// did them in turn, and the barriers kept the two waves of a SIMD in the same phase).  One
-// barrier per step.  The weights stream through two LDS rings two steps ahead, fc1's part of
+// step j the producer (waves 0-3) runs the bias, swish and split of unit tile j, interleaved
+// with the MFMAs of tile j + 1's fc1 (the swish's vector work runs while the matrix core
+// works), and writes the halves to LDS, lane by lane in the order the consumer's lanes read
+// them; the consumer (waves 4-7) runs fc2 of tile j - 1 on the halves written in the step
+// before.  (With both roles in one wave each did them in turn, and the barriers kept the two
+// waves of a SIMD in the same phase.)  One barrier per step.  The weights stream through
+// two LDS rings, fc1's part of
 // each tile for the producer and fc2's for the consumer (NeckBlockDev::mlp_h: per tile,
 // fc1's rows as [plane][k chunk][unit], 16 KB, then fc2's matching contraction block as
 // [plane][chunk][output column], 16 KB, laid out in memory as in LDS, so each load
@@ -446,18 +447,17 @@ constexpr int kMlpTiles = 8;     // tiles of 32 hidden units (240 padded to 256)
 constexpr int kMlpPart = 16384;  // bytes of a tile's fc1 part, of its fc2 part, of a hidden buffer
 constexpr int kMlpCols = 128;    // fc2's output columns, padded
 static_assert(kNeckHidden <= 32 * kMlpTiles && kNeckDim <= kMlpCols && kNeckDim <= 128, "MLP geometry");
-// LDS: the fc1 ring (3 parts: loads are issued two steps ahead), hidden buffer 0, the fc2
-// ring (3 parts), hidden buffer 1, then the constants: LN2's weight and bias, fc1's bias,
-// fc2's bias (each padded to whole 16-byte chunks; padding never reaches an output), the
-// final LayerNorm's weight and bias.  In the last step the first four parts (64 KB: the fc1
-// ring and hidden buffer 0, none of them read then) take the workgroup's rows of x, the
+// LDS: the fc1 ring (4 parts: each is loaded three steps before the step that reads it),
+// hidden buffer 0, the fc2 ring (3 parts, loaded two steps ahead), hidden buffer 1, then the
+// constants: LN2's weight and bias, fc1's bias, fc2's bias (each padded to whole 16-byte
+// chunks; padding never reaches an output), the final LayerNorm's weight and bias.  From
+// step 7 on the fc1 ring is not read, and its 64 KB take the workgroup's rows of x, the
 // residual.
-constexpr int kMlpRing = 3;
-constexpr int kMlpW1 = 0, kMlpH0 = kMlpRing * kMlpPart, kMlpW2 = (kMlpRing + 1) * kMlpPart;
-constexpr int kMlpH1 = (2 * kMlpRing + 1) * kMlpPart, kMlpConst = (2 * kMlpRing + 2) * kMlpPart;
+constexpr int kMlpRing1 = 4, kMlpRing2 = 3;
+constexpr int kMlpW1 = 0, kMlpH0 = kMlpRing1 * kMlpPart, kMlpW2 = kMlpH0 + kMlpPart;
+constexpr int kMlpH1 = kMlpW2 + kMlpRing2 * kMlpPart, kMlpConst = kMlpH1 + kMlpPart;
 constexpr int kMlpConstChunks = 256;
-static_assert(kMlpW1 == 0 && kMlpH0 + kMlpPart == 4 * kMlpPart && kMlpRows * kNeckDim * 4 <= 4 * kMlpPart,
-              "the rows of x fit the four parts at the start of LDS");
+static_assert(kMlpW1 == 0 && kMlpRows * kNeckDim * 4 <= kMlpRing1 * kMlpPart, "the rows of x fit the fc1 ring");
 constexpr size_t mlp16_lds_bytes() { return (size_t)kMlpConst + kMlpConstChunks * 16; }
 
 __device__ __forceinline__ float swish_fast(float z) { return z * __builtin_amdgcn_rcpf(1.0f + __expf(-z)); }
@@ -540,6 +540,7 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
     };
     stage_part(0, 0, kMlpW1);
     stage_part(1, 0, kMlpW1 + kMlpPart);
+    stage_part(2, 0, kMlpW1 + 2 * kMlpPart);
     stage_part(0, 1, kMlpW2);
 
     // producer: its row's chunks k = 16 s + 8 h .. + 7 (zeros past D), every load issued
@@ -602,59 +603,72 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
     }
     // hidden buffer of tile T for this row group: [q][plane][lane] 16-byte chunks
     auto hbuf = [&](int T) { return lm + ((T & 1) ? kMlpH1 : kMlpH0) + grp * 4096; };
+    // producer: MFMA step s of fc1, transposed (units 32 T + i, A from LDS, x the row, B)
+    auto fc1_step = [&](int T, int s, f32x16& a) {
+        const uint8_t* w1 = lm + kMlpW1 + (T % kMlpRing1) * kMlpPart;
+        const int c = 2 * s + h;
+        const u16x8 wh = *reinterpret_cast<const u16x8*>(w1 + ((size_t)c * 32 + i) * 16);
+        const u16x8 wl = *reinterpret_cast<const u16x8*>(w1 + ((size_t)(16 + c) * 32 + i) * 16);
+        a = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh), __builtin_bit_cast(f16x8, xh[s]), a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh), __builtin_bit_cast(f16x8, xl[s]), a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wl), __builtin_bit_cast(f16x8, xh[s]), a, 0, 0, 0);
+    };
+    // producer: hidden value r = 8 q + e of tile T (fc2's contraction value e of step 2 T + q):
+    // bias, swish, the mask past H and the split; computed for every unit (b1s holds
+    // 32 * kMlpTiles values, padded) and then masked, as a condition around the swish each
+    // value became a branch
+    auto hidden = [&](const f32x16& a, int T, int r, u16x8 (&hh)[2], u16x8 (&hl)[2]) {
+        const int u = 32 * T + 8 * (r >> 2) + 4 * h + (r & 3);
+        const float sw = swish_fast(a[r] * s1 + b1s[u]) * sh;
+        const float v = u < H ? sw : 0.0f;
+        const _Float16 vh = (_Float16)v;
+        hh[r >> 3][r & 7] = __builtin_bit_cast(unsigned short, vh);
+        hl[r >> 3][r & 7] = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)vh));
+    };
+    f32x16 a1 = f32x16{};  // producer: fc1 of the tile whose swish the step computes
+    if (producer) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) fc1_step(0, s, a1);
+    }
     f32x16 acc2[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc2[t] = f32x16{};
     for (int j = 0; j <= kMlpTiles; ++j) {
-        // the loads for the step after next: fc1 of tile j + 2, fc2 of tile j + 1 (their ring
-        // slots were last read in the step before); in the last step, the rows of x
-        const bool ld1 = j + 2 < kMlpTiles, ld2 = j + 1 < kMlpTiles;
-        if (ld1) stage_part(j + 2, 0, kMlpW1 + ((j + 2) % kMlpRing) * kMlpPart);
-        if (ld2) stage_part(j + 1, 1, kMlpW2 + ((j + 1) % kMlpRing) * kMlpPart);
-        if (j == kMlpTiles) stage_rows();
+        // loads: fc1 of tile j + 3 and fc2 of tile j + 1 (their ring slots were last read two
+        // steps and a step before); in step 7, the rows of x into the fc1 ring
+        const bool ld1 = j + 3 < kMlpTiles, ld2 = j + 1 < kMlpTiles;
+        if (ld1) stage_part(j + 3, 0, kMlpW1 + ((j + 3) % kMlpRing1) * kMlpPart);
+        if (ld2) stage_part(j + 1, 1, kMlpW2 + ((j + 1) % kMlpRing2) * kMlpPart);
+        if (j == kMlpTiles - 1) stage_rows();
         if (producer) {
             if (j < kMlpTiles) {
-                const int T = j;
-                const uint8_t* w1 = lm + kMlpW1 + (T % kMlpRing) * kMlpPart;
-                // fc1, transposed: units 32 T + i (A, from LDS) x the row (B)
-                f32x16 a1 = f32x16{};
+                // the swish of tile j (a1) interleaved with the MFMAs of tile j + 1's fc1 (an):
+                // the vector work runs while the matrix core works
+                u16x8 hh[2], hl[2];
+                f32x16 an = f32x16{};
+                if (j + 1 < kMlpTiles) {
 #pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    const int c = 2 * s + h;
-                    const u16x8 wh = *reinterpret_cast<const u16x8*>(w1 + ((size_t)c * 32 + i) * 16);
-                    const u16x8 wl = *reinterpret_cast<const u16x8*>(w1 + ((size_t)(16 + c) * 32 + i) * 16);
-                    a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh),
-                                                                __builtin_bit_cast(f16x8, xh[s]), a1, 0, 0, 0);
-                    a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wh),
-                                                                __builtin_bit_cast(f16x8, xl[s]), a1, 0, 0, 0);
-                    a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wl),
-                                                                __builtin_bit_cast(f16x8, xh[s]), a1, 0, 0, 0);
+                    for (int s = 0; s < S; ++s) {
+                        fc1_step(j + 1, s, an);
+#pragma unroll
+                        for (int r = 2 * s; r < 2 * s + 2; ++r) hidden(a1, j, r, hh, hl);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) hidden(a1, j, r, hh, hl);
                 }
-                // bias, swish and the split: r = 8 q + e is fc2's contraction value e of step
-                // 2 T + q; the halves go to LDS for the consumer lane of the same (i, h)
-                uint8_t* hb = hbuf(T);
+                uint8_t* hb = hbuf(j);
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
-                    u16x8 hh, hl;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int r = 8 * q + e;
-                        const int u = 32 * T + 8 * (r >> 2) + 4 * h + (r & 3);
-                        // computed for every unit (b1s holds 32 * kMlpTiles values, padded) and
-                        // then masked: as a condition around the swish, each value was a branch
-                        const float sw = swish_fast(a1[r] * s1 + b1s[u]) * sh;
-                        const float v = u < H ? sw : 0.0f;
-                        const _Float16 vh = (_Float16)v;
-                        hh[e] = __builtin_bit_cast(unsigned short, vh);
-                        hl[e] = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)vh));
-                    }
-                    *reinterpret_cast<u16x8*>(hb + ((size_t)(2 * q) * 64 + lane) * 16) = hh;
-                    *reinterpret_cast<u16x8*>(hb + ((size_t)(2 * q + 1) * 64 + lane) * 16) = hl;
+                    *reinterpret_cast<u16x8*>(hb + ((size_t)(2 * q) * 64 + lane) * 16) = hh[q];
+                    *reinterpret_cast<u16x8*>(hb + ((size_t)(2 * q + 1) * 64 + lane) * 16) = hl[q];
                 }
+                a1 = an;
             }
         } else if (j >= 1) {
             const int T = j - 1;
-            const uint8_t* w2 = lm + kMlpW2 + (T % kMlpRing) * kMlpPart;
+            const uint8_t* w2 = lm + kMlpW2 + (T % kMlpRing2) * kMlpPart;
             const uint8_t* hb = hbuf(T);
             // fc2, transposed: output columns 32 t + i (A, from LDS) x the row's hidden values (B)
 #pragma unroll
@@ -675,11 +689,13 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
                 }
             }
         }
-        // the parts of the next step (issued a step ago) have landed; this step's own loads
-        // (two instructions per part, per wave) may stay in flight, except the rows of x
-        if (ld1 && ld2) __builtin_amdgcn_s_waitcnt(0x4 | (0x7 << 4) | (0xF << 8));  // vmcnt(4)
-        else if (ld1 || ld2) __builtin_amdgcn_s_waitcnt(0x2 | (0x7 << 4) | (0xF << 8));  // vmcnt(2)
-        else __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
+        // what the next step reads has landed (fc1 of tile j + 2 and fc2 of tile j, issued a
+        // step ago); this step's own loads (two instructions per part, per wave) may stay in
+        // flight, except the rows of x, waited for here in steps 7 and 8
+        if (j >= kMlpTiles - 1) __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));  // vmcnt(0)
+        else if (ld1 && ld2) __builtin_amdgcn_s_waitcnt(0x4 | (0x7 << 4) | (0xF << 8));    // vmcnt(4)
+        else if (ld1 || ld2) __builtin_amdgcn_s_waitcnt(0x2 | (0x7 << 4) | (0xF << 8));    // vmcnt(2)
+        else __builtin_amdgcn_s_waitcnt(0x0 | (0x7 << 4) | (0xF << 8));                   // vmcnt(0)
         __syncthreads();  // every wave is done with this step's parts
     }
     // lane (i, h) of a consumer holds fc2 of row grp * 32 + i at columns 32 t + 8 v + 4 h +
