@@ -133,6 +133,14 @@ def fp32_accuracy(samples):
     return out
 
 
+def lines_desc(off):
+    """'256 lines x T=120', or '29 lines, T=20..120' for lines of several lengths."""
+    t = np.diff(np.asarray(off, np.int64))
+    if t.size and t.min() == t.max():
+        return f"{t.size} lines x T={int(t[0])}"
+    return f"{t.size} lines, T={int(t.min()) if t.size else 0}..{int(t.max()) if t.size else 0}"
+
+
 def cpu_baseline(wk, q, s, seconds, gpu=None):
     """The oracle's line-parallel head (one line per worker, inner serial, as
     src/pipeline.rs:417-433): whole passes over the same batch, repeated to about
@@ -154,7 +162,7 @@ def cpu_baseline(wk, q, s, seconds, gpu=None):
     dt = time.perf_counter() - t0
     out = {"value": round(passes * rows / dt, 1), "unit": "rows/s", "cores": threads, "kind": "port",
            "cpu_model": cpu_model(),
-           "sample": f"{passes} passes over the batch ({lines} lines x T=120 = {rows} rows each, "
+           "sample": f"{passes} passes over the batch ({lines_desc(off)} = {rows} rows each, "
                      f"{passes * rows} rows), INT8 AVX2 path of the reference restated in C, one line per "
                      f"OpenMP thread, {dt:.1f} s"}
     if gpu is not None:
@@ -604,7 +612,7 @@ def main():
             "vs_baseline": None,
             "dtype": MODE_NAMES[rmode] + " MFMA, f32 accumulate, int8 weights" if rmode else "f32 FMA, int8 weights",
             "data": "synthetic (seeded N(0,1) activations, N(0,0.05^2) weights packed to INT8 on the GPU)",
-            "config": {"workload": f"{args.workload}: {lines} lines x T=120, m={m}, k={k}, n={n}, fused "
+            "config": {"workload": f"{args.workload}: {lines_desc(wk['line_off'])}, m={m}, k={k}, n={n}, fused "
                                    "projection+softmax-max+argmax+CTC",
                        "mode": MODE_NAMES[mode] + (f" ({MODE_NAMES[rmode]})" if mode == 5 else ""),
                        "guarded_rows": int(head.guarded_rows(a, rmode).sum()) if rmode in TERMS else 0,

@@ -568,7 +568,7 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t p_best, p_sum, p_idx, row_max, row_inv, guard_header, guard_rows, total;
+    size_t p_best, p_sum, p_idx, row_max, row_inv, guard_header, guard_rows, skip, total;
 };
 // The guard header sits at offset 0 whatever m and nsplit are, so a workspace reused for
 // batches of other sizes finds there the header its previous call left (emptied by that
@@ -584,7 +584,8 @@ WsLayout ws_layout(int64_t m, int nsplit) {
     L.row_max = L.p_idx + pm;
     L.row_inv = L.row_max + rm;
     L.guard_rows = L.row_inv + rm;
-    L.total = L.guard_rows + rm;
+    L.skip = L.guard_rows + rm;  // a byte per row block of 128 rows or more
+    L.total = L.skip + align_up((size_t)((m + 127) / 128));
     return L;
 }
 
@@ -613,7 +614,8 @@ Guard make_guard(const ppocr_rh* h, int cfg, const WsLayout& L, uint8_t* ws, int
                  h->range_ok ? h->range_limit : 0.0f,
                  h->range_ok ? h->range_ss : 0.0f,
                  h->range_ok,
-                 h->fma};
+                 h->fma,
+                 ws + L.skip};
 }
 
 // The tile records configuration cfg reads.

@@ -19,6 +19,130 @@ static int grid_blocks(int mblocks, int nsplit, bool rows_on_one_xcd) {
     return ((mblocks + r8 - 1) / r8) * 8;
 }
 
+// Row blocks of the statistics pass whose rows the guard surely sends to the rescue: each
+// row's max|a| (exact, as the pass computes it) and sum of squares in fp64 (exact products),
+// and the row is sure when max|a| > prec, or max|a| > range_amax and the sum exceeds
+// range_ss by 1e-4 (the pass sums the squares in fp32 in its own order, within 1e-5 of the
+// exact sum for k <= 120): a sure row is one the pass's own test flags.  A block of sure rows
+// is marked in skip and its rows listed here (one atomic per workgroup); the pass then skips
+// the block, and lists the flagged rows of the other blocks itself.  A NaN never makes a row
+// sure.  Rows [rows][k]: eight lanes per row, eight consecutive rows per wave and load, so a
+// wave reads whole lines of 8 x 4k bytes; channels-first rows ([lines][k][T], vec = -T): one
+// thread per row, consecutive rows being consecutive floats of each channel.
+__device__ __forceinline__ bool guard_sure(float amax, double ss, const GuardLimits& lim) {
+    return amax > lim.prec || (amax > lim.range_amax && ss > (double)lim.range_ss * (1.0 + 1e-4));
+}
+
+// Rows [rows][k], k <= 128, of one workgroup of guard_scan_kernel: a lane reads columns
+// 4 sub + 32 j (V4: float4) or sub + 8 j (scalars) of two rows, every load issued (at a clamped
+// address) before the first use and the values outside the rows zeroed after it.
+template <bool V4>
+__device__ __forceinline__ bool guard_scan_rows(const float* __restrict__ a, int64_t m, int k,
+                                                const GuardLimits& lim, int rpb, int64_t row0, int tid) {
+    const int sub = tid & 7;                             // lane within the row's eight
+    const int r_in = (tid >> 6) * 8 + ((tid >> 3) & 7);  // wave w reads rows 8w..8w+7 of each 32
+    bool sure = true;
+    for (int i = 0; i < rpb; i += 64) {
+        float v[2][16];
+        bool live[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t row = row0 + i + 32 * h + r_in;
+            live[h] = i + 32 * h + r_in < rpb && row < m;
+            const float* rp = a + (live[h] ? row : row0) * (int64_t)k;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (V4) {
+                    const int c = min(4 * sub + 32 * j, k - 4);
+                    const float4 x = *reinterpret_cast<const float4*>(rp + c);
+                    v[h][4 * j] = x.x;
+                    v[h][4 * j + 1] = x.y;
+                    v[h][4 * j + 2] = x.z;
+                    v[h][4 * j + 3] = x.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[h][4 * j + e] = rp[min(sub + 32 * j + 8 * e, k - 1)];
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float amax = 0.0f;
+            double ss = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int c = V4 ? 4 * sub + 32 * j + e : sub + 32 * j + 8 * e;
+                    const float x = c < k ? v[h][4 * j + e] : 0.0f;
+                    amax = fmaxf(amax, __builtin_fabsf(x));
+                    ss = fma((double)x, (double)x, ss);
+                }
+            }
+            // the eight lanes of a row are consecutive, and every lane takes part in the shuffles
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+                ss += __shfl_xor(ss, o, 64);
+            }
+            if (live[h]) sure = sure && guard_sure(amax, ss, lim);
+        }
+    }
+    return sure;
+}
+
+__global__ __launch_bounds__(256) void guard_scan_kernel(const float* __restrict__ a, int64_t m, int k, int vec,
+                                                         GuardLimits lim, int rpb, uint8_t* __restrict__ skip,
+                                                         unsigned long long* __restrict__ guard_header,
+                                                         int* __restrict__ guard_rows, unsigned epoch, int capacity) {
+    __shared__ unsigned s_base;
+    const int64_t blk = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t row0 = blk * rpb;
+    bool sure = true;  // rows past the batch do not hold a block back
+    if (vec < 0) {
+        const int64_t row = row0 + tid;
+        if (tid < rpb && row < m) {
+            const int64_t T = -(int64_t)vec;
+            const int64_t line = row / T;
+            const float* rp = a + line * T * k + (row - line * T);
+            float amax = 0.0f;
+            double ss = 0.0;
+            for (int kk = 0; kk < k; ++kk) {
+                const float x = rp[kk * T];
+                amax = fmaxf(amax, __builtin_fabsf(x));
+                ss = fma((double)x, (double)x, ss);
+            }
+            sure = guard_sure(amax, ss, lim);
+        }
+    } else if (vec > 0) {
+        sure = guard_scan_rows<true>(a, m, k, lim, rpb, row0, tid);
+    } else {
+        sure = guard_scan_rows<false>(a, m, k, lim, rpb, row0, tid);
+    }
+    if (!__syncthreads_and(sure ? 1 : 0)) {
+        if (tid == 0) skip[blk] = 0;
+        return;
+    }
+    if (tid == 0) {
+        const int64_t nrows = min((int64_t)rpb, m - row0);
+        unsigned long long cur = __hip_atomic_load(guard_header, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while ((unsigned)(cur >> 32) != epoch) {
+            const unsigned long long prev = atomicCAS(guard_header, cur, (unsigned long long)epoch << 32);
+            if (prev == cur) break;
+            cur = prev;  // another workgroup changed it first; look again
+        }
+        s_base = (unsigned)atomicAdd(guard_header, (unsigned long long)nrows);
+        skip[blk] = 1;
+    }
+    __syncthreads();
+    const int64_t row = row0 + tid;
+    if (tid < rpb && row < m) {
+        const int pos = (int)(s_base + (unsigned)tid);
+        if (pos >= 0 && pos < capacity) guard_rows[pos] = (int)row;
+    }
+}
+
 // Sets the guard list's header to (epoch, 0) before a pass that is not followed by a merge.
 __global__ void guard_reset_kernel(unsigned long long* guard_header, unsigned epoch) {
     *guard_header = (unsigned long long)epoch << 32;
@@ -131,8 +255,8 @@ static int rows_nsplit(int64_t mblocks) {
 // rescue costs the launch whatever the grid, and a heavy one (a head with large weight
 // outliers guards many rows) needs the whole GPU.
 constexpr int kRescueSlots = 128;
-// Precision limits below it make the two-term bf16 main pass skip row blocks whose rows all
-// go to the rescue.
+// Precision limits below it make the two-term bf16 main pass skip the row blocks whose rows
+// all go to the rescue (guard_scan_kernel marks them).
 constexpr float kVoteLimit = 4.0f;
 
 // How the rows flagged by the precision guard of `cfg` are recomputed: an INT8 head's two
@@ -276,10 +400,17 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
                   guarded ? guard->epoch : 0u,
                   guarded ? guard->capacity : 0};
     // A precision limit below typical |a| (rows of unit variance reach max|a| ~ 2.5-3.5 over
-    // 120 values) sends nearly every row to the rescue: the main pass then votes per row
-    // block and skips the blocks it would compute for nothing.  Above the limit the vote
-    // would only cost time (0.3% on the dense batch, 2% on one line): the other variant runs.
-    x.vote = guarded && cfg == CFG_Q2 && rcfg == CFG_Q3 && guard->amax_limit < kVoteLimit;
+    // 120 values) sends nearly every row to the rescue: a scan then marks the row blocks whose
+    // rows are all surely rescued, and the main pass skips them instead of computing them for
+    // nothing.  Above the limit whole blocks are not flagged, and the scan would only cost
+    // time: the plain main pass runs.
+    if (guarded && cfg == CFG_Q2 && rcfg == CFG_Q3 && guard->amax_limit < kVoteLimit && guard->skip && rpb <= 256 &&
+        rpb % 32 == 0 && k <= 128) {
+        guard_scan_kernel<<<(unsigned)mblocks, 256, 0, st>>>(a, m, (int)k, vec, x.lim, rpb, guard->skip, guard->header,
+                                                            guard->rows, guard->epoch, guard->capacity);
+        PPOCR_HIP(hipGetLastError());
+        x.skip = guard->skip;
+    }
     const int mb = rpb / (32 * kStatsWaves);
     if (int e = call_stats_main(cfg, tg.G, x, mb, noref, (unsigned)grid, st)) return e;
     if (guarded && rcfg == kRescueFma) {

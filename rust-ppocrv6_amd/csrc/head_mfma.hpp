@@ -485,12 +485,6 @@ __device__ __forceinline__ void guard_append(float amax, float ss, const GuardLi
     const bool hit = h == 0 && valid && (amax > lim.prec || (amax > lim.range_amax && ss > lim.range_ss));
     guard_push(hit, row, guard_header, guard_rows, epoch, capacity);
 }
-// The same test, returned on both lanes of the row (the sums agree: addition commutes).
-__device__ __forceinline__ bool guard_hit(float amax, float ss, const GuardLimits& lim, bool valid) {
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    ss += __shfl_xor(ss, 32, 64);
-    return valid && (amax > lim.prec || (amax > lim.range_amax && ss > lim.range_ss));
-}
 
 // Entries of the guard list for this call's epoch (0 for a header of another epoch).
 __device__ __forceinline__ int guard_count_of(const unsigned long long* guard_header, unsigned epoch, int capacity) {
@@ -681,21 +675,10 @@ __device__ __forceinline__ void args_now(const T&... x) {
     (arg_now(x), ...);
 }
 
-// LDS of the main statistics pass: the tile ring, each wave's saved best tile and, in the
-// voting variant, one flag per wave (built where 16 more bytes keep the workgroups per CU:
-// 2, or 3 for the two-term modes' one-block kernel; 160 KiB per CU, 512-byte granules).
+// LDS of the main statistics pass: the tile ring and each wave's saved best tile.
 template <int C, int G, int MB>
-constexpr int main_vote_off() {
-    return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
-}
-template <int C, int G, int MB>
-constexpr bool main_vote_fits() {
-    constexpr int per_cu = (MB == 1 && (C == CFG_Q2 || C == CFG_H2)) ? 3 : 2;
-    return (main_vote_off<C, G, MB>() + 16 + 511) / 512 * 512 * per_cu <= 160 * 1024;
-}
-template <int C, int G, int MB, bool VOTE>
 constexpr int main_lds_bytes() {
-    return main_vote_off<C, G, MB>() + (VOTE ? 16 : 0);
+    return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
 }
 
 template <int C, int G, int MB, bool GATHER, bool NOREF, bool VOTE = false, int OCC = 8 / kStatsWaves>
@@ -703,7 +686,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
     int* __restrict__ p_idx, GuardLimits lim, unsigned long long* __restrict__ guard_header,
-    int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap) {
+    int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap, const uint8_t* __restrict__ skip) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
     constexpr int RPB = 32 * kStatsWaves * MB;
@@ -715,6 +698,12 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     int mbi, chunk;
     map_block<true>(blockIdx.x, nsplit, &mbi, &chunk);
     if (mbi >= mblocks) return;
+    // VOTE: a row block whose rows the guard surely sends to the rescue (guard_scan_kernel,
+    // which also listed them) is skipped: the rescue pass overwrites all of their partials,
+    // in every chunk
+    if constexpr (VOTE && !GATHER) {
+        if (skip[mbi]) return;
+    }
     const int t0 = chunk * tiles_per_chunk;
     const int t1 = min(t0 + tiles_per_chunk, tiles);
     // one row block, or (GATHER) the row blocks of a device-side row list, mblocks apart
@@ -727,11 +716,6 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const int lb = i * 16 + h * 512;
     // this lane's saved values of its best tile: [block][quad][lane] x 4 floats
     f32x4* save = reinterpret_cast<f32x4*>(lds + kRing * GE::BUF) + wave * (MB * 4 * 64) + lane;
-    // VOTE: one flag per wave, whether it holds a row the rescue pass does not recompute
-    constexpr bool kVote = VOTE && !GATHER;
-    static_assert(!kVote || main_vote_fits<C, G, MB>(), "no LDS left for the vote");
-    static_assert(kStatsWaves == 4, "the vote is read as one u32x4");
-    unsigned* vote = reinterpret_cast<unsigned*>(lds + main_vote_off<C, G, MB>());
 
     auto row_block = [&](int64_t blk) {
         const int64_t mrow0 = blk * RPB + wave * (32 * MB);
@@ -765,29 +749,13 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                 arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
                 act_issue<C, G>(a, valid[b] ? arow[b] : 0, k, vec, h, araw[b]);
             }
-            [[maybe_unused]] bool keep = false;  // a row of this lane the rescue pass does not recompute
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
                 float amax = 0.0f, ss = 0.0f;
                 act_split_all<C, G>(araw[b], h, bf[b], amax, ss);
-                if constexpr (kVote) {
-                    if (guard_header) {
-                        const bool hit = guard_hit(amax, ss, lim, valid[b]);
-                        if (chunk == 0)
-                            guard_push(h == 0 && hit, arow[b], guard_header, guard_rows, guard_epoch, guard_cap);
-                        keep = keep || (valid[b] && !hit);
-                    } else {
-                        keep = keep || valid[b];
-                    }
-                } else if (guard_header && chunk == 0) {
+                if (guard_header && chunk == 0)
                     guard_append(amax, ss, lim, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch,
                                  guard_cap);
-                }
-            }
-            // the vote on skipping the block (after the ring barrier below)
-            if constexpr (kVote) {
-                const bool wave_keep = __any(keep);
-                if (guard_header && lane == 0) vote[wave] = wave_keep ? 1u : 0u;
             }
         }
 
@@ -805,21 +773,6 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
         constexpr int kLead = (kRing - 3) * kOps;
         if (t0 < t1) {
             ring_barrier<kLead>();  // tiles t0 and t0+1 are in LDS
-            // Every row of the block on the guard list (a head whose weight outliers put the
-            // limit below typical activations): the rescue pass overwrites all of their
-            // partials, in every chunk, so the tiles are skipped.  Each chunk's workgroup
-            // tests the same rows with the same arithmetic, so they agree, and every wave
-            // reads the same flags (written before the barrier, in LDS nothing else uses).
-            // The staged tile loads land before the workgroup ends.
-            if constexpr (kVote) {
-                if (guard_header) {
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(vote);
-                    if ((v[0] | v[1] | v[2] | v[3]) == 0u) {
-                        vm_wait<0>();
-                        return;
-                    }
-                }
-            }
             f32x16 acc_a[MB], acc_b[MB];
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
@@ -1172,10 +1125,9 @@ constexpr int mb_of() {
 }
 template <int C, int G, int MB, bool GATHER, bool NOREF, bool VOTE = false>
 static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
-    stats_main_kernel<C, G, MB, GATHER, NOREF, VOTE>
-        <<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB, VOTE>(), st>>>(
+    stats_main_kernel<C, G, MB, GATHER, NOREF, VOTE><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
         x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.p_best, x.p_sum, x.p_idx, x.lim,
-        x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap);
+        x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap, x.skip);
 }
 
 // Main statistics pass.  The two-term modes run mb = 1 (small batches) or 2 blocks per
@@ -1183,9 +1135,9 @@ static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
 template <int C, int G>
 int stats_main_cfg(const StatsLaunch& x, int mb, bool noref, unsigned grid, hipStream_t st) {
     if constexpr (C == CFG_Q2) {
-        // the voting variants only where the host asks for them (a low precision limit)
+        // the variants that skip listed row blocks only where the host asks for them
         if (mb == 1) {
-            if (x.vote) {
+            if (x.skip) {
                 if (noref) stats_go<C, G, 1, false, true, true>(x, grid, st);
                 else stats_go<C, G, 1, false, false, true>(x, grid, st);
             } else {
@@ -1193,7 +1145,7 @@ int stats_main_cfg(const StatsLaunch& x, int mb, bool noref, unsigned grid, hipS
                 else stats_go<C, G, 1, false, false>(x, grid, st);
             }
         } else {
-            if (x.vote) {
+            if (x.skip) {
                 if (noref) stats_go<C, G, 2, false, true, true>(x, grid, st);
                 else stats_go<C, G, 2, false, false, true>(x, grid, st);
             } else {

@@ -55,8 +55,9 @@ struct StatsLaunch {
     int* guard_rows;
     unsigned guard_epoch;
     int guard_cap;
-    // the two-term bf16 main pass skips row blocks the guard sends whole to the rescue
-    bool vote = false;
+    // per row block of the main pass: 1 when the guard surely sends all of its rows to the
+    // rescue (guard_scan_kernel); null: no block is skipped
+    const uint8_t* skip = nullptr;
 };
 struct RowsLaunch {
     const float* a;
@@ -105,6 +106,7 @@ struct Guard {
     float range_ss_limit;    // or rows with ||a||_2^2 up to it (L2 bound)
     bool stats_noref;
     const FmaWeights& fma;  // the head's fp32 weights, for a rescue in fp32 FMA
+    uint8_t* skip;          // a byte per 128 rows: the statistics pass's skipped row blocks
 };
 
 // Supported group counts (k = 113..120 and k = 73..80, the PP-OCRv6 small and tiny heads).

@@ -402,6 +402,49 @@ def test_stress_1024_fused(orc, rh, mode):
     assert_close_rel(got["maxprob"][sample], ref["maxprob"], "stress maxprob", row_scale=rel_scale(lg))
 
 
+@pytest.mark.parametrize("m", [1500, 9000])
+def test_skipped_row_blocks_beside_computed_ones(orc, rh, m):
+    """BF16X2 on the stress head (precision limit 1.59, below the max|a| of unit-variance
+    rows): a scan marks the row blocks whose rows all go to the rescue, lists their rows, and
+    the main pass skips those blocks.  Rows scaled x0.3 (max|a| under the limit) hold their
+    blocks back; the main pass computes those blocks and lists their other rows itself.  The
+    1500-row batch runs 128-row blocks, the 9000-row one 256-row blocks.  Decode (argmax,
+    maximum probability, sequences) and probabilities against the oracle on the rows of the
+    held-back blocks and a seeded sample of the others; the channels-first entry bit for bit
+    against the row entry."""
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights(stress=True)
+    q, s = orc.pack_int8(w_t)
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((m, 120)).astype(np.float32)
+    rb = 128 if m <= 8192 else 256
+    held = np.array([1, 5, (m - 1) // rb])  # row blocks held back, the last (partial) one among them
+    small = np.concatenate([b * rb + rng.choice(min(rb, m - b * rb), 3, replace=False) for b in held])
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    prec, ra, _ = head.guard_limits(2)
+    print(f"m={m}: limits prec {prec:.3f} range_amax {ra:.3f}", flush=True)
+    # below both max|a| limits the row is not guarded, whatever its norm
+    a[small] *= (np.float32(0.9 * min(prec, ra)) / np.abs(a[small]).max(axis=1))[:, None]
+    guarded = head.guarded_rows(a, 2)
+    print(f"m={m}: {int(guarded.sum())} of {m} rows guarded, {small.size} held back", flush=True)
+    assert not guarded[small].any() and guarded.mean() > 0.9
+    off = split_lines(m, 120)
+    got = head.decode(a, off, 2)
+    probs = head.probs(a, 2)
+    # the same rows channels first ([lines][k][T], T = 60): the scan reads them one thread per row
+    nct = head.decode_nct(np.ascontiguousarray(a.reshape(m // 60, 60, 120).transpose(0, 2, 1)), 2)
+    head.close()
+    assert np.array_equal(nct["idx"], got["idx"])
+    assert np.array_equal(nct["maxprob"].view(np.uint32), got["maxprob"].view(np.uint32))
+    in_held = np.concatenate([np.arange(b * rb, min(m, (b + 1) * rb)) for b in held])
+    sample = np.unique(np.concatenate([in_held, rng.choice(m, 600, replace=False)]))
+    ref = orc.rechead_lines(a[sample], split_lines(sample.size), q, s, bias, want_probs=True)
+    lg = f64_logits_q(a[sample], q, s, bias)
+    check_argmax(got["idx"][sample], ref["idx"], top2_gap(lg), label=f"skipped blocks m={m}")
+    assert_close_rel(got["maxprob"][sample], ref["maxprob"], "skipped blocks maxprob", row_scale=rel_scale(lg))
+    assert_close_rel(probs[sample], ref["probs"], "skipped blocks probs", row_scale=rel_scale(lg))
+
+
 def test_precision_guard_on_large_activations(orc, rh):
     """BF16X2 recomputes rows whose max|a| * max|w| exceeds the guard with three terms:
     x50 rows against the stress weights (+-5 outliers) stay as accurate as BF16X3."""
