@@ -496,6 +496,7 @@ def main():
             rh._check(L.ppocr_rn_forward_dev(nk.handle, dfx.p, dsc.p, m, doff.p, lines, rh.NECK_ROWS, dfeat.p,
                                              dnws.p, nws, st))
 
+        ramp(neck_step)
         ms_n, _ = timed(neck_step, stream, args.steps, args.warmup)
         steps_of = np.diff(wk["line_off"])
         nflops = float(sum(int(t) * wl.neck_flops_per_row(int(t)) for t in steps_of))
@@ -519,6 +520,7 @@ def main():
                 rh._check(L.ppocr_rh_decode_dev(head.handle, dfeat.p, m, doff.p, lines, hm, didx.p, dmp.p, dseq.p,
                                                 dlen.p, dscore.p, dhws.p, hws, st))
 
+            ramp(neck_head_step)
             ms_nh, _ = timed(neck_head_step, stream, args.steps, args.warmup)
             rm = head.auto_mode() if hm == 5 else hm
             neck["neck_then_head"][MODE_NAMES[hm] + (f" ({MODE_NAMES[rm]})" if hm == 5 else "")] = {
