@@ -114,11 +114,11 @@ struct FVec<4> {
 // before the first store: with the stores in between, each load would wait for the one
 // before it.
 template <bool SWISH, bool RES, int TPW>
-__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TPW], int64_t rbase, int half, int col, int64_t m,
-                                              int n, const float* __restrict__ bias, const float* res, float* out) {
+__device__ __forceinline__ void gemm_epilogue_with_bias(const f32x16 (&acc)[TPW],
+                                                        const typename FVec<TPW>::type& bc, int64_t rbase, int half,
+                                                        int col, int64_t m, int n, const float* res, float* out) {
     using VT = typename FVec<TPW>::type;
     if (col >= n) return;
-    const VT bc = *reinterpret_cast<const VT*>(bias + col);
     VT rv[16];
     if constexpr (RES) {
 #pragma unroll
@@ -153,6 +153,15 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TPW], int64_t 
             if (rr < m) *reinterpret_cast<VT*>(out + rr * n + col) = value(r);
         }
     }
+}
+
+template <bool SWISH, bool RES, int TPW>
+__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TPW], int64_t rbase, int half, int col, int64_t m,
+                                              int n, const float* __restrict__ bias, const float* res, float* out) {
+    using VT = typename FVec<TPW>::type;
+    if (col >= n) return;
+    gemm_epilogue_with_bias<SWISH, RES, TPW>(acc, *reinterpret_cast<const VT*>(bias + col), rbase, half, col, m, n, res,
+                                             out);
 }
 
 template <int TPW>
@@ -280,13 +289,17 @@ template <int K>
 constexpr int gemm16_kp() {
     return K <= 128 ? 128 : 256;
 }
-template <int K, bool LN, int TPW>
+// NCB > 1: a workgroup computes NCB column blocks of 32 TPW columns in turn, its rows'
+// LayerNorm and halves computed once; the weights of block c + 1 are staged (a second LDS
+// buffer) while block c computes and stores.
+template <int K, bool LN, int TPW, int NCB = 1>
 constexpr size_t gemm16_lds_bytes() {
-    return (size_t)2 * (32 * TPW) * gemm16_kp<K>() * 2 + (LN ? 2 * K * 4 : 0);
+    return (size_t)(NCB > 1 ? 2 : 1) * 2 * (32 * TPW) * gemm16_kp<K>() * 2 + (LN ? 2 * K * 4 : 0);
 }
 
-// TPW: tiles of 32 columns per wave, so 32 TPW columns per workgroup.
-template <int K, bool LN, bool SWISH, bool RES, int TPW>
+// TPW: tiles of 32 columns per wave, so 32 TPW columns per column block; NCB column blocks
+// per workgroup (NCB > 1 needs n to be a multiple of 32 TPW, and no residual).
+template <int K, bool LN, bool SWISH, bool RES, int TPW, int NCB = 1>
 __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __restrict__ a, int64_t m,
                                                           const uint16_t* __restrict__ wt, int n,
                                                           const float* __restrict__ bias,
@@ -296,26 +309,32 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
     constexpr int KP = gemm16_kp<K>(), S = KP / 16, NCH = KP / 8, NC = 32 * TPW;
     static_assert(K % 8 == 0 && K <= KP, "8-element chunks of k");
     static_assert(TPW == 2 || TPW == 4, "tiles per wave");
-    extern __shared__ __align__(16) uint8_t ls16[];  // [2][NC][NCH] chunks of 16 bytes, then (LN) [2][K] floats
+    static_assert(NCB == 1 || !RES, "several column blocks per workgroup: no residual loads in the epilogue");
+    // [NCB > 1 ? 2 : 1][2][NC][NCH] chunks of 16 bytes, then (LN) [2][K] floats
+    extern __shared__ __align__(16) uint8_t ls16[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    const int n0 = blockIdx.y * NC;
-    // stage both planes: chunk e of the stage = plane e / (NC NCH), column (e / NCH) % NC,
-    // slot e % NCH, holding the column's chunk slot ^ ((column / TPW) % 8); a column past n
-    // reloads column 0 (its results are never stored, and each output column depends only
-    // on its own weights)
+    // stage both planes of column block cb into buffer buf: chunk e of the stage = plane
+    // e / (NC NCH), column (e / NCH) % NC, slot e % NCH, holding the column's chunk
+    // slot ^ ((column / TPW) % 8); a column past n reloads column 0 (its results are never
+    // stored, and each output column depends only on its own weights)
     constexpr int CH = 2 * NC * NCH;
+    constexpr size_t STAGE = (size_t)CH * 16;
     static_assert(CH % 64 == 0 && NCH % 8 == 0, "whole instructions; slots permuted within groups of 8");
-    for (int x = wave; x < CH / 64; x += 4) {
-        const int e = 64 * x + lane;
-        const int p = e / (NC * NCH), c = (e / NCH) % NC, sl = e % NCH;
-        const int col = n0 + c < n ? n0 + c : 0;
-        const uint16_t* src = wt + ((size_t)p * n + col) * KP + 8 * (sl ^ ((c / TPW) & 7));
-        __builtin_amdgcn_global_load_lds(
-            static_cast<const void*>(src),
-            reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(ls16 + 1024 * x)),
-            16, 0, 0);
-    }
-    const float* lnl = reinterpret_cast<const float*>(ls16 + (size_t)CH * 16);
+    auto stage = [&](int cb, int buf) {
+        const int n0 = ((int)blockIdx.y * NCB + cb) * NC;
+        for (int x = wave; x < CH / 64; x += 4) {
+            const int e = 64 * x + lane;
+            const int p = e / (NC * NCH), c = (e / NCH) % NC, sl = e % NCH;
+            const int col = n0 + c < n ? n0 + c : 0;
+            const uint16_t* src = wt + ((size_t)p * n + col) * KP + 8 * (sl ^ ((c / TPW) & 7));
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                             reinterpret_cast<__attribute__((address_space(3))) void*>(
+                                                 reinterpret_cast<uintptr_t>(ls16 + buf * STAGE + 1024 * x)),
+                                             16, 0, 0);
+        }
+    };
+    stage(0, 0);
+    const float* lnl = reinterpret_cast<const float*>(ls16 + (NCB > 1 ? 2 : 1) * STAGE);
     if constexpr (LN) {
         static_assert(K % 4 == 0 && K / 2 <= 64, "LayerNorm parameters in one instruction");
         if (wave == 0 && lane < K / 2) {
@@ -391,29 +410,66 @@ __global__ __launch_bounds__(256, 2) void neck_gemm16_kernel(const float* __rest
             alo[s][e] = __builtin_bit_cast(unsigned short, xl);
         }
     }
-    f32x16 acc[TPW];
+    const int64_t rbase = (int64_t)blockIdx.x * kGemmRows + wave * 32;
+    using VT = typename FVec<TPW>::type;
+#pragma unroll 1
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int n0 = ((int)blockIdx.y * NCB + cb) * NC;
+        if (n0 >= n) break;  // uniform over the workgroup
+        // this block's bias, loaded before the next block's weights (kept in that order), so
+        // that the stores wait for it alone
+        const int bcol = n0 + TPW * i;
+        const VT bc = *reinterpret_cast<const VT*>(bias + (bcol < n ? bcol : 0));
+        __builtin_amdgcn_sched_barrier(0);
+        // NCB > 1: the next block's weights, loaded into registers while this block computes
+        // and stores, then written to the other LDS buffer (the compiler waits for these
+        // loads alone, not for the stores issued after them)
+        constexpr int PER = NCB > 1 ? CH / 64 / 4 : 1;
+        u32x4 nx[PER];
+        const bool next = NCB > 1 && cb + 1 < NCB && n0 + NC < n;
+        if (next) {
+            const int n1 = n0 + NC;
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) acc[t] = f32x16{};
-    // column TPW i + t, chunk 2 s + h: slot (2 s + h) ^ (i % 8)
-    const uint8_t* whi = ls16 + (size_t)(TPW * i) * NCH * 16;
-    const uint8_t* wlo = whi + (size_t)NC * NCH * 16;
+            for (int j = 0; j < PER; ++j) {
+                const int e = 64 * (wave + 4 * j) + lane;
+                const int p = e / (NC * NCH), c = (e / NCH) % NC, sl = e % NCH;
+                const int col = n1 + c < n ? n1 + c : 0;
+                nx[j] = *reinterpret_cast<const u32x4*>(wt + ((size_t)p * n + col) * KP + 8 * (sl ^ ((c / TPW) & 7)));
+            }
+        }
+        f32x16 acc[TPW];
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-        const int sl = (2 * s + h) ^ (i & 7);
+        for (int t = 0; t < TPW; ++t) acc[t] = f32x16{};
+        // column TPW i + t, chunk 2 s + h: slot (2 s + h) ^ (i % 8)
+        const uint8_t* whi = ls16 + (size_t)(cb & 1) * STAGE + (size_t)(TPW * i) * NCH * 16;
+        const uint8_t* wlo = whi + (size_t)NC * NCH * 16;
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) {
-            const u16x8 bh = *reinterpret_cast<const u16x8*>(whi + ((size_t)t * NCH + sl) * 16);
-            const u16x8 bl = *reinterpret_cast<const u16x8*>(wlo + ((size_t)t * NCH + sl) * 16);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
-                                                            __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
-                                                            __builtin_bit_cast(f16x8, bl), acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, alo[s]),
-                                                            __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
+        for (int s = 0; s < S; ++s) {
+            const int sl = (2 * s + h) ^ (i & 7);
+#pragma unroll
+            for (int t = 0; t < TPW; ++t) {
+                const u16x8 bh = *reinterpret_cast<const u16x8*>(whi + ((size_t)t * NCH + sl) * 16);
+                const u16x8 bl = *reinterpret_cast<const u16x8*>(wlo + ((size_t)t * NCH + sl) * 16);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
+                                                                __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ahi[s]),
+                                                                __builtin_bit_cast(f16x8, bl), acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, alo[s]),
+                                                                __builtin_bit_cast(f16x8, bh), acc[t], 0, 0, 0);
+            }
+        }
+        gemm_epilogue_with_bias<SWISH, RES, TPW>(acc, bc, rbase, h, bcol, m, n, res, out);
+        if constexpr (NCB > 1) {
+            if (next) {
+                uint8_t* dst = ls16 + (size_t)((cb + 1) & 1) * STAGE;
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                    *reinterpret_cast<u32x4*>(dst + (size_t)1024 * (wave + 4 * j) + 16 * lane) = nx[j];
+            }
+            // the next block's weights are in LDS, and no wave still reads this block's
+            __syncthreads();
         }
     }
-    gemm_epilogue<SWISH, RES, TPW>(acc, (int64_t)blockIdx.x * kGemmRows + wave * 32, h, n0 + TPW * i, m, n, bias, res,
-                                   out);
 }
 
 // ---------------------------------------------------------------- MLP
@@ -1191,22 +1247,24 @@ __global__ __launch_bounds__(256) void neck_final_kernel(const float* __restrict
     for (int e = 0; e < kLnQuad; ++e) orow[e] = v[e] + sr[e];
 }
 
-// Tiles of 32 columns per wave of the fp16-halves GEMMs: 2, so 64 columns per workgroup
-// (qkv's 384 columns in 6 column blocks, 1440 workgroups for the dense batch; proj's 120 in
-// 2), with 32 KB of weights per workgroup, so up to 3 workgroups per CU.
+// Tiles of 32 columns per wave of the fp16-halves GEMMs: 2, so 64-column blocks with 32 KB
+// of weights each.  proj (120 columns) runs a workgroup per column block; qkv (384 columns)
+// runs 3 column blocks per workgroup, the rows' LayerNorm and halves computed once per
+// workgroup (480 workgroups for the dense batch instead of 1440).
 constexpr int kGemm16TilesPerWave = 2;
 
-template <int K, bool LN, bool SWISH, bool RES>
+template <int K, bool LN, bool SWISH, bool RES, int NCB = 1>
 int gemm16_go(const float* a, int64_t m, const uint16_t* wt, int n, const float* bias, const float* ln_w,
               const float* ln_b, float eps, const float* res, float* out, hipStream_t st) {
     static_assert(gemm16_kp<K>() == neck_f16_kp(K), "the planes' padding");
-    constexpr int TPW = kGemm16TilesPerWave;
+    constexpr int TPW = kGemm16TilesPerWave, NC = 32 * TPW;
+    if (NCB > 1 && n % NC != 0) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: column blocks do not tile the columns");
     const int64_t gx = (m + kGemmRows - 1) / kGemmRows;
-    const int gy = (n + 32 * TPW - 1) / (32 * TPW);
+    const int gy = (n + NC * NCB - 1) / (NC * NCB);
     if (gx > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecNeckHip: too many rows");
-    neck_gemm16_kernel<K, LN, SWISH, RES, TPW>
-        <<<dim3((unsigned)gx, (unsigned)gy), 256, gemm16_lds_bytes<K, LN, TPW>(), st>>>(a, m, wt, n, bias, ln_w, ln_b,
-                                                                                     eps, res, out);
+    neck_gemm16_kernel<K, LN, SWISH, RES, TPW, NCB>
+        <<<dim3((unsigned)gx, (unsigned)gy), 256, gemm16_lds_bytes<K, LN, TPW, NCB>(), st>>>(
+            a, m, wt, n, bias, ln_w, ln_b, eps, res, out);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
@@ -1284,8 +1342,13 @@ int launch_neck(const NeckDev& nk, const float* x_in, const float* shortcut_in, 
         const NeckBlockDev& k = nk.block[b];
         const float* xr = b == 0 ? xin : x;
         // LN1 -> qkv
-        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, false, false>(xr, m, k.qkv_h, kNeckQkvPad, k.qkv_bp, k.ln1_w,
-                                                                    k.ln1_b, k.ln1_eps, nullptr, qkv, st)
+        // qkv's 6 column blocks in two workgroups per row block (480 workgroups for the dense
+        // batch; measured 0.1427 ms per forward, against 0.146 with all 6 in one workgroup, 0.150
+        // with 2 and 0.151 with a workgroup per block)
+        constexpr int kQkvBlocks = kNeckQkvPad / (32 * kGemm16TilesPerWave) / 2;
+        if (int e = nk.f16 ? gemm16_go<kNeckDim, true, false, false, kQkvBlocks>(xr, m, k.qkv_h, kNeckQkvPad, k.qkv_bp,
+                                                                                k.ln1_w, k.ln1_b, k.ln1_eps, nullptr,
+                                                                                qkv, st)
                            : gemm_go<kNeckDim, true, false, false>(xr, m, k.qkv_w, 3 * D, k.qkv_b, k.ln1_w, k.ln1_b,
                                                                    k.ln1_eps, nullptr, qkv, st))
             return e;
