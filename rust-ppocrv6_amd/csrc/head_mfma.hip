@@ -257,7 +257,7 @@ static int rows_nsplit(int64_t mblocks) {
 constexpr int kRescueSlots = 128;
 // Precision limits below it make the two-term bf16 main pass skip the row blocks whose rows
 // all go to the rescue (guard_scan_kernel marks them).
-constexpr float kVoteLimit = 4.0f;
+constexpr float kScanLimit = 4.0f;
 
 // How the rows flagged by the precision guard of `cfg` are recomputed: an INT8 head's two
 // activation terms become three bf16 terms (exact products with int8 weights); an FP32
@@ -404,7 +404,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
     // rows are all surely rescued, and the main pass skips them instead of computing them for
     // nothing.  Above the limit whole blocks are not flagged, and the scan would only cost
     // time: the plain main pass runs.
-    if (guarded && cfg == CFG_Q2 && rcfg == CFG_Q3 && guard->amax_limit < kVoteLimit && guard->skip && rpb <= 256 &&
+    if (guarded && cfg == CFG_Q2 && rcfg == CFG_Q3 && guard->amax_limit < kScanLimit && guard->skip && rpb <= 256 &&
         rpb % 32 == 0 && k <= 128) {
         guard_scan_kernel<<<(unsigned)mblocks, 256, 0, st>>>(a, m, (int)k, vec, x.lim, rpb, guard->skip, guard->header,
                                                             guard->rows, guard->epoch, guard->capacity);

@@ -681,7 +681,7 @@ constexpr int main_lds_bytes() {
     return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
 }
 
-template <int C, int G, int MB, bool GATHER, bool NOREF, bool VOTE = false, int OCC = 8 / kStatsWaves>
+template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false, int OCC = 8 / kStatsWaves>
 __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
@@ -698,10 +698,10 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     int mbi, chunk;
     map_block<true>(blockIdx.x, nsplit, &mbi, &chunk);
     if (mbi >= mblocks) return;
-    // VOTE: a row block whose rows the guard surely sends to the rescue (guard_scan_kernel,
+    // SKIP: a row block whose rows the guard surely sends to the rescue (guard_scan_kernel,
     // which also listed them) is skipped: the rescue pass overwrites all of their partials,
     // in every chunk
-    if constexpr (VOTE && !GATHER) {
+    if constexpr (SKIP && !GATHER) {
         if (skip[mbi]) return;
     }
     const int t0 = chunk * tiles_per_chunk;
@@ -1123,9 +1123,9 @@ template <int C>
 constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1 || C == CFG_H2) ? 2 : 1;
 }
-template <int C, int G, int MB, bool GATHER, bool NOREF, bool VOTE = false>
+template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false>
 static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
-    stats_main_kernel<C, G, MB, GATHER, NOREF, VOTE><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
+    stats_main_kernel<C, G, MB, GATHER, NOREF, SKIP><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
         x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.p_best, x.p_sum, x.p_idx, x.lim,
         x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap, x.skip);
 }

@@ -408,7 +408,8 @@ def test_skipped_row_blocks_beside_computed_ones(orc, rh, m):
     rows): a scan marks the row blocks whose rows all go to the rescue, lists their rows, and
     the main pass skips those blocks.  Rows scaled x0.3 (max|a| under the limit) hold their
     blocks back; the main pass computes those blocks and lists their other rows itself.  The
-    1500-row batch runs 128-row blocks, the 9000-row one 256-row blocks.  Decode (argmax,
+    1500-row batch runs 128-row blocks (its partial last block held back), the 9000-row one
+    256-row blocks (its partial last block skipped).  Decode (argmax,
     maximum probability, sequences) and probabilities against the oracle on the rows of the
     held-back blocks and a seeded sample of the others; the channels-first entry bit for bit
     against the row entry."""
@@ -418,7 +419,9 @@ def test_skipped_row_blocks_beside_computed_ones(orc, rh, m):
     rng = np.random.default_rng(41)
     a = rng.standard_normal((m, 120)).astype(np.float32)
     rb = 128 if m <= 8192 else 256
-    held = np.array([1, 5, (m - 1) // rb])  # row blocks held back, the last (partial) one among them
+    # row blocks held back: with 1500 rows the last (partial) one among them, with 9000 rows the
+    # last (40 rows) is skipped
+    held = np.array([1, 5, (m - 1) // rb] if m == 1500 else [1, 5])
     small = np.concatenate([b * rb + rng.choice(min(rb, m - b * rb), 3, replace=False) for b in held])
     head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
     prec, ra, _ = head.guard_limits(2)
@@ -437,7 +440,8 @@ def test_skipped_row_blocks_beside_computed_ones(orc, rh, m):
     assert np.array_equal(nct["idx"], got["idx"])
     assert np.array_equal(nct["maxprob"].view(np.uint32), got["maxprob"].view(np.uint32))
     in_held = np.concatenate([np.arange(b * rb, min(m, (b + 1) * rb)) for b in held])
-    sample = np.unique(np.concatenate([in_held, rng.choice(m, 600, replace=False)]))
+    last = np.arange(((m - 1) // rb) * rb, m)  # the partial last block, skipped or held back
+    sample = np.unique(np.concatenate([in_held, last, rng.choice(m, 600, replace=False)]))
     ref = orc.rechead_lines(a[sample], split_lines(sample.size), q, s, bias, want_probs=True)
     lg = f64_logits_q(a[sample], q, s, bias)
     check_argmax(got["idx"][sample], ref["idx"], top2_gap(lg), label=f"skipped blocks m={m}")
