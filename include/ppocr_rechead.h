@@ -233,7 +233,9 @@ int ppocr_rh_decode_dev(const ppocr_rh_t* h, const float* d_a, int64_t m, const 
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Scratch comes from a fixed 32 MiB device array per GPU, held until the process ends,
  * which covers m up to 245760 rows of the 18710-class head (PPOCR_ERR_INVALID_ARG beyond
- * what it holds).  All calls on one GPU share that array: calls that overlap on one GPU
+ * what it holds).  The array is part of the library's code object: every GPU the library's
+ * kernels are loaded on holds it, whether or not this entry is ever called, and
+ * ppocr_rh_device_bytes does not count it.  All calls on one GPU share that array: calls that overlap on one GPU
  * (other streams, other threads) race and must be serialised by the caller.  The first
  * call on a device takes the array's address and clears its list header on `stream`. */
 int ppocr_rh_decode_dev_noalloc(const ppocr_rh_t* h, const float* d_a, int64_t m, const int64_t* d_line_off,
