@@ -833,6 +833,7 @@ __global__ __launch_bounds__(512, 1) void neck_mlp16_kernel(const float* x, int6
 constexpr int kAttnKeys = 128;                 // keys per LDS block
 constexpr int kAttnKeyTiles = kAttnKeys / 16;  // 16-key tiles per block
 constexpr int kAttnQBlocks = 2;                // 16-query blocks per wave and pass
+constexpr int kAttnSubTiles = 4;               // key tiles per online-softmax step (fp16 kernel)
 constexpr int kVtStride = kAttnKeys + 4;
 
 __device__ __forceinline__ int perm_dim(int d) { return 4 * (d & 3) + (d >> 2); }
@@ -1028,7 +1029,8 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
     // the exponent of the softmax per unit of raw score: 2^-(eq + ek) log2(e)
     const float ec = ldexpf(1.4426950408889634f, -(eq + ek));
     static_assert(HD <= 16, "one 16-wide MFMA tile holds a head's dims");
-    constexpr int KT = kAttnKeyTiles, QB = kAttnQBlocks;
+    constexpr int KT = kAttnKeyTiles, QB = kAttnQBlocks, KS = kAttnSubTiles;
+    static_assert(KT % KS == 0, "whole sub-blocks");
     __shared__ __align__(16) _Float16 ks[2][kAttnKeys * kKhStride];  // K block [hi, lo][t][dim]
     __shared__ __align__(16) _Float16 vt[2][16 * kVtStride];         // V block transposed [hi, lo][dim][t]
     const int64_t line = blockIdx.x;
@@ -1107,67 +1109,78 @@ __global__ __launch_bounds__(256) void neck_attn16_kernel(const float* __restric
                 if (q0 >= T) continue;  // uniform over the wave
                 // one query block at a time: interleaved, their scores would all be live
                 __builtin_amdgcn_sched_barrier(0);
-                // scores in the MFMA's units (q and k scaled by 2^eq and 2^ek; the softmax's
-                // exponent takes the scaling back, below)
-                f32x4 sc[KT];
+                // the block's keys in sub-blocks of KS tiles (an online softmax over them: fewer
+                // scores live at once); a sub-block wholly past the line's end is skipped
 #pragma unroll
-                for (int t = 0; t < KT; ++t) {
-                    const f16x4 kh = *reinterpret_cast<const f16x4*>(&ks[0][(16 * t + c) * kKhStride + 4 * g]);
-                    const f16x4 kl = *reinterpret_cast<const f16x4*>(&ks[1][(16 * t + c) * kKhStride + 4 * g]);
-                    f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, qh[x], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, ql[x], acc, 0, 0, 0);
-                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh[x], acc, 0, 0, 0);
-                }
-                // keys past the line's end score -inf (their p is then exactly 0), tested only in
-                // the tiles that reach past it; the block's maximum for query q0 + c: this lane's
-                // keys, then the lane groups
-                float bm = -INFINITY;
+                for (int sb = 0; sb < KT / KS; ++sb) {
+                    if (16 * KS * sb >= rem) break;  // uniform
+                    // scores in the MFMA's units (q and k scaled by 2^eq and 2^ek; the softmax's
+                    // exponent takes the scaling back, below)
+                    f32x4 sc[KS];
 #pragma unroll
-                for (int t = 0; t < KT; ++t) {
-                    if (16 * t + 16 > rem) {  // uniform; the asm keeps it a branch, not selects
-                        asm volatile("");
-#pragma unroll
-                        for (int jj = 0; jj < 4; ++jj) sc[t][jj] = (16 * t + 4 * g + jj < rem) ? sc[t][jj] : -INFINITY;
+                    for (int u = 0; u < KS; ++u) {
+                        const int t = KS * sb + u;
+                        const f16x4 kh = *reinterpret_cast<const f16x4*>(&ks[0][(16 * t + c) * kKhStride + 4 * g]);
+                        const f16x4 kl = *reinterpret_cast<const f16x4*>(&ks[1][(16 * t + c) * kKhStride + 4 * g]);
+                        f32x4 acc =
+                            __builtin_amdgcn_mfma_f32_16x16x16f16(kh, qh[x], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, ql[x], acc, 0, 0, 0);
+                        sc[u] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh[x], acc, 0, 0, 0);
                     }
-                    bm = max3_f32(max3_f32(bm, sc[t][0], sc[t][1]), sc[t][2], sc[t][3]);
-                }
-                bm = max_f32(bm, __shfl_xor(bm, 16, 64));
-                bm = max_f32(bm, __shfl_xor(bm, 32, 64));
-                const float nm = max_f32(mx[x], bm);
-                if (kb > 0) {
-                    // rescale the sums so far (every block of a pass after the first follows one
-                    // that set a finite maximum)
-                    const float corr = __builtin_amdgcn_exp2f((mx[x] - nm) * ec);
-                    oa[x] = oa[x] * corr;  // the sum of p (row 15) with the rest
-                }
-                mx[x] = nm;
-                // p = 2^15 e^{(s - max) 2^-(eq+ek)} = 2^{s ec + eb}: one fma and one exp2 per key.  The
-                // 2^15 (exact; it cancels in sum(p v) / sum(p)) keeps the halves of small
-                // probabilities above fp16's subnormals.
-                const float eb = fmaf(-nm, ec, 15.0f);
-                f32x4 ob = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    // keys past the line's end score -inf (their p is then exactly 0), tested only
+                    // in the tiles that reach past it; the sub-block's maximum for query q0 + c:
+                    // this lane's keys, then the lane groups
+                    float bm = -INFINITY;
 #pragma unroll
-                for (int t = 0; t < KT; ++t) {
-                    f16x4 ph, pl;
+                    for (int u = 0; u < KS; ++u) {
+                        const int t = KS * sb + u;
+                        if (16 * t + 16 > rem) {  // uniform; the asm keeps it a branch, not selects
+                            asm volatile("");
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][jj], ec, eb));
-                        // the halves: p with its low 13 mantissa bits cleared (exact in fp16 for
-                        // p >= 2^-14; below, the conversion rounds it, an error under 2^-25 on
-                        // p's scale of 2^15) and the exact remainder, rounded to fp16
-                        const float hi = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
-                        ph[jj] = (_Float16)hi;
-                        pl[jj] = (_Float16)(p - hi);
+                            for (int jj = 0; jj < 4; ++jj)
+                                sc[u][jj] = (16 * t + 4 * g + jj < rem) ? sc[u][jj] : -INFINITY;
+                        }
+                        bm = max3_f32(max3_f32(bm, sc[u][0], sc[u][1]), sc[u][2], sc[u][3]);
                     }
-                    // O^T += V^T P^T: even and odd key tiles on two accumulators
-                    const f16x4 vh = *reinterpret_cast<const f16x4*>(&vt[0][c * kVtStride + 16 * t + 4 * g]);
-                    const f16x4 vl = *reinterpret_cast<const f16x4*>(&vt[1][c * kVtStride + 16 * t + 4 * g]);
-                    f32x4& acc = (t & 1) ? ob : oa[x];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph, acc, 0, 0, 0);
+                    bm = max_f32(bm, __shfl_xor(bm, 16, 64));
+                    bm = max_f32(bm, __shfl_xor(bm, 32, 64));
+                    const float nm = max_f32(mx[x], bm);
+                    if (kb > 0 || sb > 0) {
+                        // rescale the sums so far (every sub-block after the pass's first follows
+                        // one that set a finite maximum: its first key is inside the line)
+                        const float corr = __builtin_amdgcn_exp2f((mx[x] - nm) * ec);
+                        oa[x] = oa[x] * corr;  // the sum of p (row 15) with the rest
+                    }
+                    mx[x] = nm;
+                    // p = 2^15 e^{(s - max) 2^-(eq+ek)} = 2^{s ec + eb}: one fma and one exp2 per key.
+                    // The 2^15 (exact; it cancels in sum(p v) / sum(p)) keeps the halves of small
+                    // probabilities above fp16's subnormals.
+                    const float eb = fmaf(-nm, ec, 15.0f);
+                    f32x4 ob = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int u = 0; u < KS; ++u) {
+                        const int t = KS * sb + u;
+                        f16x4 ph, pl;
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) {
+                            const float p = __builtin_amdgcn_exp2f(fmaf(sc[u][jj], ec, eb));
+                            // the halves: p with its low 13 mantissa bits cleared (exact in fp16
+                            // for p >= 2^-14; below, the conversion rounds it, an error under
+                            // 2^-25 on p's scale of 2^15) and the exact remainder, rounded to fp16
+                            const float hi = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
+                            ph[jj] = (_Float16)hi;
+                            pl[jj] = (_Float16)(p - hi);
+                        }
+                        // O^T += V^T P^T: even and odd key tiles on two accumulators
+                        const f16x4 vh = *reinterpret_cast<const f16x4*>(&vt[0][c * kVtStride + 16 * t + 4 * g]);
+                        const f16x4 vl = *reinterpret_cast<const f16x4*>(&vt[1][c * kVtStride + 16 * t + 4 * g]);
+                        f32x4& acc = (u & 1) ? ob : oa[x];
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph, acc, 0, 0, 0);
+                    }
+                    oa[x] += ob;
                 }
-                oa[x] += ob;
             }
         }
         // per query: the sums of the four lane groups; lane l writes query q0 + c, dims 4 g + j
