@@ -37,6 +37,16 @@ const FLAGS: &[&str] = &[
     "-packed-fp32-ops",
 ];
 
+// Per-file flags: the tail's kernels keep MFMA results in ordinary vector registers (no
+// accumulator-register copies before their vector work).
+fn file_flags(src: &str) -> &'static [&'static str] {
+    if src == "neck.hip" {
+        &["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+    } else {
+        &[]
+    }
+}
+
 fn run(cmd: &mut Command) {
     let status = cmd.status().unwrap_or_else(|e| panic!("failed to start {:?}: {}", cmd, e));
     if !status.success() {
@@ -58,7 +68,13 @@ fn main() {
             let src = src.to_string();
             thread::spawn(move || {
                 let obj = out.join(format!("{}.o", src));
-                run(Command::new(&hipcc).args(FLAGS).arg("-c").arg(csrc.join(&src)).arg("-o").arg(&obj));
+                run(Command::new(&hipcc)
+                    .args(FLAGS)
+                    .args(file_flags(&src))
+                    .arg("-c")
+                    .arg(csrc.join(&src))
+                    .arg("-o")
+                    .arg(&obj));
                 obj
             })
         })

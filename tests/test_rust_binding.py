@@ -91,10 +91,16 @@ def test_build_script_compiles_every_library_source_for_gfx950_only():
     b = open(os.path.join(CRATE, "build.rs")).read()
     mk = open(os.path.join(ROOT, "rust-ppocrv6_amd", "csrc", "Makefile")).read().replace("\\\n", " ")
     srcs = re.findall(r"(\w+\.(?:hip|cpp))", re.search(r"HIP_SRCS = ([^\n]*)\nCPP_SRCS = ([^\n]*)", mk).group(0))
-    listed = re.findall(r'"(\w+\.(?:hip|cpp))"', b)
+    block = re.search(r"const SOURCES: &\[&str\] = &\[(.*?)\];", b, re.S).group(1)
+    listed = re.findall(r'"(\w+\.(?:hip|cpp))"', block)
     assert sorted(srcs) == sorted(listed)
     assert re.findall(r"--offload-arch=(\w+)", b) == ["gfx950"]
     assert "-packed-fp32-ops" in b
+    # the same per-file flags as the Makefile
+    mk_file = dict(re.findall(r"\$\(OBJDIR\)/(\w+)\.o: FILE_FLAGS = ([^\n]*)", mk))
+    rs_file = {m.group(1).split(".")[0]: " ".join(re.findall(r'"([^"]+)"', m.group(2)))
+               for m in re.finditer(r'if src == "(\w+\.hip)" \{\s*&\[([^\]]*)\]', b)}
+    assert mk_file == rs_file and mk_file
 
 
 def test_reference_side_calls_match_the_declarations():
