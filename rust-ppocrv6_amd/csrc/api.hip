@@ -568,20 +568,18 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t p_best, p_sum, p_idx, row_max, row_inv, guard_header, guard_rows, skip, total;
+    size_t part, row_max, row_inv, guard_header, guard_rows, skip, total;
 };
 // The guard header sits at offset 0 whatever m and nsplit are, so a workspace reused for
 // batches of other sizes finds there the header its previous call left (emptied by that
 // call's merge), never a partial or a list entry of another layout.
 WsLayout ws_layout(int64_t m, int nsplit) {
     WsLayout L;
-    const size_t pm = align_up((size_t)nsplit * (size_t)m * 4);
+    const size_t pm = align_up((size_t)nsplit * (size_t)m * sizeof(Partial));
     const size_t rm = align_up((size_t)m * 4);
     L.guard_header = 0;
-    L.p_best = kAlign;
-    L.p_sum = L.p_best + pm;
-    L.p_idx = L.p_sum + pm;
-    L.row_max = L.p_idx + pm;
+    L.part = kAlign;
+    L.row_max = L.part + pm;
     L.row_inv = L.row_max + rm;
     L.guard_rows = L.row_inv + rm;
     L.skip = L.guard_rows + rm;  // a byte per row block of 128 rows or more
@@ -628,19 +626,15 @@ int run_stats(const ppocr_rh* h, int cfg, const float* d_a, int64_t m, int32_t* 
               int64_t line_len = 0) {
     const int nsplit = nsplit_for(h, m, cfg);
     const WsLayout L = ws_layout(m, nsplit);
-    float* p_best = reinterpret_cast<float*>(ws + L.p_best);
-    float* p_sum = reinterpret_cast<float*>(ws + L.p_sum);
-    int* p_idx = reinterpret_cast<int*>(ws + L.p_idx);
+    Partial* part = reinterpret_cast<Partial*>(ws + L.part);
     if (cfg >= 0) {
         const Guard g = make_guard(h, cfg, L, ws, m);
-        return launch_stats_mfma(cfg, h->geom, rec_of(h, cfg), h->d_rec, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
-                                 p_idx, &g, d_idx, d_maxprob, d_row_max, d_row_inv, ctc, st, line_len);
+        return launch_stats_mfma(cfg, h->geom, rec_of(h, cfg), h->d_rec, d_a, m, h->n, h->k, nsplit, part, &g, d_idx, d_maxprob, d_row_max, d_row_inv, ctc, st, line_len);
     }
-    if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, p_best, p_sum,
-                                 p_idx, st, line_len))
+    if (int e = launch_stats_fma(h->d_q, h->d_w, h->d_scale, h->d_bias, d_a, m, h->n, h->k, nsplit, part, st, line_len))
         return e;
-    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, d_idx, d_maxprob, nullptr, st);
-    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, nullptr, st);
+    if (ctc) return launch_merge_ctc(part, m, nsplit, *ctc, d_idx, d_maxprob, nullptr, st);
+    return launch_merge_stats(part, m, nsplit, d_idx, d_maxprob, d_row_max, d_row_inv, nullptr, st);
 }
 
 // Workspace: caller's, or stream-ordered scratch freed on the same stream.
@@ -1109,7 +1103,7 @@ static int decode_dev_common(const ppocr_rh_t* h, const float* d_a, int64_t m, c
     if (dg.err) return fail(PPOCR_ERR_DEVICE, "RecHeadHip: hipSetDevice failed");
     hipStream_t st = (hipStream_t)stream;
     const CtcOut ctc{d_line_off, lines, 0, d_seq, d_seq_len, d_score};
-    if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
+    if (m == 0) return launch_merge_ctc(nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
     if (noalloc) {
         uint8_t* ws = nullptr;
         if (int e = scratch_of(h->device, st, &ws)) return e;
@@ -1178,7 +1172,7 @@ int ppocr_rh_decode_nct_dev(const ppocr_rh_t* h, const float* d_x, int64_t lines
     DeviceGuard dg(h->device);
     hipStream_t st = (hipStream_t)stream;
     const CtcOut ctc{nullptr, lines, 0, d_seq, d_seq_len, d_score, steps};
-    if (m == 0) return launch_merge_ctc(nullptr, nullptr, nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
+    if (m == 0) return launch_merge_ctc(nullptr, 0, 1, ctc, nullptr, nullptr, nullptr, st);
     const WsLayout L = ws_layout(m, nsplit_for(h, m, cfg));
     Workspace ws;
     if (int e = ws.get(d_workspace, workspace_bytes, L.total, st, "RecHeadHip")) return e;

@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
     const int8_t* __restrict__ q, const float* __restrict__ w, const float* __restrict__ scale,
     const float* __restrict__ bias, const float* __restrict__ a, int64_t m, int n, int k, int cpc,
     float* __restrict__ out, const float* __restrict__ row_max, const float* __restrict__ row_inv,
-    float* __restrict__ p_best, float* __restrict__ p_sum, int* __restrict__ p_idx, int64_t line_len,
+    Partial* __restrict__ part, int64_t line_len,
     const unsigned long long* __restrict__ guard_header, const int* __restrict__ guard_rows, unsigned guard_epoch,
     int guard_cap) {
     __shared__ __align__(16) float As[KC * AST];  // [k][row]
@@ -234,9 +234,7 @@ __global__ __launch_bounds__(256) void head_fma_kernel(
                     s = stat_merge(s, other);
                 }
                 if (tn == 0 && rvalid[r]) {
-                    p_best[(int64_t)chunk * m + rows[r]] = s.best;
-                    p_sum[(int64_t)chunk * m + rows[r]] = s.sum;
-                    p_idx[(int64_t)chunk * m + rows[r]] = s.idx;
+                    part[(int64_t)chunk * m + rows[r]] = Partial{s.best, s.sum, s.idx};
                 }
             }
         }
@@ -257,8 +255,7 @@ int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const
     const int ntiles = (int)((n + BN - 1) / BN);
     dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
     head_fma_kernel<EPI_LOGITS, false><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, BN, out,
-                                                             nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
-                                                             nullptr, 0u, 0);
+                                                             nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0u, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
@@ -271,15 +268,14 @@ int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const 
     const int ntiles = (int)((n + BN - 1) / BN);
     dim3 grid(ntiles, (unsigned)((m + BM - 1) / BM));
     head_fma_kernel<EPI_PROBS, false><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, BN, probs,
-                                                            row_max, row_inv, nullptr, nullptr, nullptr, 0, nullptr,
-                                                            nullptr, 0u, 0);
+                                                            row_max, row_inv, nullptr, 0, nullptr, nullptr, 0u, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
 
 int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
-                     const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
-                     float* p_sum, int* p_idx, hipStream_t st, int64_t line_len) {
+                     const float* a, int64_t m, int64_t n, int64_t k, int nsplit, Partial* part,
+                     hipStream_t st, int64_t line_len) {
     if (int e = check_fma_args(m, n, k)) return e;
     if (line_len < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
     if (nsplit < 1 || nsplit > 1024) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad nsplit");
@@ -288,15 +284,15 @@ int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const 
     const int tpc = (ntiles + nsplit - 1) / nsplit;
     dim3 grid(nsplit, (unsigned)((m + BM - 1) / BM));
     head_fma_kernel<EPI_STATS, false><<<grid, 256, 0, st>>>(q, w, scale, bias, a, m, (int)n, (int)k, tpc * BN,
-                                                            nullptr, nullptr, nullptr, p_best, p_sum, p_idx, line_len,
+                                                            nullptr, nullptr, nullptr, part, line_len,
                                                             nullptr, nullptr, 0u, 0);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
 
 int launch_rescue_fma(int epi, const FmaWeights& fw, const float* a, int64_t m, int64_t n, int64_t k, int nsplit,
-                      int classes_per_chunk, float* out, const float* row_max, const float* row_inv, float* p_best,
-                      float* p_sum, int* p_idx, int64_t line_len, const Guard& guard, hipStream_t st) {
+                      int classes_per_chunk, float* out, const float* row_max, const float* row_inv, Partial* part,
+                      int64_t line_len, const Guard& guard, hipStream_t st) {
     if (int e = check_fma_args(m, n, k)) return e;
     if (line_len < 0) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
     if (m <= 0 || n <= 0) return PPOCR_OK;
@@ -313,7 +309,7 @@ int launch_rescue_fma(int epi, const FmaWeights& fw, const float* a, int64_t m, 
     dim3 grid((unsigned)chunks, slots);
     auto args = [&](auto kern) {
         kern<<<grid, 256, 0, st>>>(fw.q, fw.w, fw.scale, fw.bias, a, m, (int)n, (int)k, cpc, out, row_max, row_inv,
-                                   p_best, p_sum, p_idx, line_len, guard.header, guard.rows, guard.epoch,
+                                   part, line_len, guard.header, guard.rows, guard.epoch,
                                    guard.capacity);
     };
     if (epi == EPI_LOGITS) args(head_fma_kernel<EPI_LOGITS, true>);

@@ -329,7 +329,7 @@ static int launch_rows(int cfg, int epi, const TileGeom& tg, const uint8_t* rec,
     if (!guarded) return PPOCR_OK;
     if (rcfg == kRescueFma)
         return launch_rescue_fma(epi == 0 ? EPI_LOGITS : EPI_PROBS, guard->fma, a, m, n, k, 0, 0, out, row_max, row_inv,
-                                 nullptr, nullptr, nullptr, 0, *guard, st);
+                                 nullptr, 0, *guard, st);
     // rescue: the flagged rows again, three bf16 activation terms, every column
     const int slots = (int)std::min<int64_t>(mblocks, kRescueSlots);
     const int rgrid = grid_blocks(slots, nsplit, false);
@@ -361,7 +361,7 @@ int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
 }
 
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a,
-                      int64_t m, int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
+                      int64_t m, int64_t n, int64_t k, int nsplit, Partial* part,
                       const Guard* guard, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
                       const CtcOut* ctc, hipStream_t st, int64_t line_len) {
     if (line_len < 0 || line_len > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
@@ -391,9 +391,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
                   nsplit,
                   tpc,
                   (int)mblocks,
-                  p_best,
-                  p_sum,
-                  p_idx,
+                  part,
                   guarded ? stats_limit_of(cfg, *guard) : GuardLimits{0.0f, 0.0f, 0.0f},
                   guarded ? guard->header : nullptr,
                   guarded ? guard->rows : nullptr,
@@ -415,7 +413,7 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
     if (int e = call_stats_main(cfg, tg.G, x, mb, noref, (unsigned)grid, st)) return e;
     if (guarded && rcfg == kRescueFma) {
         if (int e = launch_rescue_fma(EPI_STATS, guard->fma, a, m, n, k, nsplit, tpc * 32, nullptr, nullptr, nullptr,
-                                      p_best, p_sum, p_idx, line_len, *guard, st))
+                                      part, line_len, *guard, st))
             return e;
     } else if (guarded) {
         // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
@@ -429,8 +427,8 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
         if (int e = call_stats_gather(rcfg, tg.G, x, (unsigned)rgrid, st)) return e;
     }
     const Guard* reset = guarded ? guard : nullptr;
-    if (ctc) return launch_merge_ctc(p_best, p_sum, p_idx, m, nsplit, *ctc, idx, maxprob, reset, st);
-    return launch_merge_stats(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max, row_inv, reset, st);
+    if (ctc) return launch_merge_ctc(part, m, nsplit, *ctc, idx, maxprob, reset, st);
+    return launch_merge_stats(part, m, nsplit, idx, maxprob, row_max, row_inv, reset, st);
 }
 
 }  // namespace ppocr

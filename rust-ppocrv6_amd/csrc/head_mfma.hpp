@@ -684,15 +684,14 @@ constexpr int main_lds_bytes() {
 template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false, int OCC = 8 / kStatsWaves>
 __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
-    int nsplit, int tiles_per_chunk, int mblocks, float* __restrict__ p_best, float* __restrict__ p_sum,
-    int* __restrict__ p_idx, GuardLimits lim, unsigned long long* __restrict__ guard_header,
+    int nsplit, int tiles_per_chunk, int mblocks, Partial* __restrict__ part, GuardLimits lim, unsigned long long* __restrict__ guard_header,
     int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap, const uint8_t* __restrict__ skip) {
     using GE = Geo<C, G>;
     constexpr int S = GE::S;
     constexpr int RPB = 32 * kStatsWaves * MB;
     constexpr int NT = 64 * kStatsWaves;
     extern __shared__ __align__(16) uint8_t lds[];
-    args_now(a, m, k, vec, rec, tiles, nsplit, tiles_per_chunk, mblocks, p_best, p_sum, p_idx, lim.prec,
+    args_now(a, m, k, vec, rec, tiles, nsplit, tiles_per_chunk, mblocks, part, lim.prec,
              lim.range_amax, lim.range_ss, guard_header, guard_rows, guard_epoch, guard_cap);
 
     int mbi, chunk;
@@ -884,9 +883,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                           __shfl_xor(cls, 32, 64)};
             const RowStat r = stat_merge(mine, other);
             if (h == 0 && valid[b]) {
-                p_best[(int64_t)chunk * m + arow[b]] = r.best;
-                p_sum[(int64_t)chunk * m + arow[b]] = r.sum;
-                p_idx[(int64_t)chunk * m + arow[b]] = r.idx;
+                part[(int64_t)chunk * m + arow[b]] = Partial{r.best, r.sum, r.idx};
             }
         }
     };
@@ -1126,7 +1123,7 @@ constexpr int mb_of() {
 template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false>
 static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
     stats_main_kernel<C, G, MB, GATHER, NOREF, SKIP><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
-        x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.p_best, x.p_sum, x.p_idx, x.lim,
+        x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.part, x.lim,
         x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap, x.skip);
 }
 

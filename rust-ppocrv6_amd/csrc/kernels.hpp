@@ -40,6 +40,16 @@ struct GuardLimits {
     float prec, range_amax, range_ss;
 };
 
+// One row's softmax statistics over one vocabulary chunk, as the statistics passes write
+// them and the merges read them: partials [nsplit][m], one 12-byte record per (chunk, row),
+// so a merge loads a chunk's three values in one instruction.
+struct Partial {
+    float best;  // log2-domain maximum of the chunk's logits
+    float sum;   // sum of exp2 over the chunk (relative to the reference, see the kernels)
+    int idx;     // first class reaching the maximum
+};
+static_assert(sizeof(Partial) == 12, "partial record");
+
 // Arguments of one launch of the statistics kernels and of the writer (head_mfma.hpp).
 struct StatsLaunch {
     const float* a;
@@ -47,9 +57,7 @@ struct StatsLaunch {
     int k, vec;
     const uint8_t* rec;
     int tiles, nsplit, tpc, mblocks;
-    float* p_best;
-    float* p_sum;
-    int* p_idx;
+    Partial* part;
     GuardLimits lim;
     unsigned long long* guard_header;
     int* guard_rows;
@@ -164,7 +172,7 @@ struct CtcOut {
 // line_len > 0: `a` is channels-first, [m / line_len][k][line_len] (the tensor before the
 // neck's transpose); row r is step r % line_len of line r / line_len.
 int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a, int64_t m,
-                      int64_t n, int64_t k, int nsplit, float* p_best, float* p_sum, int* p_idx,
+                      int64_t n, int64_t k, int nsplit, Partial* part,
                       const Guard* guard, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
                       const CtcOut* ctc, hipStream_t st, int64_t line_len = 0);
 int launch_probs_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uint8_t* rec_rescue, const float* a, int64_t m,
@@ -179,8 +187,8 @@ int launch_logits_fma(const int8_t* q, const float* w, const float* scale, const
                       const float* a, int64_t m, int64_t n, int64_t k, float* out, hipStream_t st);
 constexpr int kFmaRowsPerBlock = 128, kFmaCols = 128;  // rows and classes of a workgroup's tile
 int launch_stats_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
-                     const float* a, int64_t m, int64_t n, int64_t k, int nsplit, float* p_best,
-                     float* p_sum, int* p_idx, hipStream_t st, int64_t line_len = 0);
+                     const float* a, int64_t m, int64_t n, int64_t k, int nsplit, Partial* part,
+                     hipStream_t st, int64_t line_len = 0);
 int launch_probs_fma(const int8_t* q, const float* w, const float* scale, const float* bias,
                      const float* a, int64_t m, int64_t n, int64_t k, const float* row_max,
                      const float* row_inv, float* probs, hipStream_t st);
@@ -196,14 +204,13 @@ struct FmaWeights {
 // statistics partials of the MFMA pass's vocabulary chunks (EPI_STATS: nsplit chunks of
 // classes_per_chunk classes), overwriting what that pass wrote for those rows.
 int launch_rescue_fma(int epi, const FmaWeights& fw, const float* a, int64_t m, int64_t n, int64_t k, int nsplit,
-                      int classes_per_chunk, float* out, const float* row_max, const float* row_inv, float* p_best,
-                      float* p_sum, int* p_idx, int64_t line_len, const Guard& guard, hipStream_t st);
+                      int classes_per_chunk, float* out, const float* row_max, const float* row_inv, Partial* part,
+                      int64_t line_len, const Guard& guard, hipStream_t st);
 
 // Merge the per-chunk partials of each row: argmax index, max probability, and (when
 // row_max/row_inv are non-null) the row's log2-domain maximum and 1/sum for a probs pass.
 // With `guard`, the merge also resets the guard header to (epoch, 0) (see Guard).
-int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m,
-                       int nsplit, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
+int launch_merge_stats(const Partial* part, int64_t m, int nsplit, int32_t* idx, float* maxprob, float* row_max, float* row_inv,
                        const Guard* guard, hipStream_t st);
 
 int launch_softmax_rows(float* x, int64_t rows, int64_t cols, int32_t* idx, float* maxprob,
@@ -215,7 +222,7 @@ int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* l
                       hipStream_t st);
 // Merge of the vocabulary-chunk partials and the CTC collapse in one kernel; idx and
 // maxprob (per row) may be null.
-int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
+int launch_merge_ctc(const Partial* part, int64_t m, int nsplit,
                      const CtcOut& ctc, int32_t* idx, float* maxprob, const Guard* guard, hipStream_t st);
 
 }  // namespace ppocr

@@ -181,17 +181,17 @@ struct MergeLoad {
     float bv[kMergeBatch], sv[kMergeBatch];
     int iv[kMergeBatch];
 };
-__device__ __forceinline__ void merge_issue(const float* __restrict__ p_best, const float* __restrict__ p_sum,
-                                            const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
+__device__ __forceinline__ void merge_issue(const Partial* __restrict__ part, int64_t m, int nsplit, int64_t row,
                                             bool valid, int c0, MergeLoad& ld) {
     if (valid) {
 #pragma unroll
         for (int x = 0; x < kMergeBatch; ++x) {
             const int c = c0 + x * kMergeLanes;
             if (c < nsplit) {
-                ld.bv[x] = p_best[(int64_t)c * m + row];
-                ld.sv[x] = p_sum[(int64_t)c * m + row];
-                ld.iv[x] = p_idx[(int64_t)c * m + row];
+                const Partial p = part[(int64_t)c * m + row];
+                ld.bv[x] = p.best;
+                ld.sv[x] = p.sum;
+                ld.iv[x] = p.idx;
             }
         }
     }
@@ -219,24 +219,21 @@ __device__ __forceinline__ RowStat merge_lanes(RowStat s, float* inv_out) {
     *inv_out = S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
     return s;
 }
-__device__ __forceinline__ RowStat merged_row(const float* __restrict__ p_best, const float* __restrict__ p_sum,
-                                              const int* __restrict__ p_idx, int64_t m, int nsplit, int64_t row,
+__device__ __forceinline__ RowStat merged_row(const Partial* __restrict__ part, int64_t m, int nsplit, int64_t row,
                                               bool valid, int g, float* inv_out) {
     RowStat s{-INFINITY, 0.0f, 0.0f, 0};
     if (valid) {
         // chunks g, g + 8, g + 16, ... in order, kMergeBatch of them loaded at a time
         for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
             MergeLoad ld;
-            merge_issue(p_best, p_sum, p_idx, m, nsplit, row, true, c0, ld);
+            merge_issue(part, m, nsplit, row, true, c0, ld);
             merge_batch(s, ld, nsplit, c0);
         }
     }
     return merge_lanes(s, inv_out);
 }
 
-__global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restrict__ p_best,
-                                                          const float* __restrict__ p_sum,
-                                                          const int* __restrict__ p_idx, int64_t m, int nsplit,
+__global__ __launch_bounds__(256) void merge_stats_kernel(const Partial* __restrict__ part, int64_t m, int nsplit,
                                                           int32_t* __restrict__ idx, float* __restrict__ maxprob,
                                                           float* __restrict__ row_max, float* __restrict__ row_inv,
                                                           unsigned long long* __restrict__ guard_header,
@@ -245,7 +242,7 @@ __global__ __launch_bounds__(256) void merge_stats_kernel(const float* __restric
     const int64_t row = (int64_t)blockIdx.x * (256 / kMergeLanes) + threadIdx.x / kMergeLanes;
     const int g = threadIdx.x % kMergeLanes;
     float inv;
-    const RowStat s = merged_row(p_best, p_sum, p_idx, m, nsplit, row, row < m, g, &inv);
+    const RowStat s = merged_row(part, m, nsplit, row, row < m, g, &inv);
     // the guard list of this call is emptied for the next (row 0 exists: m >= 1)
     if (guard_header && row == 0 && g == 0) *guard_header = (unsigned long long)guard_epoch << 32;
     if (row >= m || g != 0) return;
@@ -311,9 +308,7 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
 // the previous index between rounds.  Offsets are clamped into [0, m] (a line with t1 < t0
 // is empty); with no offsets, line i is steps i * line_len .. (i + 1) * line_len - 1.
 constexpr int kCtcRound = 1024 / kMergeLanes;
-__global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict__ p_best,
-                                                         const float* __restrict__ p_sum,
-                                                         const int* __restrict__ p_idx, int64_t m, int nsplit,
+__global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restrict__ part, int64_t m, int nsplit,
                                                          const int64_t* __restrict__ line_off, int64_t lines,
                                                          int32_t blank, int32_t* __restrict__ idx_out,
                                                          float* __restrict__ val_out, int32_t* __restrict__ seq,
@@ -330,7 +325,7 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
     const int64_t guess = min(line * (line_off ? even_len : line_len), m);
     const bool one_batch = nsplit <= kMergeLanes * kMergeBatch;
     MergeLoad spec;
-    if (one_batch) merge_issue(p_best, p_sum, p_idx, m, nsplit, guess + step, guess + step < m, g, spec);
+    if (one_batch) merge_issue(part, m, nsplit, guess + step, guess + step < m, g, spec);
     // both offsets of the line in one wait
     int64_t o0 = line * line_len, o1 = o0 + line_len;
     if (line_off) {
@@ -352,7 +347,7 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const float* __restrict
             if (t < t1) merge_batch(s0, spec, nsplit, g);
             st = merge_lanes(s0, &v);
         } else {
-            st = merged_row(p_best, p_sum, p_idx, m, nsplit, t, t < t1, g, &v);
+            st = merged_row(part, m, nsplit, t, t < t1, g, &v);
         }
         if (g == 0) {
             const int32_t id = t < t1 ? st.idx : blank;
@@ -416,13 +411,13 @@ int launch_argmax_rows(const float* x, int64_t rows, int64_t cols, int32_t* idx,
     return PPOCR_OK;
 }
 
-int launch_merge_stats(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
+int launch_merge_stats(const Partial* part, int64_t m, int nsplit,
                        int32_t* idx, float* maxprob, float* row_max, float* row_inv, const Guard* guard,
                        hipStream_t st) {
     if (m <= 0) return PPOCR_OK;
     const int64_t blocks = (m + 256 / kMergeLanes - 1) / (256 / kMergeLanes);
     if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
-    merge_stats_kernel<<<(unsigned)blocks, 256, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, idx, maxprob, row_max,
+    merge_stats_kernel<<<(unsigned)blocks, 256, 0, st>>>(part, m, nsplit, idx, maxprob, row_max,
                                                          row_inv, guard ? guard->header : nullptr,
                                                          guard ? guard->epoch : 0u);
     PPOCR_HIP(hipGetLastError());
@@ -440,12 +435,12 @@ int launch_ctc_greedy(const int32_t* idx, const float* maxprob, const int64_t* l
     return PPOCR_OK;
 }
 
-int launch_merge_ctc(const float* p_best, const float* p_sum, const int* p_idx, int64_t m, int nsplit,
+int launch_merge_ctc(const Partial* part, int64_t m, int nsplit,
                      const CtcOut& ctc, int32_t* idx, float* maxprob, const Guard* guard, hipStream_t st) {
     if (ctc.lines < 0) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: negative line count");
     if (ctc.lines == 0) return PPOCR_OK;
     if (ctc.lines > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "CtcDecode: too many lines");
-    merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(p_best, p_sum, p_idx, m, nsplit, ctc.line_off, ctc.lines,
+    merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(part, m, nsplit, ctc.line_off, ctc.lines,
                                                        ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score,
                                                        guard ? guard->header : nullptr, guard ? guard->epoch : 0u,
                                                        ctc.line_len, m / ctc.lines);
