@@ -410,8 +410,17 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
         x.skip = guard->skip;
     }
     const int mb = rpb / (32 * kStatsWaves);
+    // one block per wave (small batches) of the two-term modes: the main pass recomputes its
+    // flagged rows itself, in three bf16 terms, and no rescue is launched
+    // (its three-term pass holds about 220 registers, two workgroups per CU: used when the
+    // grid fits on the GPU at that occupancy, a single line and a few lines)
+    const bool fused = guarded && rcfg == CFG_Q3 && (cfg == CFG_Q2 || cfg == CFG_H2) && mb == 1 && !x.skip &&
+                       grid <= 2 * 256;
+    if (fused) x.rec3 = rec_rescue;
     if (int e = call_stats_main(cfg, tg.G, x, mb, noref, (unsigned)grid, st)) return e;
-    if (guarded && rcfg == kRescueFma) {
+    if (fused) {
+        // the list stays empty; the merge below resets its header as after a rescue
+    } else if (guarded && rcfg == kRescueFma) {
         if (int e = launch_rescue_fma(EPI_STATS, guard->fma, a, m, n, k, nsplit, tpc * 32, nullptr, nullptr, nullptr,
                                       part, line_len, *guard, st))
             return e;

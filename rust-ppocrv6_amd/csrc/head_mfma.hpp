@@ -681,13 +681,14 @@ constexpr int main_lds_bytes() {
     return kRing * Geo<C, G>::BUF + kStatsWaves * MB * 16 * 64 * 4;
 }
 
-template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false, int OCC = 8 / kStatsWaves>
+template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false, bool FUSE = false,
+          int OCC = 8 / kStatsWaves>
 __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     const float* __restrict__ a, int64_t m, int k, int vec, const uint8_t* __restrict__ rec, int tiles,
     int nsplit, int tiles_per_chunk, int mblocks, Partial* __restrict__ part, GuardLimits lim, unsigned long long* __restrict__ guard_header,
-    int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap, const uint8_t* __restrict__ skip) {
+    int* __restrict__ guard_rows, unsigned guard_epoch, int guard_cap, const uint8_t* __restrict__ skip,
+    const uint8_t* __restrict__ rec3) {
     using GE = Geo<C, G>;
-    constexpr int S = GE::S;
     constexpr int RPB = 32 * kStatsWaves * MB;
     constexpr int NT = 64 * kStatsWaves;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -716,7 +717,14 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
     // this lane's saved values of its best tile: [block][quad][lane] x 4 floats
     f32x4* save = reinterpret_cast<f32x4*>(lds + kRing * GE::BUF) + wave * (MB * 4 * 64) + lane;
 
-    auto row_block = [&](int64_t blk) {
+    // one row block over this chunk's tiles, in arithmetic configuration CC (NR: without the
+    // reference shift); RESCUE: the fused rescue, writing the partials of the rows set in
+    // `keep` only.  Returns (FUSE, first pass) the rows of its blocks the guard flags.
+    auto row_block = [&]<int CC, bool NR, bool RESCUE>(int64_t blk, const uint8_t* recc, unsigned keep) -> unsigned {
+        using GE = Geo<CC, G>;
+        constexpr int S = GE::S;
+        unsigned flagged = 0;
+        (void)keep;
         const int64_t mrow0 = blk * RPB + wave * (32 * MB);
         int64_t arow[MB];
         bool valid[MB];
@@ -727,7 +735,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             if constexpr (GATHER) ring_barrier<0>();  // a previous row block's tiles are no longer read
 #pragma unroll
             for (int x = 0; x < kRing - 1; ++x)
-                stage_direct<GE::REC, NT>(rec + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
+                stage_direct<GE::REC, NT>(recc + (size_t)min(t0 + x, t1 - 1) * GE::REC, lds + x * GE::BUF, tid);
         }
         if constexpr (GATHER) {
 #pragma unroll
@@ -738,23 +746,32 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                 const float* rp = row_ptr(a, arow[b], k, vec, kst);
                 const int kv = opaque_vgpr(k);
                 [&]<int... s>(std::integer_sequence<int, s...>) {
-                    ((bf[b][s] = act_frag<C, G, s>(rp, kst, valid[b], kv, vec > 0, h, amax, ss)), ...);
+                    ((bf[b][s] = act_frag<CC, G, s>(rp, kst, valid[b], kv, vec > 0, h, amax, ss)), ...);
                 }(std::make_integer_sequence<int, S>{});
             }
         } else {
-            float araw[MB][ActPlan<C, G>::NL][8];
+            float araw[MB][ActPlan<CC, G>::NL][8];
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
                 arow[b] = src.row(mrow0 + 32 * b + i, m, valid[b]);
-                act_issue<C, G>(a, valid[b] ? arow[b] : 0, k, vec, h, araw[b]);
+                act_issue<CC, G>(a, valid[b] ? arow[b] : 0, k, vec, h, araw[b]);
             }
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
                 float amax = 0.0f, ss = 0.0f;
-                act_split_all<C, G>(araw[b], h, bf[b], amax, ss);
-                if (guard_header && chunk == 0)
+                act_split_all<CC, G>(araw[b], h, bf[b], amax, ss);
+                if constexpr (FUSE) {
+                    // the guard's test, for this workgroup's own rescue below (no row list)
+                    if constexpr (!RESCUE) {
+                        const float am = fmaxf(amax, __shfl_xor(amax, 32, 64));
+                        const float s2 = ss + __shfl_xor(ss, 32, 64);
+                        if (valid[b] && (am > lim.prec || (am > lim.range_amax && s2 > lim.range_ss)))
+                            flagged |= 1u << b;
+                    }
+                } else if (guard_header && chunk == 0) {
                     guard_append(amax, ss, lim, valid[b], arow[b], h, guard_header, guard_rows, guard_epoch,
                                  guard_cap);
+                }
             }
         }
 
@@ -777,9 +794,9 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             for (int b = 0; b < MB; ++b) acc_a[b] = f32x16{};
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const u16x8 wf = weight_frag<C, G>(lds, s, lb, i * 16, h);
+                const u16x8 wf = weight_frag<CC, G>(lds, s, lb, i * 16, h);
 #pragma unroll
-                for (int b = 0; b < MB; ++b) acc_a[b] = mfma16<CfgT<C>::f16>(wf, bf[b][s], acc_a[b]);
+                for (int b = 0; b < MB; ++b) acc_a[b] = mfma16<CfgT<CC>::f16>(wf, bf[b][s], acc_a[b]);
             }
             // One tile: start loading tile j+3, the MFMAs of tile j+1 into accM interleaved
             // with the epilogue of tile j on accE, the saves of a raised maximum, the rare
@@ -788,7 +805,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             // keeps the body branch-free.
             auto step = [&]<int R>(int j, f32x16 (&accE)[MB], f32x16 (&accM)[MB]) {
                 constexpr unsigned rel = (unsigned)R;  // (j - t0) % kRing
-                stage_direct<GE::REC, NT>(rec + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
+                stage_direct<GE::REC, NT>(recc + (size_t)min(j + kRing - 1, t1 - 1) * GE::REC,
                                       lds + ((rel + kRing - 1) & (kRing - 1)) * GE::BUF, tid);
                 const uint8_t* bufn = lds + ((rel + 1) & (kRing - 1)) * GE::BUF;
                 const float* ep = reinterpret_cast<const float*>(lds + (rel & (kRing - 1)) * GE::BUF + GE::FRAG);
@@ -805,27 +822,27 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
                 // weight fragments are read kPrefetch MFMA steps ahead of their use, so a wave
                 // never waits on LDS with epilogue work queued behind the wait
                 u16x8 wq[kPrefetch];
-                frag_prefetch_first<C, G, kPrefetch>(wq, bufn, lb, i * 16, h);
+                frag_prefetch_first<CC, G, kPrefetch>(wq, bufn, lb, i * 16, h);
                 // each MFMA step: the MFMA of block 0, half of the step's epilogue work, the
                 // MFMAs of the other blocks and the fragment prefetch, the other half; so a
                 // wave always has vector work to issue while its MFMAs run
                 [&]<int... s>(std::integer_sequence<int, s...>) {
                     ([&] {
-                        const u16x8& wf = frag_of<C, G, kPrefetch, s>(wq);
-                        accM[0] = mfma16<CfgT<C>::f16>(wf, bf[0][s], accM[0]);
+                        const u16x8& wf = frag_of<CC, G, kPrefetch, s>(wq);
+                        accM[0] = mfma16<CfgT<CC>::f16>(wf, bf[0][s], accM[0]);
                         __builtin_amdgcn_sched_barrier(0);
-                        epi_pieces_of_half<2 * S, 2 * s, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
+                        epi_pieces_of_half<2 * S, 2 * s, MB, NR>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
                         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                         for (int b = 1; b < MB; ++b)
-                            accM[b] = mfma16<CfgT<C>::f16>(wf, bf[b][s], accM[b]);
-                        frag_prefetch_after<C, G, kPrefetch, s>(wq, bufn, lb, i * 16, h);
+                            accM[b] = mfma16<CfgT<CC>::f16>(wf, bf[b][s], accM[b]);
+                        frag_prefetch_after<CC, G, kPrefetch, s>(wq, bufn, lb, i * 16, h);
                         __builtin_amdgcn_sched_barrier(0);
-                        epi_pieces_of_half<2 * S, 2 * s + 1, MB, NOREF>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
+                        epi_pieces_of_half<2 * S, 2 * s + 1, MB, NR>(accE, ep, h, j, cs, cb, ref, best, bt, save, st);
                         __builtin_amdgcn_sched_barrier(0);
                     }(), ...);
                 }(std::make_integer_sequence<int, S>{});
-                if (!NOREF && __any(st.need)) {
+                if (!NR && __any(st.need)) {
 #pragma unroll
                     for (int b = 0; b < MB; ++b) {
                         if (best[b] != -INFINITY && __builtin_fabsf(best[b] - ref[b]) > 64.0f) {
@@ -882,16 +899,32 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
             RowStat other{__shfl_xor(best[b], 32, 64), __shfl_xor(sum[b], 32, 64), __shfl_xor(ref[b], 32, 64),
                           __shfl_xor(cls, 32, 64)};
             const RowStat r = stat_merge(mine, other);
-            if (h == 0 && valid[b]) {
+            if (h == 0 && valid[b] && (!RESCUE || ((keep >> b) & 1u))) {
                 part[(int64_t)chunk * m + arow[b]] = Partial{r.best, r.sum, r.idx};
             }
         }
+        return flagged;
     };
     if constexpr (GATHER) {
-        for (int64_t blk = mbi; blk < blk_end; blk += mblocks) row_block(blk);
+        for (int64_t blk = mbi; blk < blk_end; blk += mblocks)
+            row_block.template operator()<C, NOREF, false>(blk, rec, 0u);
+    } else if constexpr (FUSE) {
+        // small batches: the rows the guard flags are recomputed here, by the workgroups that
+        // hold them, with three bf16 terms (the rescue configuration's records, rec3), instead
+        // of by a rescue launch; every wave has left the first pass's ring at the barrier
+        static_assert(MB == 1 && Geo<CFG_Q3, G>::BUF == GE::BUF, "the fused rescue shares the ring");
+        (void)blk_end;
+        const unsigned fl = row_block.template operator()<C, NOREF, false>(mbi, rec, 0u);
+        if (__syncthreads_or(fl != 0u)) {
+            // the first pass's last (clamped) tile loads may still be landing in the ring:
+            // every wave drains its own before any restages a slot
+            ring_barrier<0>();
+            row_block.template operator()<CFG_Q3, false, true>(mbi, rec3, fl);
+        }
     } else {
         (void)blk_end;
-        row_block(mbi);
+        (void)rec3;
+        row_block.template operator()<C, NOREF, false>(mbi, rec, 0u);
     }
 }
 
@@ -1120,11 +1153,11 @@ template <int C>
 constexpr int mb_of() {
     return (C == CFG_Q1 || C == CFG_Q2 || C == CFG_F1 || C == CFG_H2) ? 2 : 1;
 }
-template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false>
+template <int C, int G, int MB, bool GATHER, bool NOREF, bool SKIP = false, bool FUSE = false>
 static void stats_go(const StatsLaunch& x, unsigned grid, hipStream_t st) {
-    stats_main_kernel<C, G, MB, GATHER, NOREF, SKIP><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
+    stats_main_kernel<C, G, MB, GATHER, NOREF, SKIP, FUSE><<<grid, 64 * kStatsWaves, main_lds_bytes<C, G, MB>(), st>>>(
         x.a, x.m, x.k, x.vec, x.rec, x.tiles, x.nsplit, x.tpc, x.mblocks, x.part, x.lim,
-        x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap, x.skip);
+        x.guard_header, x.guard_rows, x.guard_epoch, x.guard_cap, x.skip, x.rec3);
 }
 
 // Main statistics pass.  The two-term modes run mb = 1 (small batches) or 2 blocks per
@@ -1137,6 +1170,9 @@ int stats_main_cfg(const StatsLaunch& x, int mb, bool noref, unsigned grid, hipS
             if (x.skip) {
                 if (noref) stats_go<C, G, 1, false, true, true>(x, grid, st);
                 else stats_go<C, G, 1, false, false, true>(x, grid, st);
+            } else if (x.rec3) {
+                if (noref) stats_go<C, G, 1, false, true, false, true>(x, grid, st);
+                else stats_go<C, G, 1, false, false, false, true>(x, grid, st);
             } else {
                 if (noref) stats_go<C, G, 1, false, true>(x, grid, st);
                 else stats_go<C, G, 1, false, false>(x, grid, st);
@@ -1152,8 +1188,13 @@ int stats_main_cfg(const StatsLaunch& x, int mb, bool noref, unsigned grid, hipS
         }
     } else if constexpr (C == CFG_H2) {
         if (mb == 1) {
-            if (noref) stats_go<C, G, 1, false, true>(x, grid, st);
-            else stats_go<C, G, 1, false, false>(x, grid, st);
+            if (x.rec3) {
+                if (noref) stats_go<C, G, 1, false, true, false, true>(x, grid, st);
+                else stats_go<C, G, 1, false, false, false, true>(x, grid, st);
+            } else {
+                if (noref) stats_go<C, G, 1, false, true>(x, grid, st);
+                else stats_go<C, G, 1, false, false>(x, grid, st);
+            }
         } else {
             if (noref) stats_go<C, G, 2, false, true>(x, grid, st);
             else stats_go<C, G, 2, false, false>(x, grid, st);

@@ -66,6 +66,10 @@ struct StatsLaunch {
     // per row block of the main pass: 1 when the guard surely sends all of its rows to the
     // rescue (guard_scan_kernel); null: no block is skipped
     const uint8_t* skip = nullptr;
+    // small batches of the two-term modes: the three-term records the main pass's own
+    // workgroups recompute their flagged rows with (no rescue launch, no row list); null: the
+    // rescue is a pass of its own
+    const uint8_t* rec3 = nullptr;
 };
 struct RowsLaunch {
     const float* a;

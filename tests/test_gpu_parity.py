@@ -449,6 +449,45 @@ def test_skipped_row_blocks_beside_computed_ones(orc, rh, m):
     assert_close_rel(probs[sample], ref["probs"], "skipped blocks probs", row_scale=rel_scale(lg))
 
 
+@pytest.mark.parametrize("mode", [2, 4], ids=["bf16x2", "f16x2"])
+def test_small_batch_rescue_inside_the_main_pass(orc, rh, mode):
+    """Small batches of the two-term modes recompute their guarded rows inside the main
+    pass (each workgroup its chunk of its rows, three bf16 terms) instead of in a rescue
+    launch.  600 rows (five 128-row blocks): rows x30 and x300 in blocks 1 and 3 only, so
+    blocks with and without guarded rows meet in one call; argmax, maximum probability,
+    sequences and probabilities against the oracle, and the statistics pass's maxima
+    against the probabilities pass's (each pass rescues the same rows)."""
+    from ppocr_rechead import workloads as wl
+    w_t, bias = wl.weights()
+    q, s = orc.pack_int8(w_t)
+    rng = np.random.default_rng(77)
+    m = 600
+    a = rng.standard_normal((m, 120)).astype(np.float32)
+    big = np.concatenate([128 + rng.choice(128, 5, replace=False), 384 + rng.choice(128, 5, replace=False)])
+    a[big[:5]] *= np.float32(30.0)
+    a[big[5:]] *= np.float32(300.0)
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    guarded = head.guarded_rows(a, mode)
+    print(f"mode {mode}: {int(guarded.sum())} of {m} rows guarded", flush=True)
+    assert guarded[big[5:]].all() and not guarded[np.setdiff1d(np.arange(m), big)].any()
+    off = split_lines(m, 120)
+    got = head.decode(a, off, mode)
+    idx2, mp2 = head.argmax(a, mode)
+    probs = head.probs(a, mode)
+    head.close()
+    assert np.array_equal(got["idx"], idx2) and np.array_equal(got["maxprob"].view(np.uint32), mp2.view(np.uint32))
+    ref = orc.rechead_lines(a, off, q, s, bias, want_probs=True)
+    lg = f64_logits_q(a, q, s, bias)
+    exempt = check_argmax(got["idx"], ref["idx"], top2_gap(lg), label=f"fused rescue mode {mode}")
+    assert_close_rel(got["maxprob"], ref["maxprob"], "fused rescue maxprob", row_scale=rel_scale(lg))
+    assert_close_rel(probs, ref["probs"], "fused rescue probs", row_scale=rel_scale(lg))
+    np.testing.assert_allclose(probs.max(axis=1), got["maxprob"], rtol=1e-6, atol=1e-7)
+    for b in range(len(off) - 1):
+        if np.any((exempt >= off[b]) & (exempt < off[b + 1])):
+            continue
+        assert np.array_equal(got["seqs"][b], ref["seqs"][b]), b
+
+
 def test_precision_guard_on_large_activations(orc, rh):
     """BF16X2 recomputes rows whose max|a| * max|w| exceeds the guard with three terms:
     x50 rows against the stress weights (+-5 outliers) stay as accurate as BF16X3."""
