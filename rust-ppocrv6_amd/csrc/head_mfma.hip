@@ -255,6 +255,10 @@ static int rows_nsplit(int64_t mblocks) {
 // rescue costs the launch whatever the grid, and a heavy one (a head with large weight
 // outliers guards many rows) needs the whole GPU.
 constexpr int kRescueSlots = 128;
+// Workgroups of a statistics rescue: one round of the GPU at the three-term pass's two
+// workgroups per CU.  A larger grid walks no more blocks at once (a full list of 18 blocks
+// in 64 chunks takes three rounds either way) and an empty list still dispatches all of it.
+constexpr int kRescueGrid = 2 * 256;
 // Precision limits below it make the two-term bf16 main pass skip the row blocks whose rows
 // all go to the rescue (guard_scan_kernel marks them).
 constexpr float kScanLimit = 4.0f;
@@ -428,7 +432,8 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
         // rescue: same vocabulary chunks, so each flagged row's partials are overwritten
         // (with exact class indices)
         const int rrpb = stats_rows_per_block_mfma(rcfg, m);
-        const int slots = (int)std::min<int64_t>((m + rrpb - 1) / rrpb, kRescueSlots);
+        const int slots = (int)std::min<int64_t>({(m + rrpb - 1) / rrpb, (int64_t)kRescueSlots,
+                                                  (int64_t)std::max(1, kRescueGrid / nsplit)});
         const int rgrid = grid_blocks(slots, nsplit, true);
         x.rec = rec_rescue;
         x.mblocks = slots;
