@@ -13,7 +13,7 @@ bool mfma_supports_groups(int G) { return G == 15 || G == 10; }
 // Grid of row blocks x vocabulary chunks, laid out as map_block<rows_on_one_xcd> reads it
 // (workgroup id mod 8 is the XCD a workgroup lands on).
 static int grid_blocks(int mblocks, int nsplit, bool rows_on_one_xcd) {
-    if (nsplit >= 8) return mblocks * nsplit;
+    if (nsplit >= 8) return mblocks * 8 * ((nsplit + 7) / 8);
     if (rows_on_one_xcd) return ((mblocks + 7) / 8) * nsplit * 8;
     const int r8 = 8 / nsplit;
     return ((mblocks + r8 - 1) / r8) * 8;
@@ -168,26 +168,40 @@ int stats_rows_per_block_mfma(int cfg, int64_t m) { return 32 * kStatsWaves * ma
 // Vocabulary chunks per row block.  The grid runs in rounds of `slots` workgroups (those
 // that fit on the 256 CUs of an MI355X at once), and a workgroup costs a fixed start and
 // finish (its rows' activations, the pipeline fill, the partials) worth about `fixed`
-// tiles of the main loop.  The chunk count from 4 to 64 minimising rounds x (fixed + tiles
-// per chunk) is taken.  From 8 chunks up each XCD keeps its slice of the weight records (the
-// chunks of workgroup id mod 8) in its L2; with 4, an XCD takes all chunks of its row blocks,
-// and its workgroups walk the chunks' tiles in step.  Most kernels run 2 workgroups per CU with
-// a fixed cost of 8 tiles (measured: 30720 rows run 5% faster in 4 chunks of 147 tiles,
-// one round, than in 8 chunks of 74, two rounds).  The two-term modes' one-block-per-wave
-// kernel (small batches: 128-row workgroups, 51 KB of LDS, 148 VGPRs) runs 3 per CU, fixed
+// tiles of the main loop.  The chunk count minimising rounds x (fixed + tiles per chunk)
+// is taken, from 4, 8, 16, 32, 64 and, when the grid fits in one round, the multiples of 8
+// between them (2245 rows: 39 chunks of 15 tiles instead of 32 of 19, 37.2 -> 35.9 us per
+// step), without empty chunks.  From 8 chunks up each XCD keeps its slice of the weight
+// records (the chunks of workgroup id mod 8) in its L2; with 4, an XCD takes all chunks of
+// its row blocks, and its workgroups walk the chunks' tiles in step.  Most kernels run 2
+// workgroups per CU with a fixed cost of 8 tiles (measured: 30720 rows run 5% faster in 4
+// chunks of 147 tiles, one round, than in 8 chunks of 74, two rounds).  The two-term modes'
+// one-block-per-wave kernel (small batches: 128-row workgroups, 51 KB of LDS, 154 VGPRs) runs 3 per CU, fixed
 // 10 tiles (measured against 2 per CU and 8 tiles: 2280 rows 43.8 -> 40.5 us per step in 32
 // chunks instead of 16, 4800 rows 63.5 -> 61.6 in 16 instead of 8; 8160 rows keep 8
 // chunks, which the 8-tile estimate would have traded for 32 in three rounds, 84 -> 95 us).
 int stats_per_cu_mfma(int cfg, int64_t m) { return main_blocks(cfg, m) == 1 && (cfg == CFG_Q2 || cfg == CFG_H2) ? 3 : 2; }
 int stats_nsplit(int64_t m, int rows_per_block, int tiles, int per_cu) {
     const int64_t mblocks = (m + rows_per_block - 1) / rows_per_block;
-    const int64_t slots = 256 * (int64_t)per_cu;
+    const int64_t xcd_slots = 32 * (int64_t)per_cu;
     const int64_t fixed = per_cu == 3 ? 10 : 8;
     int best = 4;
     int64_t best_cost = -1;
-    for (int ns = 4; ns <= 64; ns *= 2) {
-        const int64_t rounds = (mblocks * ns + slots - 1) / slots;
-        const int64_t cost = rounds * (fixed + (tiles + ns - 1) / ns);
+    for (int cand = 4; cand <= 64; cand += cand < 8 ? 4 : 8) {
+        // the chunks that hold tiles (no empty one; below 8 a count that divides 8, empty
+        // chunks included), and their tiles as the kernels split them
+        int ns = (tiles + (tiles + cand - 1) / cand - 1) / ((tiles + cand - 1) / cand);
+        if (ns < 8) ns = ns <= 1 ? 1 : ns <= 2 ? 2 : ns <= 4 ? 4 : 8;
+        const int tpc = (tiles + ns - 1) / ns;
+        // workgroups per XCD: a row block's ceil(ns / 8) chunk slots there, or (fewer than 8
+        // chunks) all chunks of every 8th row block
+        const int64_t per_xcd = ns >= 8 ? mblocks * ((ns + 7) / 8) : (mblocks + 7) / 8 * ns;
+        const int64_t rounds = (per_xcd + xcd_slots - 1) / xcd_slots;
+        const int64_t cost = rounds * (fixed + tpc);
+        // counts between the powers of two only in one round, where every CU's share is set
+        // by the grid (over several rounds the estimate favoured them wrongly: 8160 rows 78.4
+        // -> 84.5 us in 24 chunks, two rounds, against 8 in one)
+        if ((cand & (cand - 1)) != 0 && rounds > 1) continue;
         if (best_cost < 0 || cost < best_cost) {
             best = ns;
             best_cost = cost;
@@ -370,8 +384,8 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
                       const CtcOut* ctc, hipStream_t st, int64_t line_len) {
     if (line_len < 0 || line_len > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
     if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
-    if (nsplit != 1 && nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16 && nsplit != 32 && nsplit != 64)
-        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be a power of two <= 64");
+    if (nsplit != 1 && nsplit != 2 && nsplit != 4 && (nsplit < 8 || nsplit > 64))
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be 1, 2, 4 or 8..64");
     if (m <= 0) return PPOCR_OK;
     const int rpb = stats_rows_per_block_mfma(cfg, m);
     const int64_t mblocks = (m + rpb - 1) / rpb;

@@ -192,12 +192,14 @@ __device__ __forceinline__ const u16x8& frag_of(const u16x8 (&wq)[NB]) {
 // one per chunk (the statistics pass: the XCD's workgroups walk the chunks' tiles in step,
 // so each tile is fetched once per XCD and read from L2 by the others; measured on the
 // 30720-row batch in 4 chunks, 0.2250 -> 0.2220 ms per launch); otherwise each XCD takes
-// one chunk (the writer).
+// one chunk (the writer).  From 8 chunks up the count need not be a multiple of 8: every
+// XCD gets ceil(nsplit / 8) chunk slots, and the workgroups whose chunk is nsplit or more
+// (on the last XCDs) have nothing to do.  Below 8 it divides 8.
 template <bool ROWS_ON_ONE_XCD>
 __device__ __forceinline__ void map_block(int bid, int nsplit, int* mbi, int* chunk) {
     const int x = bid & 7, slot = bid >> 3;
     if (nsplit >= 8) {
-        const int per = nsplit >> 3;
+        const int per = (nsplit + 7) >> 3;
         *chunk = x * per + slot % per;
         *mbi = slot / per;
     } else if (ROWS_ON_ONE_XCD) {
@@ -697,7 +699,7 @@ __global__ __launch_bounds__(64 * kStatsWaves, OCC) void stats_main_kernel(
 
     int mbi, chunk;
     map_block<true>(blockIdx.x, nsplit, &mbi, &chunk);
-    if (mbi >= mblocks) return;
+    if (mbi >= mblocks || chunk >= nsplit) return;
     // SKIP: a row block whose rows the guard surely sends to the rescue (guard_scan_kernel,
     // which also listed them) is skipped: the rescue pass overwrites all of their partials,
     // in every chunk
