@@ -96,3 +96,52 @@ def test_large_batch_argmax_matches_oracle(orc, rh, mode):
     lg = f64_logits_q(a, q, s, bias)
     check_argmax(idx, ref["idx"], top2_gap(lg), label=f"large batch mode {mode}")
     assert_close_rel(mp, ref["maxprob"], f"large batch maxprob mode {mode}", row_scale=rel_scale(lg))
+
+
+# Ties inside one vocabulary chunk of the small-batch kernel (a single line to 512 rows of
+# the 18710-class head: chunks of 10 tiles): across neighbouring tiles, the first class in
+# the earlier tile or in the later tile's neighbour, two tiles apart, inside one tile, and
+# across two chunks (the merge's choice).
+GROUPS_SETS = [
+    ((40, 10), (0, 24)),           # tiles 1 and 0 of chunk 0
+    ((70, 50), (24, 48)),          # tiles 2 and 1
+    ((72, 20), (48, 72)),          # tiles 2 and 0
+    ((101, 100, 96), (72, 96)),    # tile 3
+    ((1610, 1590), (96, 120)),     # tiles 50 and 49: chunks 5 and 4
+]
+
+
+@pytest.mark.parametrize("m", [120, 480])
+@pytest.mark.parametrize("mode", [2, 4])
+def test_exact_ties_across_tiles_of_a_chunk(orc, rh, mode, m):
+    from ppocr_rechead import workloads as wl
+    w, bias = wl.weights()
+    w, bias = w.copy(), bias.copy()
+    for classes, (k0, k1) in GROUPS_SETS:
+        row = np.zeros(K, np.float32)
+        row[k0:k1] = 0.5
+        for c in classes:
+            w[c] = row
+            bias[c] = 0.0
+    q, s = orc.pack_int8(w)
+    rng = np.random.default_rng(8)
+    a = (rng.standard_normal((m, K)) * 0.3).astype(np.float32)
+    group = np.arange(m) % len(GROUPS_SETS)
+    for g, (_, (k0, k1)) in enumerate(GROUPS_SETS):
+        a[group == g, k0:k1] += 2.0
+    expect = np.array([min(GROUPS_SETS[g][0]) for g in group], np.int32)
+    print(f"ties across tiles of a chunk: mode {mode}, {m} rows", flush=True)
+    head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
+    try:
+        idx, mp = head.argmax(a, mode)
+        bad = np.nonzero(idx != expect)[0]
+        assert bad.size == 0, f"mode {mode}: {bad.size} rows off the first tied class, e.g. rows {bad[:5]} " \
+                              f"got {idx[bad[:5]]} expected {expect[bad[:5]]}"
+        off = split_lines(m, 120)
+        dec = head.decode(a, off, mode)
+        assert np.array_equal(dec["idx"], idx) and np.array_equal(dec["maxprob"], mp)
+    finally:
+        head.close()
+    ref = orc.rechead_lines(a, split_lines(m, 120), q, s, bias)
+    assert np.array_equal(ref["idx"], expect), "the oracle's first occurrence"
+    assert_close_rel(mp, ref["maxprob"], f"tie rows maxprob mode {mode}", row_scale=rel_scale(f64_logits_q(a, q, s, bias)))

@@ -449,21 +449,25 @@ def test_skipped_row_blocks_beside_computed_ones(orc, rh, m):
     assert_close_rel(probs[sample], ref["probs"], "skipped blocks probs", row_scale=rel_scale(lg))
 
 
+@pytest.mark.parametrize("m", [600, 240])
 @pytest.mark.parametrize("mode", [2, 4], ids=["bf16x2", "f16x2"])
-def test_small_batch_rescue_inside_the_main_pass(orc, rh, mode):
+def test_small_batch_rescue_inside_the_main_pass(orc, rh, mode, m):
     """Small batches of the two-term modes recompute their guarded rows inside the main
     pass (each workgroup its chunk of its rows, three bf16 terms) instead of in a rescue
     launch.  600 rows (five 128-row blocks): rows x30 and x300 in blocks 1 and 3 only, so
-    blocks with and without guarded rows meet in one call; argmax, maximum probability,
-    sequences and probabilities against the oracle, and the statistics pass's maxima
-    against the probabilities pass's (each pass rescues the same rows)."""
+    blocks with and without guarded rows meet in one call; 240 rows (two blocks, the
+    second a partial one): x30 rows in block 0, x300 rows in block 1.  Argmax,
+    maximum probability, sequences and probabilities against the oracle, and the statistics
+    pass's maxima against the probabilities pass's (each pass rescues the same rows)."""
     from ppocr_rechead import workloads as wl
     w_t, bias = wl.weights()
     q, s = orc.pack_int8(w_t)
     rng = np.random.default_rng(77)
-    m = 600
     a = rng.standard_normal((m, 120)).astype(np.float32)
-    big = np.concatenate([128 + rng.choice(128, 5, replace=False), 384 + rng.choice(128, 5, replace=False)])
+    if m == 600:
+        big = np.concatenate([128 + rng.choice(128, 5, replace=False), 384 + rng.choice(128, 5, replace=False)])
+    else:
+        big = np.concatenate([rng.choice(128, 5, replace=False), 128 + rng.choice(m - 128, 5, replace=False)])
     a[big[:5]] *= np.float32(30.0)
     a[big[5:]] *= np.float32(300.0)
     head = rh.RecHead(qw=rh.QuantizedWeight(q, s), bias=bias)
