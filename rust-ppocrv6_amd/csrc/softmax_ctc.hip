@@ -206,6 +206,13 @@ __device__ __forceinline__ void merge_batch(RowStat& s, const MergeLoad& ld, int
         }
     }
 }
+// 1 / the row's sum: s.sum is relative to s.best, so the maximum itself contributes
+// exp2(0) = 1 and the sum is at least 1 (rounding of the rescaling could leave it an ulp
+// below).
+__device__ __forceinline__ float merged_inv(const RowStat& s) {
+    const float S = (s.best == -INFINITY) ? 0.0f : fmaxf(s.sum, 1.0f);
+    return S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
+}
 __device__ __forceinline__ RowStat merge_lanes(RowStat s, float* inv_out) {
 #pragma unroll
     for (int off = 1; off < kMergeLanes; off <<= 1) {
@@ -213,11 +220,19 @@ __device__ __forceinline__ RowStat merge_lanes(RowStat s, float* inv_out) {
                         __shfl_xor(s.idx, off, 64)};
         s = stat_merge_norm(s, o);
     }
-    // s.sum is relative to s.best, so the maximum itself contributes exp2(0) = 1 and the
-    // sum is at least 1 (rounding of the rescaling could leave it an ulp below).
-    const float S = (s.best == -INFINITY) ? 0.0f : fmaxf(s.sum, 1.0f);
-    *inv_out = S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
+    *inv_out = merged_inv(s);
     return s;
+}
+// The value merge_lanes leaves in lane 0 of its group, from the eight lanes' statistics
+// held elsewhere (s[g * stride], g = 0..7): the same merges in the same order, so the
+// result is the same bit for bit.
+__device__ __forceinline__ RowStat merge_tree8(const RowStat* s, int stride) {
+    static_assert(kMergeLanes == 8, "a tree of eight");
+    const RowStat m01 = stat_merge_norm(s[0], s[stride]);
+    const RowStat m23 = stat_merge_norm(s[2 * stride], s[3 * stride]);
+    const RowStat m45 = stat_merge_norm(s[4 * stride], s[5 * stride]);
+    const RowStat m67 = stat_merge_norm(s[6 * stride], s[7 * stride]);
+    return stat_merge_norm(stat_merge_norm(m01, m23), stat_merge_norm(m45, m67));
 }
 __device__ __forceinline__ RowStat merged_row(const Partial* __restrict__ part, int64_t m, int nsplit, int64_t row,
                                               bool valid, int g, float* inv_out) {
@@ -302,10 +317,14 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
 }
 
 // The merge of the vocabulary chunks and the CTC collapse in one pass: one workgroup of
-// 1024 threads per text line.  The line is taken kCtcRound steps at a time: each step's row
-// is merged by a group of kMergeLanes lanes into LDS, then wave 0 collapses the round as
-// ctc_greedy_kernel does (ballot, prefix popcount, score summed in step order), carrying
-// the previous index between rounds.  Offsets are clamped into [0, m] (a line with t1 < t0
+// 1024 threads per text line.  The line is taken kCtcRound steps at a time.  Thread
+// (g, step) merges chunks g, g + 8, ... of the round's row `step`, so each load instruction
+// of a wave reads 64 consecutive rows of one chunk (768 contiguous bytes; with the 8 chunks
+// of 8 rows of merge_stats_kernel's lane groups it reads eight 96-byte pieces, about twice
+// the cache lines); the eight statistics of a row meet in LDS and are merged in
+// merge_lanes' order.  Then wave 0 collapses the round as ctc_greedy_kernel does (ballot,
+// prefix popcount, score summed in step order), carrying the previous index between
+// rounds.  Offsets are clamped into [0, m] (a line with t1 < t0
 // is empty); with no offsets, line i is steps i * line_len .. (i + 1) * line_len - 1.
 constexpr int kCtcRound = 1024 / kMergeLanes;
 __global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restrict__ part, int64_t m, int nsplit,
@@ -317,7 +336,8 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restri
                                                          unsigned guard_epoch, int64_t line_len, int64_t even_len) {
     __shared__ int32_t s_id[kCtcRound];
     __shared__ float s_v[kCtcRound];
-    const int tid = threadIdx.x, lane = tid & 63, g = tid % kMergeLanes, step = tid / kMergeLanes;
+    __shared__ RowStat s_st[kMergeLanes * kCtcRound];  // [g][step]
+    const int tid = threadIdx.x, lane = tid & 63, g = tid / kCtcRound, step = tid % kCtcRound;
     const int64_t line = blockIdx.x;
     // The first round's partials are loaded while the line's offsets are: at the start the
     // line would have with equal lines (even_len = m / lines steps each; 0 for line 0), the
@@ -337,19 +357,28 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restri
     int64_t cnt = 0;
     float sum = -0.0f;
     int32_t carry = blank;  // index of the step before the current one
+    // the first round's rows when the line starts where guessed: t0 + step < t1 <= m were
+    // loaded by the speculative issue (merged here, so its registers are free for the loop)
+    const bool first_loaded = one_batch && t0 == guess;
+    RowStat s_first{-INFINITY, 0.0f, 0.0f, 0};
+    if (first_loaded && t0 + step < t1) merge_batch(s_first, spec, nsplit, g);
     for (int64_t base = t0; base < t1; base += kCtcRound) {
         const int64_t t = base + step;
-        float v = 0.0f;
-        RowStat st;
-        if (one_batch && base == guess) {
-            // rows t < t1 <= m were loaded by the speculative issue (guess + step = t < m)
-            RowStat s0{-INFINITY, 0.0f, 0.0f, 0};
-            if (t < t1) merge_batch(s0, spec, nsplit, g);
-            st = merge_lanes(s0, &v);
-        } else {
-            st = merged_row(part, m, nsplit, t, t < t1, g, &v);
+        RowStat s0{-INFINITY, 0.0f, 0.0f, 0};
+        if (first_loaded && base == t0) {
+            s0 = s_first;
+        } else if (t < t1) {
+            for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
+                MergeLoad ld;
+                merge_issue(part, m, nsplit, t, true, c0, ld);
+                merge_batch(s0, ld, nsplit, c0);
+            }
         }
+        s_st[g * kCtcRound + step] = s0;
+        __syncthreads();
         if (g == 0) {
+            const RowStat st = merge_tree8(s_st + step, kCtcRound);
+            const float v = merged_inv(st);
             const int32_t id = t < t1 ? st.idx : blank;
             if (t < t1) {
                 if (idx_out) idx_out[t] = id;
