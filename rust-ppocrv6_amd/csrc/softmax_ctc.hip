@@ -168,12 +168,13 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
     }
 }
 
-// A row's statistics merged over its vocabulary chunks by a group of kMergeLanes
-// consecutive lanes of one wave: lane g of the group takes chunks g, g + kMergeLanes, ...,
-// then the group combines with xor shuffles, so every lane of the group ends with the
-// merged statistic (first-index argmax) and 1 / sum exp2(t - max) (the maximum
-// probability).  Every kernel that merges partials uses this one order, so their results
-// agree bit for bit.
+// A row's statistics merged over its vocabulary chunks: kMergeLanes threads per row,
+// thread g taking chunks g, g + kMergeLanes, ... in order (merge_batch), then the eight
+// results merged pairwise in a fixed tree (merge_tree8), so every lane of every merge kernel
+// that reads the partials produces the same merged statistic (first-index argmax) and
+// 1 / sum exp2(t - max) (the maximum probability), bit for bit.  The threads of one load
+// instruction take consecutive rows of one chunk (whole runs of records, not 8-row
+// pieces of 8 chunks); their statistics meet in LDS.
 constexpr int kMergeLanes = 8;
 constexpr int kMergeBatch = 8;  // partials per lane loaded together (all of them for nsplit <= 64)
 // The partials of one row a lane merges, chunks c0, c0 + 8, ..., loaded before any is used
@@ -213,19 +214,8 @@ __device__ __forceinline__ float merged_inv(const RowStat& s) {
     const float S = (s.best == -INFINITY) ? 0.0f : fmaxf(s.sum, 1.0f);
     return S > 0.0f ? __fdiv_rn(1.0f, S) : 0.0f;
 }
-__device__ __forceinline__ RowStat merge_lanes(RowStat s, float* inv_out) {
-#pragma unroll
-    for (int off = 1; off < kMergeLanes; off <<= 1) {
-        const RowStat o{__shfl_xor(s.best, off, 64), __shfl_xor(s.sum, off, 64), __shfl_xor(s.ref, off, 64),
-                        __shfl_xor(s.idx, off, 64)};
-        s = stat_merge_norm(s, o);
-    }
-    *inv_out = merged_inv(s);
-    return s;
-}
-// The value merge_lanes leaves in lane 0 of its group, from the eight lanes' statistics
-// held elsewhere (s[g * stride], g = 0..7): the same merges in the same order, so the
-// result is the same bit for bit.
+// The eight threads' statistics of a row (s[g * stride], g = 0..7) merged as
+// ((0,1),(2,3)),((4,5),(6,7)), the lower group first in each pair.
 __device__ __forceinline__ RowStat merge_tree8(const RowStat* s, int stride) {
     static_assert(kMergeLanes == 8, "a tree of eight");
     const RowStat m01 = stat_merge_norm(s[0], s[stride]);
@@ -234,33 +224,34 @@ __device__ __forceinline__ RowStat merge_tree8(const RowStat* s, int stride) {
     const RowStat m67 = stat_merge_norm(s[6 * stride], s[7 * stride]);
     return stat_merge_norm(stat_merge_norm(m01, m23), stat_merge_norm(m45, m67));
 }
-__device__ __forceinline__ RowStat merged_row(const Partial* __restrict__ part, int64_t m, int nsplit, int64_t row,
-                                              bool valid, int g, float* inv_out) {
-    RowStat s{-INFINITY, 0.0f, 0.0f, 0};
-    if (valid) {
-        // chunks g, g + 8, g + 16, ... in order, kMergeBatch of them loaded at a time
-        for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
-            MergeLoad ld;
-            merge_issue(part, m, nsplit, row, true, c0, ld);
-            merge_batch(s, ld, nsplit, c0);
-        }
-    }
-    return merge_lanes(s, inv_out);
-}
-
+// Rows per merge_ctc_kernel round (1024 threads) and per merge_stats_kernel workgroup (256
+// threads: four workgroups per 128 rows, so a single line's rows load through four CUs;
+// each load instruction reads two chunks of 32 consecutive rows).
+constexpr int kCtcRound = 1024 / kMergeLanes;
+constexpr int kStatRows = 256 / kMergeLanes;
 __global__ __launch_bounds__(256) void merge_stats_kernel(const Partial* __restrict__ part, int64_t m, int nsplit,
                                                           int32_t* __restrict__ idx, float* __restrict__ maxprob,
                                                           float* __restrict__ row_max, float* __restrict__ row_inv,
                                                           unsigned long long* __restrict__ guard_header,
                                                           unsigned guard_epoch) {
-    // 256 / kMergeLanes rows per workgroup
-    const int64_t row = (int64_t)blockIdx.x * (256 / kMergeLanes) + threadIdx.x / kMergeLanes;
-    const int g = threadIdx.x % kMergeLanes;
-    float inv;
-    const RowStat s = merged_row(part, m, nsplit, row, row < m, g, &inv);
+    __shared__ RowStat s_st[kMergeLanes * kStatRows];  // [g][row of the workgroup]
+    const int tid = threadIdx.x, g = tid / kStatRows, step = tid % kStatRows;
+    const int64_t row = (int64_t)blockIdx.x * kStatRows + step;
+    RowStat s0{-INFINITY, 0.0f, 0.0f, 0};
+    if (row < m) {
+        for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
+            MergeLoad ld;
+            merge_issue(part, m, nsplit, row, true, c0, ld);
+            merge_batch(s0, ld, nsplit, c0);
+        }
+    }
+    s_st[g * kStatRows + step] = s0;
     // the guard list of this call is emptied for the next (row 0 exists: m >= 1)
     if (guard_header && row == 0 && g == 0) *guard_header = (unsigned long long)guard_epoch << 32;
+    __syncthreads();
     if (row >= m || g != 0) return;
+    const RowStat s = merge_tree8(s_st + step, kStatRows);
+    const float inv = merged_inv(s);
     if (idx) idx[row] = s.idx;
     if (maxprob) maxprob[row] = inv;
     if (row_max) row_max[row] = s.best;
@@ -319,14 +310,13 @@ __global__ __launch_bounds__(256) void ctc_greedy_kernel(const int32_t* __restri
 // The merge of the vocabulary chunks and the CTC collapse in one pass: one workgroup of
 // 1024 threads per text line.  The line is taken kCtcRound steps at a time.  Thread
 // (g, step) merges chunks g, g + 8, ... of the round's row `step`, so each load instruction
-// of a wave reads 64 consecutive rows of one chunk (768 contiguous bytes; with the 8 chunks
-// of 8 rows of merge_stats_kernel's lane groups it reads eight 96-byte pieces, about twice
-// the cache lines); the eight statistics of a row meet in LDS and are merged in
-// merge_lanes' order.  Then wave 0 collapses the round as ctc_greedy_kernel does (ballot,
+// of a wave reads 64 consecutive rows of one chunk (768 contiguous bytes; 8 chunks of 8 rows
+// per instruction read eight 96-byte pieces, about twice the cache lines, and took an A4
+// page's step from 32.8 to 34.2 us); the eight statistics of a row meet in LDS and are
+// merged by merge_tree8.  Then wave 0 collapses the round as ctc_greedy_kernel does (ballot,
 // prefix popcount, score summed in step order), carrying the previous index between
 // rounds.  Offsets are clamped into [0, m] (a line with t1 < t0
 // is empty); with no offsets, line i is steps i * line_len .. (i + 1) * line_len - 1.
-constexpr int kCtcRound = 1024 / kMergeLanes;
 __global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restrict__ part, int64_t m, int nsplit,
                                                          const int64_t* __restrict__ line_off, int64_t lines,
                                                          int32_t blank, int32_t* __restrict__ idx_out,
@@ -444,7 +434,7 @@ int launch_merge_stats(const Partial* part, int64_t m, int nsplit,
                        int32_t* idx, float* maxprob, float* row_max, float* row_inv, const Guard* guard,
                        hipStream_t st) {
     if (m <= 0) return PPOCR_OK;
-    const int64_t blocks = (m + 256 / kMergeLanes - 1) / (256 / kMergeLanes);
+    const int64_t blocks = (m + kStatRows - 1) / kStatRows;
     if (blocks > 0x7fffffffLL) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: m too large");
     merge_stats_kernel<<<(unsigned)blocks, 256, 0, st>>>(part, m, nsplit, idx, maxprob, row_max,
                                                          row_inv, guard ? guard->header : nullptr,
