@@ -169,9 +169,9 @@ int stats_rows_per_block_mfma(int cfg, int64_t m) { return 32 * kStatsWaves * ma
 // that fit on the 256 CUs of an MI355X at once), and a workgroup costs a fixed start and
 // finish (its rows' activations, the pipeline fill, the partials) worth about `fixed`
 // tiles of the main loop.  The chunk count minimising rounds x (fixed + tiles per chunk)
-// is taken, from 4, 8, 16, 32, 64 and, when the grid fits in one round, the multiples of 8
-// between them (2245 rows: 39 chunks of 15 tiles instead of 32 of 19, 37.2 -> 35.9 us per
-// step), without empty chunks.  From 8 chunks up each XCD keeps its slice of the weight
+// is taken, from 4, 8, 16, 32, 64, 128 and, when the grid fits in one round, the multiples
+// of 8 between them (2245 rows: 39 chunks of 15 tiles instead of 32 of 19, 37.2 -> 35.9 us
+// per step), without empty chunks; above 64 only for grids of at most a workgroup per CU.  From 8 chunks up each XCD keeps its slice of the weight
 // records (the chunks of workgroup id mod 8) in its L2; with 4, an XCD takes all chunks of
 // its row blocks, and its workgroups walk the chunks' tiles in step.  Most kernels run 2
 // workgroups per CU with a fixed cost of 8 tiles (measured: 30720 rows run 5% faster in 4
@@ -180,6 +180,8 @@ int stats_rows_per_block_mfma(int cfg, int64_t m) { return 32 * kStatsWaves * ma
 // 10 tiles (measured against 2 per CU and 8 tiles: 2280 rows 43.8 -> 40.5 us per step in 32
 // chunks instead of 16, 4800 rows 63.5 -> 61.6 in 16 instead of 8; 8160 rows keep 8
 // chunks, which the 8-tile estimate would have traded for 32 in three rounds, 84 -> 95 us).
+// Most vocabulary chunks of the statistics pass.
+constexpr int kMaxChunks = 128;
 int stats_per_cu_mfma(int cfg, int64_t m) { return main_blocks(cfg, m) == 1 && (cfg == CFG_Q2 || cfg == CFG_H2) ? 3 : 2; }
 int stats_nsplit(int64_t m, int rows_per_block, int tiles, int per_cu) {
     const int64_t mblocks = (m + rows_per_block - 1) / rows_per_block;
@@ -187,7 +189,7 @@ int stats_nsplit(int64_t m, int rows_per_block, int tiles, int per_cu) {
     const int64_t fixed = per_cu == 3 ? 10 : 8;
     int best = 4;
     int64_t best_cost = -1;
-    for (int cand = 4; cand <= 64; cand += cand < 8 ? 4 : 8) {
+    for (int cand = 4; cand <= kMaxChunks; cand += cand < 8 ? 4 : 8) {
         // the chunks that hold tiles (no empty one; below 8 a count that divides 8, empty
         // chunks included), and their tiles as the kernels split them
         int ns = (tiles + (tiles + cand - 1) / cand - 1) / ((tiles + cand - 1) / cand);
@@ -202,6 +204,10 @@ int stats_nsplit(int64_t m, int rows_per_block, int tiles, int per_cu) {
         // by the grid (over several rounds the estimate favoured them wrongly: 8160 rows 78.4
         // -> 84.5 us in 24 chunks, two rounds, against 8 in one)
         if ((cand & (cand - 1)) != 0 && rounds > 1) continue;
+        // more than 64 chunks only for grids of at most one workgroup per CU (a line or two):
+        // the merge then reads its rows' partials in two batches, which the estimate leaves
+        // out (one line: 59 chunks 16.4 us per step, 117 chunks 15.2, 147 chunks 15.7)
+        if (ns > 64 && per_xcd > 32) continue;
         if (best_cost < 0 || cost < best_cost) {
             best = ns;
             best_cost = cost;
@@ -384,8 +390,8 @@ int launch_stats_mfma(int cfg, const TileGeom& tg, const uint8_t* rec, const uin
                       const CtcOut* ctc, hipStream_t st, int64_t line_len) {
     if (line_len < 0 || line_len > INT32_MAX) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: bad line length");
     if (!check_geom(cfg, tg, n, k)) return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: tile geometry mismatch");
-    if (nsplit != 1 && nsplit != 2 && nsplit != 4 && (nsplit < 8 || nsplit > 64))
-        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be 1, 2, 4 or 8..64");
+    if (nsplit != 1 && nsplit != 2 && nsplit != 4 && (nsplit < 8 || nsplit > kMaxChunks))
+        return fail(PPOCR_ERR_INVALID_ARG, "RecHeadHip: nsplit must be 1, 2, 4 or 8..128");
     if (m <= 0) return PPOCR_OK;
     const int rpb = stats_rows_per_block_mfma(cfg, m);
     const int64_t mblocks = (m + rpb - 1) / rpb;
