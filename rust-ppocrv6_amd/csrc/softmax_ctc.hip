@@ -323,19 +323,16 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restri
                                                          float* __restrict__ val_out, int32_t* __restrict__ seq,
                                                          int64_t* __restrict__ seq_len, float* __restrict__ score,
                                                          unsigned long long* __restrict__ guard_header,
-                                                         unsigned guard_epoch, int64_t line_len, int64_t even_len) {
+                                                         unsigned guard_epoch, int64_t line_len) {
     __shared__ int32_t s_id[kCtcRound];
     __shared__ float s_v[kCtcRound];
     __shared__ RowStat s_st[kMergeLanes * kCtcRound];  // [g][step]
     const int tid = threadIdx.x, lane = tid & 63, g = tid / kCtcRound, step = tid % kCtcRound;
     const int64_t line = blockIdx.x;
-    // The first round's partials are loaded while the line's offsets are: at the start the
-    // line would have with equal lines (even_len = m / lines steps each; 0 for line 0), the
-    // usual case.  When the offsets say otherwise the round loads again.
-    const int64_t guess = min(line * (line_off ? even_len : line_len), m);
-    const bool one_batch = nsplit <= kMergeLanes * kMergeBatch;
-    MergeLoad spec;
-    if (one_batch) merge_issue(part, m, nsplit, guess + step, guess + step < m, g, spec);
+    // The partials are loaded once the line's offsets are known.  Loading the first round's
+    // rows at a guessed start meanwhile (the start with equal lines) measured slower even
+    // where the guess held: its loads queue beside the real ones (an A4 page of ragged lines
+    // 34.5 -> 33.9 us per step without it, four lines of 120 steps 17.4 -> 17.2).
     // both offsets of the line in one wait
     int64_t o0 = line * line_len, o1 = o0 + line_len;
     if (line_off) {
@@ -347,17 +344,10 @@ __global__ __launch_bounds__(1024) void merge_ctc_kernel(const Partial* __restri
     int64_t cnt = 0;
     float sum = -0.0f;
     int32_t carry = blank;  // index of the step before the current one
-    // the first round's rows when the line starts where guessed: t0 + step < t1 <= m were
-    // loaded by the speculative issue (merged here, so its registers are free for the loop)
-    const bool first_loaded = one_batch && t0 == guess;
-    RowStat s_first{-INFINITY, 0.0f, 0.0f, 0};
-    if (first_loaded && t0 + step < t1) merge_batch(s_first, spec, nsplit, g);
     for (int64_t base = t0; base < t1; base += kCtcRound) {
         const int64_t t = base + step;
         RowStat s0{-INFINITY, 0.0f, 0.0f, 0};
-        if (first_loaded && base == t0) {
-            s0 = s_first;
-        } else if (t < t1) {
+        if (t < t1) {
             for (int c0 = g; c0 < nsplit; c0 += kMergeLanes * kMergeBatch) {
                 MergeLoad ld;
                 merge_issue(part, m, nsplit, t, true, c0, ld);
@@ -462,7 +452,7 @@ int launch_merge_ctc(const Partial* part, int64_t m, int nsplit,
     merge_ctc_kernel<<<(unsigned)ctc.lines, 1024, 0, st>>>(part, m, nsplit, ctc.line_off, ctc.lines,
                                                        ctc.blank, idx, maxprob, ctc.seq, ctc.seq_len, ctc.score,
                                                        guard ? guard->header : nullptr, guard ? guard->epoch : 0u,
-                                                       ctc.line_len, m / ctc.lines);
+                                                       ctc.line_len);
     PPOCR_HIP(hipGetLastError());
     return PPOCR_OK;
 }
